@@ -1,0 +1,104 @@
+// mlxvs C++ API of the MI355X exact k-NN engine.
+//
+// Mirrors the reference's C++ entry points (mikepapadim/mlxvs 0.16.1,
+// include/mlxvs/mlxvs.h:21-65 brute_force_knn / Metric / Neighbors /
+// KnnOptions, :775-784 hamming_knn) with plain row views in place of
+// mx::array: same names, argument order, Metric values, KnnOptions and
+// std::invalid_argument("[mlxvs::...] ...") errors.  Host views are copied
+// to the GPU; device views are used in place and results stay on the device.
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <vector>
+
+#define MLXVS_API __attribute__((visibility("default")))
+
+namespace mlxvs {
+
+/** How two rows compare (reference include/mlxvs/mlxvs.h:21-29). */
+enum class Metric {
+  /** Dot product, larger is closer. */
+  InnerProduct = 0,
+  /** Squared Euclidean distance, smaller is closer. */
+  L2 = 1,
+  /** Cosine similarity, larger is closer; rows are normalised on the fly. */
+  Cosine = 2,
+};
+
+/** Element type of a row view. */
+enum class Dtype { Float32, Float16, Uint8 };
+
+/** Row-major, contiguous [n, d] rows (d = bytes per row for Uint8). */
+struct Rows {
+  const void* data = nullptr;
+  int64_t n = 0;
+  int32_t d = 0;
+  Dtype dtype = Dtype::Float32;
+};
+
+/** The k nearest rows of each query, nearest first (reference mlxvs.h:31-42). */
+struct Neighbors {
+  /** int32 [nq, k] row ids; -1 where fewer than k rows exist. */
+  std::vector<int32_t> ids;
+  /** float32 [nq, k]: squared L2 ascending (+inf missing), similarity
+   * descending (-inf missing), or Hamming distance ascending (+inf missing). */
+  std::vector<float> distances;
+  int64_t nq = 0;
+  int32_t k = 0;
+};
+
+/** Options of brute_force_knn (reference mlxvs.h:44-51).  tile_rows is kept
+ * for source compatibility: the fused kernels choose their own tiling, and
+ * the result does not depend on it. */
+struct KnnOptions {
+  int tile_rows = 65536;
+};
+
+/**
+ * Exact k nearest neighbours of every query row among the base rows
+ * (float32, or float16 multiplied on the fp16 MFMA units with float32
+ * accumulation).  1 <= k <= 256 when base has rows.  `stream` is a
+ * hipStream_t (nullptr: the null stream).  Replaces reference
+ * include/mlxvs/mlxvs.h:59-65.
+ */
+MLXVS_API Neighbors brute_force_knn(const Rows& base, const Rows& queries, int k,
+                                    Metric metric, const KnnOptions& options = {},
+                                    void* stream = nullptr);
+
+/** brute_force_knn on device views; writes device ids / distances [nq, k]
+ * (distances may be null) and returns once the work is enqueued. */
+MLXVS_API void brute_force_knn_device(const Rows& base, const Rows& queries, int k,
+                                      Metric metric, int32_t* ids, float* distances,
+                                      const KnnOptions& options = {},
+                                      void* stream = nullptr);
+
+/**
+ * Exact Hamming k-NN of bit-packed uint8 rows [n, bytes] for bit-packed
+ * queries [nq, bytes]; 1 <= k <= 256.  Replaces reference
+ * include/mlxvs/mlxvs.h:775-784.
+ */
+MLXVS_API Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k,
+                                void* stream = nullptr);
+MLXVS_API void hamming_knn_device(const Rows& rows, const Rows& queries, int k,
+                                  int32_t* ids, float* distances,
+                                  void* stream = nullptr);
+
+/**
+ * The k-NN graph of rows against themselves, each row's own id dropped:
+ * the single-cluster brute-force route of reference mlxvs::all_neighbors
+ * (src/all_neighbors.cpp:250-263, 56-95).  1 <= k <= 255, n >= 2.
+ */
+MLXVS_API Neighbors knn_self_graph(const Rows& rows, int k, Metric metric,
+                                   void* stream = nullptr);
+MLXVS_API void knn_self_graph_device(const Rows& rows, int k, Metric metric,
+                                     int32_t* ids, float* distances,
+                                     void* stream = nullptr);
+
+/** Frees the per-device workspace kept between calls. */
+MLXVS_API void release_workspace();
+
+/** "0.16.1-mi355x". */
+MLXVS_API const char* version();
+
+}  // namespace mlxvs

@@ -1,0 +1,200 @@
+/*
+ * mlxvs C ABI for the MI355X (gfx950) exact k-nearest-neighbour engine.
+ *
+ * The first three functions and both enums are the drop-in surface of the
+ * reference's C API (include/mlxvs/mlxvs_c.h:24-45, 243-256 and
+ * src/c_api.cpp:190-196 in mikepapadim/mlxvs 0.16.1): same names, argument
+ * order, enum values, status codes and per-thread error string, so a caller
+ * that binds the reference (Java FFM, ctypes, cgo) binds this library
+ * unchanged.  Everything after the marked line is an extension with no
+ * counterpart in the reference's C API; each says which reference function
+ * it exposes.
+ *
+ * Conventions (as the reference):
+ *  - every function returns MLXVS_OK (0) or an mlxvs_status error code, and
+ *    mlxvs_last_error() then describes the failure for the calling thread
+ *    ("" after a success);
+ *  - host arrays are row-major and owned by the caller: inputs are copied in,
+ *    outputs are written into the caller's buffers;
+ *  - ids are int32 [nq, k], -1 where fewer than k rows exist; distances are
+ *    float32 [nq, k], nearest first: squared L2 ascending (+inf when
+ *    missing), inner product / cosine similarity descending (-inf when
+ *    missing), Hamming distance ascending (+inf when missing).
+ *
+ * Device-pointer variants (suffix _device) take pointers to device memory
+ * (hipMalloc'ed on the current HIP device) and a hipStream_t passed as
+ * void* (NULL = the null stream).  They enqueue all work on that stream and
+ * return without waiting, except where the text says that they synchronise.
+ */
+#ifndef MLXVS_C_H
+#define MLXVS_C_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXVS_C_API __attribute__((visibility("default")))
+
+/** C API version, major * 10000 + minor (reference mlxvs_c.h:25). */
+#define MLXVS_C_API_VERSION 100
+
+/** Status codes (reference include/mlxvs/mlxvs_c.h:27-35). */
+typedef enum {
+  MLXVS_OK = 0,
+  /** An argument was out of range (mlxvs_last_error says which). */
+  MLXVS_ERROR_INVALID_ARGUMENT = 1,
+  /** A file could not be read or written (unused by the k-NN functions). */
+  MLXVS_ERROR_IO = 2,
+  /** Anything else: no GPU, out of device memory, a HIP runtime error. */
+  MLXVS_ERROR_INTERNAL = 3,
+} mlxvs_status;
+
+/** How two rows compare (reference include/mlxvs/mlxvs_c.h:37-45). */
+typedef enum {
+  /** Dot product, larger is closer. */
+  MLXVS_INNER_PRODUCT = 0,
+  /** Squared Euclidean distance, smaller is closer. */
+  MLXVS_L2 = 1,
+  /** Cosine similarity, larger is closer; rows are normalised on the fly. */
+  MLXVS_COSINE = 2,
+} mlxvs_metric;
+
+/**
+ * The calling thread's message for its last failed call, "" after a
+ * success.  Replaces reference src/c_api.cpp:190-192.
+ */
+MLXVS_C_API const char* mlxvs_last_error(void);
+
+/** Library version string, "0.16.1-mi355x".  Replaces src/c_api.cpp:194-196. */
+MLXVS_C_API const char* mlxvs_version(void);
+
+/**
+ * Exact k-nearest neighbours of nq queries among n base rows (float32,
+ * row-major, d columns).  1 <= k <= 256 (checked only when n >= 1, as the
+ * reference).  distances may be NULL.  Replaces reference
+ * include/mlxvs/mlxvs_c.h:243-256 / src/c_api.cpp:468-489.
+ */
+MLXVS_C_API int mlxvs_brute_force_knn(
+    const float* base,
+    int64_t n,
+    const float* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances);
+
+/* ---- extensions: no counterpart in the reference's C API ---------------- */
+
+/**
+ * Exact Hamming k-NN of bit-packed rows (uint8 [n, bytes], as
+ * numpy.packbits) for bit-packed queries (uint8 [nq, bytes]); 1 <= k <= 256.
+ * Distances are popcounts of the XOR, as float32, ascending, lowest id first
+ * among equal distances.  Exposes reference mlxvs::hamming_knn
+ * (include/mlxvs/mlxvs.h:775-784, src/ivf.cpp:1343-1403), which the
+ * reference binds to Python only (python/bindings.cpp:681-709).
+ */
+MLXVS_C_API int mlxvs_hamming_knn(
+    const uint8_t* rows,
+    int64_t n,
+    const uint8_t* queries,
+    int64_t nq,
+    int32_t bytes,
+    int32_t k,
+    int32_t* ids,
+    float* distances);
+
+/**
+ * As mlxvs_brute_force_knn, for float16 rows (IEEE binary16 bit patterns,
+ * uint16 [n, d]) multiplied on the fp16 MFMA units with float32
+ * accumulation.  The reference upcasts float16 input to float32
+ * (src/utils.h:28) and computes in float32; products of binary16 values are
+ * exact in float32, so the two differ only in summation order.
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_f16(
+    const uint16_t* base,
+    int64_t n,
+    const uint16_t* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances);
+
+/**
+ * The k-NN graph of rows against themselves with each row's own id dropped:
+ * ids int32 [n, k] and distances float32 [n, k].  rows are float32
+ * (f16 == 0) or binary16 bit patterns (f16 != 0).  1 <= k <= 255, n >= 2.
+ * Exposes the single-cluster brute-force route of reference
+ * mlxvs::all_neighbors (src/all_neighbors.cpp:250-263, 56-95, 265-272).
+ */
+MLXVS_C_API int mlxvs_knn_self_graph(
+    const void* rows,
+    int64_t n,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances);
+
+/**
+ * mlxvs_brute_force_knn on device memory: base [n, d] and queries [nq, d]
+ * float32 (f16 == 0) or binary16 (f16 != 0), outputs ids / distances
+ * [nq, k] in device memory (distances may be NULL).  Enqueued on stream.
+ * Synchronises with stream only when k > 16 (the merge step then checks on
+ * the host whether a query needs the exhaustive select).
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_device(
+    const void* base,
+    int64_t n,
+    const void* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/** mlxvs_hamming_knn on device memory (see mlxvs_brute_force_knn_device). */
+MLXVS_C_API int mlxvs_hamming_knn_device(
+    const uint8_t* rows,
+    int64_t n,
+    const uint8_t* queries,
+    int64_t nq,
+    int32_t bytes,
+    int32_t k,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/** mlxvs_knn_self_graph on device memory (see mlxvs_brute_force_knn_device). */
+MLXVS_C_API int mlxvs_knn_self_graph_device(
+    const void* rows,
+    int64_t n,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/**
+ * Releases the workspace the library keeps on the current device between
+ * calls (it is grown on demand and reused).  Safe to call at any time when
+ * no other call is running on that device.
+ */
+MLXVS_C_API int mlxvs_release_workspace(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXVS_C_H */

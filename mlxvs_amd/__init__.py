@@ -1,0 +1,246 @@
+"""Exact k-nearest-neighbour search on the AMD Instinct MI355X (gfx950).
+
+Drop-in for the brute-force slice of mlxvs (mikepapadim/mlxvs 0.16.1):
+
+    import mlxvs_amd as mlxvs
+    ids, dist = mlxvs.brute_force_knn(base, queries, 10, "l2")
+    ids, dist = mlxvs.hamming_knn(codes, qcodes, 100)
+
+Same names, arguments, metric names / enum values and error types as the
+reference's Python API (python/mlxvs/__init__.py:56-115,
+python/bindings.cpp:37-75, 681-709); results are NumPy arrays instead of
+mlx.core arrays (``numpy.asarray`` of an mlx array gives the same values).
+The work runs in libmlxvs_c.so, a C-ABI library of hand-written HIP kernels;
+importing this package fails when the library has not been built
+(``python -m mlxvs_amd.build``): the first call then raises ImportError, and
+every call raises RuntimeError when no GPU is present.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from pathlib import Path
+
+import numpy as np
+
+__all__ = [
+    "Metric",
+    "all_neighbors",
+    "brute_force_knn",
+    "hamming_knn",
+    "library_path",
+]
+__version__ = "0.16.1"
+
+_LIB_PATH = Path(__file__).resolve().parent / "libmlxvs_c.so"
+
+# mlxvs_status (include/mlxvs/mlxvs_c.h)
+OK, INVALID_ARGUMENT, IO_ERROR, INTERNAL = 0, 1, 2, 3
+
+
+def library_path() -> str:
+    return str(_LIB_PATH)
+
+
+def _load():
+    if not _LIB_PATH.exists():
+        raise ImportError(
+            f"{_LIB_PATH} is missing: build it with `python -m mlxvs_amd.build` "
+            "(the engine has no CPU fallback)")
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    i64, i32, vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+    sig = {
+        "mlxvs_brute_force_knn": [vp, i64, vp, i64, i32, i32, ctypes.c_int, vp, vp],
+        "mlxvs_brute_force_knn_f16": [vp, i64, vp, i64, i32, i32, ctypes.c_int, vp, vp],
+        "mlxvs_hamming_knn": [vp, i64, vp, i64, i32, i32, vp, vp],
+        "mlxvs_knn_self_graph": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp],
+        "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
+        "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
+        "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
+        "mlxvs_release_workspace": [],
+    }
+    for name, args in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.mlxvs_last_error.restype = ctypes.c_char_p
+    lib.mlxvs_last_error.argtypes = []
+    lib.mlxvs_version.restype = ctypes.c_char_p
+    lib.mlxvs_version.argtypes = []
+    return lib
+
+
+_LIB = None
+
+
+def _L():
+    """The loaded library (loaded on first use, so that the pure-Python parts
+    of the package -- synth -- import without it)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = _load()
+    return _LIB
+
+
+def _check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = _L().mlxvs_last_error().decode()
+    if rc == INVALID_ARGUMENT:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+class Metric(enum.IntEnum):
+    """How two rows compare (values of reference include/mlxvs/mlxvs_c.h:38-45)."""
+
+    inner_product = 0
+    l2 = 1
+    cosine = 2
+
+
+def _metric(metric) -> Metric:
+    # reference python/mlxvs/__init__.py:80-87, 102-103
+    if isinstance(metric, str):
+        try:
+            return Metric[metric]
+        except KeyError:
+            names = ", ".join(repr(n) for n in Metric.__members__)
+            raise ValueError(f"unknown Metric {metric!r}; one of {names}") from None
+    return Metric(int(metric))
+
+
+def _rows(x, name: str, op: str) -> np.ndarray:
+    """2-D real rows as a C-contiguous array (reference src/utils.h:18-29)."""
+    a = np.asarray(x)
+    if a.ndim != 2:
+        raise ValueError(f"[{op}] {name} must be 2-D [n, d].")
+    if a.dtype == np.bool_ or np.iscomplexobj(a) or not np.issubdtype(a.dtype, np.number):
+        raise ValueError(f"[{op}] {name} must be real numbers.")
+    return a
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stream=None):
+    """Exact k-nearest neighbours of every query among the base rows.
+
+    Mirrors reference python/bindings.cpp:37-75.  ``base`` [n, d] and
+    ``queries`` [nq, d] take any real dtype and are computed in float32;
+    float16 inputs (both) are multiplied on the fp16 MFMA units with float32
+    accumulation, which forms the same products as float32.  Returns
+    ``(ids int32 [nq, k], distances float32 [nq, k])``, nearest first:
+    squared L2 ascending, otherwise similarity descending; -1 / +-inf where
+    fewer than k rows exist.  ``tile_rows`` is accepted for compatibility
+    (the result does not depend on it); ``stream`` is a hipStream_t handle
+    (int) or None.
+    """
+    op = "mlxvs::brute_force_knn"
+    b = _rows(base, "base", op)
+    q = _rows(queries, "queries", op)
+    if b.shape[1] != q.shape[1]:
+        raise ValueError(f"[{op}] base and queries must have the same number of columns.")
+    m = _metric(metric)
+    k = int(k)
+    nq = q.shape[0]
+    if b.dtype == np.float16 and q.dtype == np.float16:
+        b = np.ascontiguousarray(b)
+        q = np.ascontiguousarray(q)
+        fn = _L().mlxvs_brute_force_knn_f16
+    else:
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        fn = _L().mlxvs_brute_force_knn
+    ids = np.empty((nq, max(k, 0)), dtype=np.int32)
+    dist = np.empty((nq, max(k, 0)), dtype=np.float32)
+    _check(fn(_ptr(b), b.shape[0], _ptr(q), nq, b.shape[1], k, int(m), _ptr(ids), _ptr(dist)))
+    return ids, dist
+
+
+def hamming_knn(rows, queries, k, *, stream=None):
+    """Exact k-NN of bit-packed uint8 rows by Hamming distance.
+
+    Mirrors reference python/bindings.cpp:681-709 (src/ivf.cpp:1343-1403):
+    ``rows`` uint8 [n, bytes] (as numpy.packbits), ``queries`` uint8
+    [nq, bytes], k <= 256.  Returns ``(ids int32, distances float32)``
+    [nq, k], nearest first, lowest id first among equal distances.
+    """
+    op = "mlxvs::hamming_knn"
+    r = np.asarray(rows)
+    q = np.asarray(queries)
+    if r.ndim != 2 or r.dtype != np.uint8 or q.ndim != 2 or q.dtype != np.uint8:
+        raise ValueError(f"[{op}] rows must be bit-packed uint8 [n, bytes].")
+    if r.shape[1] != q.shape[1]:
+        raise ValueError(f"[{op}] queries must have the rows' bytes.")
+    r = np.ascontiguousarray(r)
+    q = np.ascontiguousarray(q)
+    k = int(k)
+    nq = q.shape[0]
+    ids = np.empty((nq, max(k, 0)), dtype=np.int32)
+    dist = np.empty((nq, max(k, 0)), dtype=np.float32)
+    _check(_L().mlxvs_hamming_knn(_ptr(r), r.shape[0], _ptr(q), nq, r.shape[1], k,
+                                  _ptr(ids), _ptr(dist)))
+    return ids, dist
+
+
+def all_neighbors(rows, k, metric=Metric.l2, *, algo="brute_force", n_clusters=1, **kwargs):
+    """The k-NN graph of ``rows`` against themselves, each row's own id dropped.
+
+    The single-cluster brute-force route of reference mlxvs.all_neighbors
+    (python/mlxvs/__init__.py:224-230, src/all_neighbors.cpp:250-263,
+    56-95): ``algo="brute_force"`` with one cluster only.  float16 rows are
+    multiplied on the fp16 MFMA units.  Returns ``(ids int32 [n, k],
+    distances float32 [n, k])``.
+    """
+    op = "mlxvs::all_neighbors"
+    if algo not in ("brute_force",) or n_clusters not in (0, 1):
+        raise ValueError(f"[{op}] only algo='brute_force' with one cluster is supported")
+    x = _rows(rows, "rows", op)
+    m = _metric(metric)
+    if x.dtype == np.float16:
+        x = np.ascontiguousarray(x)
+        f16 = 1
+    else:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        f16 = 0
+    k = int(k)
+    n = x.shape[0]
+    ids = np.empty((n, max(k, 0)), dtype=np.int32)
+    dist = np.empty((n, max(k, 0)), dtype=np.float32)
+    _check(_L().mlxvs_knn_self_graph(_ptr(x), n, x.shape[1], f16, k, int(m), _ptr(ids),
+                                     _ptr(dist)))
+    return ids, dist
+
+
+def brute_force_knn_device(base_ptr, n, queries_ptr, nq, d, k, metric, ids_ptr,
+                           dist_ptr, *, f16=False, stream=None):
+    """mlxvs_brute_force_knn_device on device pointers (ints); enqueues only."""
+    _check(_L().mlxvs_brute_force_knn_device(
+        base_ptr, n, queries_ptr, nq, d, int(bool(f16)), int(k), int(_metric(metric)),
+        ids_ptr, dist_ptr, stream))
+
+
+def hamming_knn_device(rows_ptr, n, queries_ptr, nq, nbytes, k, ids_ptr, dist_ptr, *,
+                       stream=None):
+    """mlxvs_hamming_knn_device on device pointers (ints)."""
+    _check(_L().mlxvs_hamming_knn_device(rows_ptr, n, queries_ptr, nq, nbytes, int(k),
+                                         ids_ptr, dist_ptr, stream))
+
+
+def knn_self_graph_device(rows_ptr, n, d, k, metric, ids_ptr, dist_ptr, *, f16=False,
+                          stream=None):
+    """mlxvs_knn_self_graph_device on device pointers (ints)."""
+    _check(_L().mlxvs_knn_self_graph_device(rows_ptr, n, d, int(bool(f16)), int(k),
+                                            int(_metric(metric)), ids_ptr, dist_ptr, stream))
+
+
+def release_workspace() -> None:
+    _check(_L().mlxvs_release_workspace())
+
+
+def version() -> str:
+    return _L().mlxvs_version().decode()

@@ -1,0 +1,153 @@
+// The C ABI of include/mlxvs/mlxvs_c.h over the C++ API.
+//
+// Error convention of reference src/c_api.cpp:26-47: std::invalid_argument
+// -> MLXVS_ERROR_INVALID_ARGUMENT, any other exception -> MLXVS_ERROR_INTERNAL,
+// message kept per thread and cleared on success.  Host input checks follow
+// reference src/c_api.cpp:84-91 (host_rows) and :468-489 in the same order.
+#include <stdexcept>
+#include <string>
+
+#include "mlxvs/mlxvs.hpp"
+#include "mlxvs/mlxvs_c.h"
+
+namespace {
+
+thread_local std::string last_error;
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    last_error.clear();
+    return MLXVS_OK;
+  } catch (const std::invalid_argument& e) {
+    last_error = e.what();
+    return MLXVS_ERROR_INVALID_ARGUMENT;
+  } catch (const std::exception& e) {
+    last_error = e.what();
+    return MLXVS_ERROR_INTERNAL;
+  } catch (...) {
+    last_error = "unknown error";
+    return MLXVS_ERROR_INTERNAL;
+  }
+}
+
+void require(bool ok, const char* what) {
+  if (!ok) throw std::invalid_argument(std::string("[mlxvs] ") + what);
+}
+
+mlxvs::Rows host_rows(const void* rows, int64_t n, int32_t d, mlxvs::Dtype t) {
+  require(rows != nullptr || n == 0, "rows must not be NULL.");
+  require(n >= 0 && n < (1LL << 31), "the number of rows must be in [0, 2^31).");
+  require(d >= 1, "the dimension must be at least 1.");
+  return mlxvs::Rows{rows, n, d, t};
+}
+
+mlxvs::Metric to_metric(mlxvs_metric m) {
+  switch (m) {
+    case MLXVS_INNER_PRODUCT: return mlxvs::Metric::InnerProduct;
+    case MLXVS_L2: return mlxvs::Metric::L2;
+    case MLXVS_COSINE: return mlxvs::Metric::Cosine;
+  }
+  throw std::invalid_argument("[mlxvs] unknown metric.");
+}
+
+void copy_out(const mlxvs::Neighbors& r, int32_t* ids, float* distances) {
+  const size_t count = (size_t)r.nq * (size_t)r.k;
+  for (size_t i = 0; i < count; ++i) ids[i] = r.ids[i];
+  if (distances)
+    for (size_t i = 0; i < count; ++i) distances[i] = r.distances[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mlxvs_last_error(void) { return last_error.c_str(); }
+
+const char* mlxvs_version(void) { return mlxvs::version(); }
+
+int mlxvs_brute_force_knn(const float* base, int64_t n, const float* queries, int64_t nq,
+                          int32_t d, int32_t k, mlxvs_metric metric, int32_t* ids,
+                          float* distances) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto b = host_rows(base, n, d, mlxvs::Dtype::Float32);
+    auto q = host_rows(queries, nq, d, mlxvs::Dtype::Float32);
+    auto r = mlxvs::brute_force_knn(b, q, k, to_metric(metric));
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_brute_force_knn_f16(const uint16_t* base, int64_t n, const uint16_t* queries,
+                              int64_t nq, int32_t d, int32_t k, mlxvs_metric metric,
+                              int32_t* ids, float* distances) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto b = host_rows(base, n, d, mlxvs::Dtype::Float16);
+    auto q = host_rows(queries, nq, d, mlxvs::Dtype::Float16);
+    auto r = mlxvs::brute_force_knn(b, q, k, to_metric(metric));
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_hamming_knn(const uint8_t* rows, int64_t n, const uint8_t* queries, int64_t nq,
+                      int32_t bytes, int32_t k, int32_t* ids, float* distances) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto b = host_rows(rows, n, bytes, mlxvs::Dtype::Uint8);
+    auto q = host_rows(queries, nq, bytes, mlxvs::Dtype::Uint8);
+    auto r = mlxvs::hamming_knn(b, q, k);
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_knn_self_graph(const void* rows, int64_t n, int32_t d, int32_t f16, int32_t k,
+                         mlxvs_metric metric, int32_t* ids, float* distances) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto x = host_rows(rows, n, d, f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32);
+    auto r = mlxvs::knn_self_graph(x, k, to_metric(metric));
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_brute_force_knn_device(const void* base, int64_t n, const void* queries,
+                                 int64_t nq, int32_t d, int32_t f16, int32_t k,
+                                 mlxvs_metric metric, int32_t* ids, float* distances,
+                                 void* stream) {
+  return guarded([&] {
+    require(ids != nullptr || nq == 0, "ids must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto b = host_rows(base, n, d, t);
+    auto q = host_rows(queries, nq, d, t);
+    mlxvs::brute_force_knn_device(b, q, k, to_metric(metric), ids, distances, {}, stream);
+  });
+}
+
+int mlxvs_hamming_knn_device(const uint8_t* rows, int64_t n, const uint8_t* queries,
+                             int64_t nq, int32_t bytes, int32_t k, int32_t* ids,
+                             float* distances, void* stream) {
+  return guarded([&] {
+    require(ids != nullptr || nq == 0, "ids must not be NULL.");
+    auto b = host_rows(rows, n, bytes, mlxvs::Dtype::Uint8);
+    auto q = host_rows(queries, nq, bytes, mlxvs::Dtype::Uint8);
+    mlxvs::hamming_knn_device(b, q, k, ids, distances, stream);
+  });
+}
+
+int mlxvs_knn_self_graph_device(const void* rows, int64_t n, int32_t d, int32_t f16,
+                                int32_t k, mlxvs_metric metric, int32_t* ids,
+                                float* distances, void* stream) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto x = host_rows(rows, n, d, f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32);
+    mlxvs::knn_self_graph_device(x, k, to_metric(metric), ids, distances, stream);
+  });
+}
+
+int mlxvs_release_workspace(void) {
+  return guarded([&] { mlxvs::release_workspace(); });
+}
+
+}  // extern "C"

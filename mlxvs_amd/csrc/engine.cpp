@@ -1,0 +1,600 @@
+// Host driver of the MI355X exact k-NN engine: validation, per-device
+// workspace, planning of the fused launch, the exhaustive fallback, and the
+// C++ API of include/mlxvs/mlxvs.hpp.
+//
+// Reference control flow replaced (mikepapadim/mlxvs 0.16.1):
+//  * src/knn.cpp:71-142: a host loop over query blocks x base tiles with a
+//    host synchronisation per tile.  Here: one prep launch per input, one
+//    fused launch over (base split x 128-query block), one merge launch; the
+//    host waits only when the merge may have flagged queries (k > T).
+//  * src/ivf.cpp:1343-1403 (hamming_knn): tiles of IVF lists with a
+//    per-tile select and a host argsort merge.  Here: pack, fused popcount
+//    launch, merge.
+//  * src/all_neighbors.cpp:250-263, 56-95 (single-cluster brute force):
+//    k + 1 neighbours, then a device pass dropping the row itself.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "knn_kernels.h"
+#include "mlxvs/mlxvs.hpp"
+
+namespace mlxvs {
+namespace {
+
+using kern::kQueriesPerBlock;
+
+[[noreturn]] void invalid(const char* op, const std::string& msg) {
+  throw std::invalid_argument(std::string("[") + op + "] " + msg);
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    throw std::runtime_error(std::string("[mlxvs] ") + what + ": " +
+                             hipGetErrorString(e));
+  }
+}
+
+int current_device() {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count < 1) {
+    throw std::runtime_error(
+        std::string("[mlxvs] no HIP device available: ") +
+        (e != hipSuccess ? hipGetErrorString(e) : "device count is 0"));
+  }
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  return dev;
+}
+
+// ---- workspace ----------------------------------------------------------------
+//
+// A per-device bump arena.  Every call takes what it needs in order; when a
+// request does not fit, a new chunk is added, and after the call the chunks
+// are folded into one of the combined size, so steady-state calls never
+// allocate.  Work of consecutive calls is ordered through an event, which
+// makes calls on different streams safe to issue back to back.
+class Arena {
+ public:
+  ~Arena() = default;  // device memory is reclaimed at process exit
+
+  void begin(hipStream_t s) {
+    if (done_) check_hip(hipStreamWaitEvent(s, done_, 0), "hipStreamWaitEvent");
+    for (auto& c : chunks_) c.used = 0;
+  }
+
+  template <typename T>
+  T* take(size_t count) {
+    return static_cast<T*>(take_bytes(count * sizeof(T)));
+  }
+
+  void* take_bytes(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes == 0) bytes = 256;
+    for (auto& c : chunks_) {
+      if (c.size - c.used >= bytes) {
+        void* p = c.ptr + c.used;
+        c.used += bytes;
+        return p;
+      }
+    }
+    size_t total = 0;
+    for (auto& c : chunks_) total += c.size;
+    size_t size = std::max(bytes, total);
+    size = std::max<size_t>(size, 64u << 20);
+    char* p = nullptr;
+    check_hip(hipMalloc(&p, size), "hipMalloc (workspace)");
+    chunks_.push_back({p, size, bytes});
+    return p;
+  }
+
+  void end(hipStream_t s) {
+    if (!done_) check_hip(hipEventCreateWithFlags(&done_, hipEventDisableTiming), "hipEventCreate");
+    check_hip(hipEventRecord(done_, s), "hipEventRecord");
+    if (chunks_.size() > 1) {
+      check_hip(hipEventSynchronize(done_), "hipEventSynchronize");
+      size_t total = 0;
+      for (auto& c : chunks_) {
+        total += c.size;
+        hipFree(c.ptr);
+      }
+      chunks_.clear();
+      char* p = nullptr;
+      check_hip(hipMalloc(&p, total), "hipMalloc (workspace)");
+      chunks_.push_back({p, total, 0});
+    }
+  }
+
+  void release() {
+    if (done_) hipEventSynchronize(done_);
+    for (auto& c : chunks_) hipFree(c.ptr);
+    chunks_.clear();
+  }
+
+ private:
+  struct Chunk {
+    char* ptr;
+    size_t size;
+    size_t used;
+  };
+  std::vector<Chunk> chunks_;
+  hipEvent_t done_ = nullptr;
+};
+
+std::mutex g_mutex;
+std::map<int, std::unique_ptr<Arena>> g_arenas;
+
+// Holds the device's arena for the duration of one call.
+class Session {
+ public:
+  explicit Session(hipStream_t s) : lock_(g_mutex), stream_(s) {
+    int dev = current_device();
+    auto& slot = g_arenas[dev];
+    if (!slot) slot = std::make_unique<Arena>();
+    arena_ = slot.get();
+    arena_->begin(s);
+  }
+  ~Session() {
+    try {
+      arena_->end(stream_);
+    } catch (...) {
+    }
+  }
+  Arena& arena() { return *arena_; }
+  hipStream_t stream() const { return stream_; }
+
+ private:
+  std::lock_guard<std::mutex> lock_;
+  hipStream_t stream_;
+  Arena* arena_ = nullptr;
+};
+
+// ---- planning ------------------------------------------------------------------
+
+// Workgroups one fused launch should have: 256 CUs x 2 resident x 4 waves of
+// workgroups, so the last partial wave costs little.
+constexpr int64_t kTargetBlocks = 2048;
+
+int list_len_float(int k) {
+  if (k <= 4) return 4;
+  if (k <= 8) return 8;
+  if (k <= 10) return 10;
+  return 16;
+}
+
+int list_len_hamming(int k) {
+  if (k <= 4) return 4;
+  if (k <= 8) return 8;
+  return 16;
+}
+
+struct SplitPlan {
+  bool ok = false;
+  int nsplit = 0;
+  int64_t rows_per_split = 0;
+};
+
+// Splits of the base for a fused launch with `lanes` segment lists per split
+// and query and lists of length T.  For k > T the merge sees nseg * T
+// candidates per query; at least 4k of them keep the chance that one
+// segment holds more than T of the k best small (such queries are redone
+// exhaustively).  Returns !ok when the merge cannot hold that many.
+SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
+                      int64_t align) {
+  SplitPlan p;
+  if (n <= 0) return p;
+  const int64_t cap = kern::kMaxMergeCandidates / ((int64_t)lanes * T);
+  int64_t want = (kTargetBlocks + nq_blocks - 1) / nq_blocks;
+  const int64_t need = k > T ? (4 * (int64_t)k + lanes * T - 1) / (lanes * T) : 1;
+  want = std::max(want, need);
+  int64_t ns = std::clamp<int64_t>(want, 1, cap);
+  ns = std::min<int64_t>(ns, (n + align - 1) / align);
+  int64_t rps = (n + ns - 1) / ns;
+  rps = (rps + align - 1) / align * align;
+  ns = (n + rps - 1) / rps;
+  if (ns < need) return p;
+  p.ok = true;
+  p.nsplit = (int)ns;
+  p.rows_per_split = rps;
+  return p;
+}
+
+// ---- validation ------------------------------------------------------------------
+
+void check_rows(const Rows& r, const char* op, const char* name) {
+  if (r.data == nullptr && r.n != 0) invalid(op, std::string(name) + " must not be NULL.");
+  if (r.n < 0 || r.n >= (int64_t(1) << 31))
+    invalid(op, std::string("the number of ") + name + " rows must be in [0, 2^31).");
+  if (r.d < 1) invalid(op, std::string(name) + ": the dimension must be at least 1.");
+}
+
+void check_k(int k, int64_t n, const char* op) {
+  if (k < 0) invalid(op, "k must be in [1, 256]");
+  // reference src/knn.cpp:50-54: the range lives in the select step, which
+  // an empty base never reaches
+  if (n >= 1 && (k < 1 || k > kern::kMaxK)) invalid(op, "k must be in [1, 256]");
+}
+
+// ---- float path -------------------------------------------------------------------
+
+struct FloatInputs {
+  const void* base;
+  const void* queries;
+  int64_t n;
+  int64_t nq;
+  int d;
+  bool f16;
+};
+
+// Exhaustive exact k-NN for the queries listed in qsel (device ints), on
+// prepared fp32 rows.
+void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
+                      const float* queries, const float* bnorm, const float* qnorm,
+                      int64_t n, int d, int metric, const int* qsel_dev, int rows,
+                      int k, int32_t* ids, float* dists) {
+  if (rows <= 0) return;
+  const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t(1) << 28) / std::max<int64_t>(n, 1)));
+  float* S = ar.take<float>((size_t)per_block * (size_t)std::max<int64_t>(n, 1));
+  for (int64_t r0 = 0; r0 < rows; r0 += per_block) {
+    const int cnt = (int)std::min<int64_t>(per_block, rows - r0);
+    kern::ScoresArgs sa{base, queries, qsel_dev + r0, bnorm, n, cnt, d, metric, S};
+    check_hip(kern::launch_scores(sa, s), "scores kernel");
+    kern::SelectArgs se{S, n, cnt, k, qsel_dev + r0, metric, qnorm, 0, ids, dists};
+    check_hip(kern::launch_select(se, s), "select kernel");
+  }
+}
+
+void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* ids,
+               float* dists) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int64_t n = in.n, nq = in.nq;
+  const int d = in.d;
+  if (nq == 0 || k == 0) return;
+  if (n == 0) {
+    check_hip(kern::launch_fill(ids, dists, nq * k,
+                                metric == kern::kL2 ? INFINITY : -INFINITY, s),
+              "fill kernel");
+    return;
+  }
+  // Operand preparation.  Cosine: unit rows in fp32 (reference normalises
+  // in float32, src/knn.cpp:30-33, even for float16 input, src/utils.h:28).
+  const bool cosine = metric == kern::kCosine;
+  const bool l2 = metric == kern::kL2;
+  const bool f16_kernel = in.f16 && !cosine;
+  const void* kbase = in.base;
+  const void* kq = in.queries;
+  float* bnorm = nullptr;
+  float* qnorm = nullptr;
+  float* ub = nullptr;
+  float* uq = nullptr;
+  if (cosine) {
+    ub = ar.take<float>((size_t)n * d);
+    uq = ar.take<float>((size_t)nq * d);
+    check_hip(kern::launch_prep({in.base, n, d, in.f16, nullptr, ub, nullptr}, s), "prep");
+    check_hip(kern::launch_prep({in.queries, nq, d, in.f16, nullptr, uq, nullptr}, s), "prep");
+    kbase = ub;
+    kq = uq;
+  } else if (l2) {
+    bnorm = ar.take<float>((size_t)n);
+    qnorm = ar.take<float>((size_t)nq);
+    check_hip(kern::launch_prep({in.base, n, d, in.f16, bnorm, nullptr, nullptr}, s), "prep");
+    check_hip(kern::launch_prep({in.queries, nq, d, in.f16, qnorm, nullptr, nullptr}, s), "prep");
+  }
+
+  const int T = list_len_float(k);
+  const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  SplitPlan plan;
+  if (kern::fused_supported(d, T, f16_kernel) && nq < (int64_t(1) << 31))
+    plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows);
+
+  // fp32 copies for the exhaustive path (only when it may run)
+  auto fp32_rows = [&](const void* x, int64_t rows, float** out) {
+    if (!in.f16 || cosine) {
+      *out = (float*)x;  // already fp32 (cosine: unit rows)
+      return;
+    }
+    *out = ar.take<float>((size_t)rows * d);
+    check_hip(kern::launch_prep({x, rows, d, 1, nullptr, nullptr, *out}, s), "prep");
+  };
+
+  if (!plan.ok) {
+    float *eb, *eq;
+    fp32_rows(kbase, n, &eb);
+    fp32_rows(kq, nq, &eq);
+    std::vector<int> all((size_t)nq);
+    for (int64_t i = 0; i < nq; ++i) all[(size_t)i] = (int)i;
+    int* qsel = ar.take<int>((size_t)nq);
+    check_hip(hipMemcpyAsync(qsel, all.data(), sizeof(int) * nq, hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync");
+    // the host vector must outlive the copy
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    exhaustive_float(ar, s, eb, eq, bnorm, qnorm, n, d, metric, qsel, (int)nq, k, ids, dists);
+    return;
+  }
+
+  const int nseg = 2 * plan.nsplit;
+  uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
+  const int vmul = f16_kernel ? 8 : 4;
+  const bool aligned = ((uintptr_t)kbase % 16 == 0) && ((uintptr_t)kq % 16 == 0);
+  kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, d, cosine ? kern::kInnerProduct : metric,
+                     plan.rows_per_split, plan.nsplit, T, part,
+                     (d % vmul == 0 && aligned) ? 1 : 0};
+  check_hip(f16_kernel ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s),
+            "fused kernel");
+  int* flags = nullptr;
+  if (T < k) flags = ar.take<int>((size_t)nq);
+  kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};
+  check_hip(kern::launch_merge(ma, s), "merge kernel");
+  if (T >= k) return;
+
+  // k > T: queries whose lists may have dropped a member go exhaustive.
+  std::vector<int> hflags((size_t)nq);
+  check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
+            "hipMemcpyAsync");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  std::vector<int> redo;
+  for (int64_t i = 0; i < nq; ++i)
+    if (hflags[(size_t)i]) redo.push_back((int)i);
+  if (redo.empty()) return;
+  float *eb, *eq;
+  fp32_rows(kbase, n, &eb);
+  fp32_rows(kq, nq, &eq);
+  int* qsel = ar.take<int>(redo.size());
+  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
+            "hipMemcpyAsync");
+  exhaustive_float(ar, s, eb, eq, bnorm, qnorm, n, d, metric, qsel, (int)redo.size(), k,
+                   ids, dists);
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// ---- Hamming path --------------------------------------------------------------------
+
+void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
+             int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  if (nq == 0) return;
+  if (n == 0) {
+    check_hip(kern::launch_fill(ids, dists, nq * k, INFINITY, s), "fill kernel");
+    return;
+  }
+  const int W = (nbytes + 3) / 4;
+  const int T = list_len_hamming(k);
+  const int Wp = kern::hamming_padded_words(W);
+  const int64_t qblocks = (nq + kern::kHammingQueriesPerBlock - 1) / kern::kHammingQueriesPerBlock;
+  SplitPlan plan;
+  if (Wp != 0 && kern::hamming_supported(Wp, T)) plan = plan_splits(n, qblocks, k, T, 1, 2);
+  const int wstride = plan.ok ? Wp : W;
+  uint32_t* bw = ar.take<uint32_t>((size_t)n * wstride);
+  uint32_t* qw = ar.take<uint32_t>((size_t)nq * wstride);
+  check_hip(kern::launch_pack({rows, n, nbytes, bw, wstride}, s), "pack kernel");
+  check_hip(kern::launch_pack({queries, nq, nbytes, qw, wstride}, s), "pack kernel");
+
+  std::vector<int> redo;
+  if (plan.ok) {
+    uint64_t* part = ar.take<uint64_t>((size_t)nq * plan.nsplit * T);
+    kern::HammingArgs ha{bw, qw, n, (int)nq, Wp, plan.rows_per_split, plan.nsplit, T, part};
+    check_hip(kern::launch_hamming(ha, s), "hamming kernel");
+    int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
+    kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags};
+    check_hip(kern::launch_merge(ma, s), "merge kernel");
+    if (T >= k) return;
+    std::vector<int> hflags((size_t)nq);
+    check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
+              "hipMemcpyAsync");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    for (int64_t i = 0; i < nq; ++i)
+      if (hflags[(size_t)i]) redo.push_back((int)i);
+    if (redo.empty()) return;
+  } else {
+    redo.resize((size_t)nq);
+    for (int64_t i = 0; i < nq; ++i) redo[(size_t)i] = (int)i;
+  }
+  int* qsel = ar.take<int>(redo.size());
+  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
+            "hipMemcpyAsync");
+  const int64_t rcount = (int64_t)redo.size();
+  const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rcount, (int64_t(1) << 28) / n));
+  float* S = ar.take<float>((size_t)per_block * n);
+  for (int64_t r0 = 0; r0 < rcount; r0 += per_block) {
+    const int cnt = (int)std::min<int64_t>(per_block, rcount - r0);
+    kern::HammingScoresArgs hs{bw, qw, qsel + r0, n, cnt, wstride, S};
+    check_hip(kern::launch_hamming_scores(hs, s), "hamming scores kernel");
+    kern::SelectArgs se{S, n, cnt, k, qsel + r0, kern::kL2, nullptr, 1, ids, dists};
+    check_hip(kern::launch_select(se, s), "select kernel");
+  }
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// ---- host <-> device helpers ----------------------------------------------------
+
+size_t elem_size(Dtype t) {
+  switch (t) {
+    case Dtype::Float32: return 4;
+    case Dtype::Float16: return 2;
+    case Dtype::Uint8: return 1;
+  }
+  return 0;
+}
+
+const void* upload(Arena& ar, hipStream_t s, const Rows& r) {
+  const size_t bytes = (size_t)r.n * r.d * elem_size(r.dtype);
+  if (bytes == 0) return nullptr;
+  void* p = ar.take_bytes(bytes);
+  check_hip(hipMemcpyAsync(p, r.data, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync (inputs)");
+  return p;
+}
+
+Neighbors download(Arena& ar, hipStream_t s, const int32_t* ids, const float* dists,
+                   int64_t nq, int k) {
+  (void)ar;
+  Neighbors out;
+  out.nq = nq;
+  out.k = k;
+  out.ids.resize((size_t)(nq * k));
+  out.distances.resize((size_t)(nq * k));
+  if (nq * k > 0) {
+    check_hip(hipMemcpyAsync(out.ids.data(), ids, sizeof(int32_t) * nq * k,
+                             hipMemcpyDeviceToHost, s), "hipMemcpyAsync (ids)");
+    check_hip(hipMemcpyAsync(out.distances.data(), dists, sizeof(float) * nq * k,
+                             hipMemcpyDeviceToHost, s), "hipMemcpyAsync (distances)");
+  }
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return out;
+}
+
+void float_args(const Rows& base, const Rows& queries, int k, Metric metric,
+                const char* op) {
+  check_rows(base, op, "base");
+  check_rows(queries, op, "queries");
+  if ((int)metric < 0 || (int)metric > 2) invalid(op, "unknown metric.");
+  if (base.dtype == Dtype::Uint8 || queries.dtype == Dtype::Uint8)
+    invalid(op, "rows must be float32 or float16.");
+  if (base.dtype != queries.dtype) invalid(op, "base and queries must have the same dtype.");
+  if (base.d != queries.d)
+    invalid(op, "base and queries must have the same number of columns.");
+  check_k(k, base.n, op);
+}
+
+void hamming_args(const Rows& rows, const Rows& queries, int k, const char* op) {
+  check_rows(rows, op, "rows");
+  check_rows(queries, op, "queries");
+  if (rows.dtype != Dtype::Uint8 || queries.dtype != Dtype::Uint8)
+    invalid(op, "rows must be bit-packed uint8 [n, bytes].");
+  if (rows.d != queries.d) invalid(op, "queries must have the rows' bytes.");
+  // reference src/ivf.cpp:1357-1359: always checked
+  if (k < 1 || k > kern::kMaxK) invalid(op, "k must be in [1, 256].");
+}
+
+void self_args(const Rows& rows, int k, Metric metric, const char* op) {
+  check_rows(rows, op, "rows");
+  if ((int)metric < 0 || (int)metric > 2) invalid(op, "unknown metric.");
+  if (rows.dtype == Dtype::Uint8) invalid(op, "rows must be float32 or float16.");
+  // reference src/all_neighbors.cpp:272-277
+  if (k < 1 || k > 255 || rows.n < 2)
+    invalid(op, "1 <= k <= 255, n >= 2 and d >= 1");
+}
+
+void self_graph(Session& ss, const void* rows, int64_t n, int d, bool f16, int k,
+                int metric, int32_t* ids, float* dists) {
+  Arena& ar = ss.arena();
+  const int kin = (int)std::min<int64_t>(k + 1, n);
+  int32_t* tid = ar.take<int32_t>((size_t)n * kin);
+  float* tds = ar.take<float>((size_t)n * kin);
+  float_knn(ss, {rows, rows, n, n, d, f16}, kin, metric, tid, tds);
+  float* out_d = dists ? dists : ar.take<float>((size_t)n * k);
+  kern::SelfDropArgs sd{tid, tds, n, kin, k, metric, ids, out_d};
+  check_hip(kern::launch_self_drop(sd, ss.stream()), "self drop kernel");
+}
+
+}  // namespace
+
+// ---- public API --------------------------------------------------------------------
+
+Neighbors brute_force_knn(const Rows& base, const Rows& queries, int k, Metric metric,
+                          const KnnOptions& options, void* stream) {
+  const char* op = "mlxvs::brute_force_knn";
+  (void)options;
+  float_args(base, queries, k, metric, op);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int64_t nq = queries.n;
+  const void* db = upload(ar, s, base);
+  const void* dq = upload(ar, s, queries);
+  int32_t* ids = ar.take<int32_t>((size_t)std::max<int64_t>(1, nq * k));
+  float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
+  float_knn(ss, {db, dq, base.n, nq, base.d, base.dtype == Dtype::Float16}, k, (int)metric,
+            ids, dists);
+  return download(ar, s, ids, dists, nq, k);
+}
+
+void brute_force_knn_device(const Rows& base, const Rows& queries, int k, Metric metric,
+                            int32_t* ids, float* distances, const KnnOptions& options,
+                            void* stream) {
+  const char* op = "mlxvs::brute_force_knn";
+  (void)options;
+  float_args(base, queries, k, metric, op);
+  if (ids == nullptr && queries.n * k > 0) invalid(op, "ids must not be NULL.");
+  Session ss((hipStream_t)stream);
+  float* dists = distances;
+  if (dists == nullptr) dists = ss.arena().take<float>((size_t)std::max<int64_t>(1, queries.n * k));
+  float_knn(ss, {base.data, queries.data, base.n, queries.n, base.d,
+                 base.dtype == Dtype::Float16},
+            k, (int)metric, ids, dists);
+}
+
+Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k, void* stream) {
+  const char* op = "mlxvs::hamming_knn";
+  hamming_args(rows, queries, k, op);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int64_t nq = queries.n;
+  const void* db = upload(ar, s, rows);
+  const void* dq = upload(ar, s, queries);
+  int32_t* ids = ar.take<int32_t>((size_t)std::max<int64_t>(1, nq * k));
+  float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
+  hamming(ss, (const uint8_t*)db, rows.n, (const uint8_t*)dq, nq, rows.d, k, ids, dists);
+  return download(ar, s, ids, dists, nq, k);
+}
+
+void hamming_knn_device(const Rows& rows, const Rows& queries, int k, int32_t* ids,
+                        float* distances, void* stream) {
+  const char* op = "mlxvs::hamming_knn";
+  hamming_args(rows, queries, k, op);
+  if (ids == nullptr && queries.n > 0) invalid(op, "ids must not be NULL.");
+  Session ss((hipStream_t)stream);
+  float* dists = distances;
+  if (dists == nullptr) dists = ss.arena().take<float>((size_t)std::max<int64_t>(1, queries.n * k));
+  hamming(ss, (const uint8_t*)rows.data, rows.n, (const uint8_t*)queries.data, queries.n,
+          rows.d, k, ids, dists);
+}
+
+Neighbors knn_self_graph(const Rows& rows, int k, Metric metric, void* stream) {
+  const char* op = "mlxvs::all_neighbors";
+  self_args(rows, k, metric, op);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const void* dr = upload(ar, s, rows);
+  int32_t* ids = ar.take<int32_t>((size_t)rows.n * k);
+  float* dists = ar.take<float>((size_t)rows.n * k);
+  self_graph(ss, dr, rows.n, rows.d, rows.dtype == Dtype::Float16, k, (int)metric, ids,
+             dists);
+  return download(ar, s, ids, dists, rows.n, k);
+}
+
+void knn_self_graph_device(const Rows& rows, int k, Metric metric, int32_t* ids,
+                           float* distances, void* stream) {
+  const char* op = "mlxvs::all_neighbors";
+  self_args(rows, k, metric, op);
+  if (ids == nullptr) invalid(op, "ids must not be NULL.");
+  Session ss((hipStream_t)stream);
+  self_graph(ss, rows.data, rows.n, rows.d, rows.dtype == Dtype::Float16, k, (int)metric,
+             ids, distances);
+}
+
+void release_workspace() {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  int dev = current_device();
+  auto it = g_arenas.find(dev);
+  if (it != g_arenas.end()) {
+    it->second->release();
+    g_arenas.erase(it);
+  }
+}
+
+const char* version() { return "0.16.1-mi355x"; }
+
+}  // namespace mlxvs

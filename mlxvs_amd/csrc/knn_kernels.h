@@ -1,0 +1,174 @@
+// Launch interface between the host driver (engine.cpp) and the gfx950
+// kernels (knn_float.hip, knn_hamming.hip).  Plain structs of device pointers
+// and sizes; every launcher enqueues on the given stream and returns the HIP
+// status of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlxvs::kern {
+
+enum Metric : int { kInnerProduct = 0, kL2 = 1, kCosine = 2 };
+
+// Rows streamed per step of the fused kernels, and queries per workgroup
+// (four wavefronts of 32 query columns each).
+constexpr int kTileRows = 32;
+constexpr int kQueriesPerBlock = 128;
+// Largest padded dimension the register-resident fused kernels take:
+// fp32 2 * 128, fp16 2 * 256.
+constexpr int kMaxFusedDimF32 = 256;
+constexpr int kMaxFusedDimF16 = 512;
+// Largest candidate count one merge workgroup sorts in LDS.
+constexpr int kMaxMergeCandidates = 4096;
+// Largest k of the exact selection.
+constexpr int kMaxK = 256;
+
+// Row preparation: squared norms (L2), unit rows (cosine), fp16 -> fp32.
+struct PrepArgs {
+  const void* x;   // rows [n, d], fp32 or binary16
+  int64_t n;
+  int d;
+  int f16;         // x holds binary16
+  float* norm;     // out: sum of squares [n] (may be null)
+  float* unit;     // out: x / max(|x|, 1e-30) as fp32 [n, d] (may be null)
+  float* upcast;   // out: x as fp32 [n, d] (may be null)
+};
+hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
+
+// Fused distance + per-lane top-T selection.
+//   grid (nsplit, ceil(nq / 128)); workgroup 256 threads.
+// Lane l of wavefront w of block (split, qb) keeps the best T candidates of
+// query qb*128 + 32w + l%32 among base rows of the split whose tile position
+// has bit 2 equal to l/32 ("segment" 2*split + l/32).  Output part
+// [nq][nseg = 2*nsplit][T] of ranks (see rank_of); 0 marks an empty slot.
+struct FusedArgs {
+  const void* base;      // [n, d] fp32 or binary16 (prepared: unit rows for cosine)
+  const void* queries;   // [nq, d]
+  const float* bnorm;    // [n] squared norms (L2), else null
+  int64_t n;
+  int nq;
+  int d;
+  int metric;            // kInnerProduct / kL2 / kCosine (cosine == IP on unit rows)
+  int64_t rows_per_split;
+  int nsplit;
+  int T;                 // list length per lane
+  uint64_t* part;        // [nq][2*nsplit][T]
+  int vec;               // rows may be read as 16-byte vectors (d multiple of
+                         // 4 (fp32) / 8 (fp16) and 16-byte aligned pointers)
+};
+hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
+hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
+// true when the fused kernels have an instance for (d, T)
+bool fused_supported(int d, int T, bool f16);
+
+// Exact merge of the per-segment lists into the final sorted k best.
+//   grid nq; workgroup 256 threads.
+struct MergeArgs {
+  const uint64_t* part;  // [nq][nseg][T]
+  int nseg;
+  int T;
+  int k;
+  int nq;
+  int metric;            // output convention: L2 distances or similarities
+  const float* qnorm;    // [nq] (L2), else null
+  int dist_mode;         // 0: float metric, 1: Hamming (score = -distance)
+  int32_t* ids;          // [nq][k]
+  float* dists;          // [nq][k] (may be null)
+  int* flags;            // [nq] set to 1 when a segment may have dropped a member
+};
+hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
+
+// Exhaustive path (exact for every input, used when the fused path does not
+// apply and for queries the merge flagged).  Scores of `rows` queries (query
+// i is queries[qsel[i]]) against all n base rows into S [rows][n], then a
+// radix select of each row.
+struct ScoresArgs {
+  const float* base;     // [n, d] fp32 (prepared)
+  const float* queries;  // [*, d] fp32 (prepared)
+  const int* qsel;       // [rows] query index of each scored row
+  const float* bnorm;    // [n] (L2) else null
+  int64_t n;
+  int rows;
+  int d;
+  int metric;
+  float* S;              // [rows][n]
+};
+hipError_t launch_scores(const ScoresArgs& a, hipStream_t s);
+
+struct SelectArgs {
+  const float* S;        // [rows][n] scores (larger is better)
+  int64_t n;
+  int rows;
+  int k;
+  const int* qsel;       // [rows] output row of each scored row
+  int metric;
+  const float* qnorm;    // indexed by qsel (L2) else null
+  int dist_mode;         // 0 float metric, 1 Hamming
+  int32_t* ids;
+  float* dists;
+};
+hipError_t launch_select(const SelectArgs& a, hipStream_t s);
+
+// Output fill for empty inputs: ids -1, distances `pad`.
+hipError_t launch_fill(int32_t* ids, float* dists, int64_t count, float pad,
+                       hipStream_t s);
+
+// Hamming: packed uint32 words.
+struct PackArgs {
+  const uint8_t* bytes;  // [n, nbytes]
+  int64_t n;
+  int nbytes;
+  uint32_t* words;       // out [n, wp]
+  int wp;                // words per packed row, >= ceil(nbytes / 4)
+};
+hipError_t launch_pack(const PackArgs& a, hipStream_t s);
+
+struct HammingArgs {
+  const uint32_t* base;    // [n, W]
+  const uint32_t* queries; // [nq, W]
+  int64_t n;
+  int nq;
+  int W;
+  int64_t rows_per_split;
+  int nsplit;
+  int T;
+  uint64_t* part;          // [nq][nsplit][T]
+};
+hipError_t launch_hamming(const HammingArgs& a, hipStream_t s);
+bool hamming_supported(int W, int T);
+// The padded word count the fused Hamming kernel takes for W words (0: none).
+int hamming_padded_words(int W);
+constexpr int kHammingQueriesPerBlock = 256;
+
+// Hamming scores for the exhaustive path: S[i][j] = -popcount(q ^ b).
+struct HammingScoresArgs {
+  const uint32_t* base;
+  const uint32_t* queries;
+  const int* qsel;
+  int64_t n;
+  int rows;
+  int W;
+  float* S;
+};
+hipError_t launch_hamming_scores(const HammingScoresArgs& a, hipStream_t s);
+
+// Gather rows (for compacting flagged queries): out[i] = in[sel[i]].
+hipError_t launch_gather_f32(const float* in, const int* sel, int rows, int d,
+                             float* out, hipStream_t s);
+
+// Self-graph post-pass: drop each row's own id from a k+1 list and re-order
+// by distance (src/all_neighbors.cpp:56-95).
+struct SelfDropArgs {
+  const int32_t* ids_in;   // [n][k+1]
+  const float* dists_in;
+  int64_t n;
+  int kin;                 // k + 1 (or n when n <= k)
+  int k;
+  int metric;
+  int32_t* ids;            // [n][k]
+  float* dists;
+};
+hipError_t launch_self_drop(const SelfDropArgs& a, hipStream_t s);
+
+}  // namespace mlxvs::kern

@@ -1,0 +1,134 @@
+// Device-side ordering helpers shared by the float and Hamming kernels.
+//
+// Selection order (reference src/kernels.h:14-24, 104-147): a candidate is
+// better when its order-preserving float key is larger, and among equal keys
+// when its id is lower (unsigned).  rank_of packs both into one 64-bit value
+// whose unsigned order is exactly that order, so every selection here is a
+// plain "largest k of a set of distinct uint64" problem.  An empty slot is 0,
+// which loses to every real candidate (the low word ~id is >= 2^31 for any
+// id < 2^31).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlxvs::kern {
+
+// Larger float, larger key (reference src/kernels.h:16-19).
+__device__ __forceinline__ uint32_t key_of(float v) {
+  uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inverse of key_of.
+__device__ __forceinline__ float score_of_key(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint64_t rank_of(float s, uint32_t id) {
+  return ((uint64_t)key_of(s) << 32) | (uint32_t)(~id);
+}
+
+__device__ __forceinline__ int32_t id_of_rank(uint64_t r) {
+  return (int32_t)(~(uint32_t)r);
+}
+
+// The final order of the reference's bitonic sort (src/kernels.h:20-23):
+// float score descending -- so -0.0 and +0.0 tie -- then id ascending.  Keys
+// of -0.0 (0x7fffffff) and +0.0 (0x80000000) are adjacent, so mapping the
+// first onto the second gives that order as an unsigned comparison.
+__device__ __forceinline__ uint64_t output_order(uint64_t r) {
+  uint32_t k = (uint32_t)(r >> 32);
+  k = k == 0x7fffffffu ? 0x80000000u : k;
+  return ((uint64_t)k << 32) | (uint32_t)r;
+}
+
+// Sorted insertion into a descending register list: the candidate walks down
+// and swaps with every entry it beats; a candidate worse than L[T-1] leaves
+// the list unchanged.  5 VALU ops per slot (one 64-bit compare, four selects).
+template <int T>
+__device__ __forceinline__ void list_insert(uint64_t (&L)[T], uint64_t c) {
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    uint64_t cur = L[j];
+    bool b = c > cur;
+    L[j] = b ? c : cur;
+    c = b ? cur : c;
+  }
+}
+
+// In-LDS bitonic sort of P (a power of two) values, descending by `ord`.
+// All threads of the workgroup call it; it ends with a barrier.
+template <int NT, typename Ord>
+__device__ void bitonic_desc(uint64_t* buf, int P, Ord ord) {
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (P >> 1); i += NT) {
+        int lo = (i / stride) * 2 * stride + (i % stride);
+        int hi = lo + stride;
+        uint64_t x = buf[lo], y = buf[hi];
+        bool desc = (lo & size) == 0;
+        uint64_t ox = ord(x), oy = ord(y);
+        bool swap = desc ? (ox < oy) : (ox > oy);
+        if (swap) {
+          buf[lo] = y;
+          buf[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+struct IdentityOrder {
+  __device__ uint64_t operator()(uint64_t r) const { return r; }
+};
+struct OutputOrder {
+  __device__ uint64_t operator()(uint64_t r) const { return output_order(r); }
+};
+
+__device__ __forceinline__ int pow2_at_least(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// Writes the k best of `best` (sorted descending by rank, first k entries
+// valid, 0 = empty) to ids / dists row `orow`, in the reference's output
+// order.  `work` is LDS scratch of at least pow2(k) entries.  Distances:
+// dist_mode 0 -> L2: max(qn - s, 0) (+inf when empty); IP / cosine: s
+// (-inf when empty); dist_mode 1 -> Hamming: -s (+inf when empty).
+template <int NT>
+__device__ void emit_topk(const uint64_t* best, uint64_t* work, int k,
+                          int64_t orow, int metric, float qn, int dist_mode,
+                          int32_t* ids, float* dists) {
+  const int K2 = pow2_at_least(k);
+  for (int i = threadIdx.x; i < K2; i += NT) work[i] = i < k ? best[i] : 0;
+  __syncthreads();
+  bitonic_desc<NT>(work, K2, OutputOrder{});
+  const bool l2 = metric == 1;
+  for (int i = threadIdx.x; i < k; i += NT) {
+    uint64_t r = work[i];
+    int64_t o = orow * k + i;
+    if (r == 0) {
+      ids[o] = -1;
+      if (dists) dists[o] = (dist_mode == 1 || l2) ? INFINITY : -INFINITY;
+    } else {
+      ids[o] = id_of_rank(r);
+      float s = score_of_key((uint32_t)(r >> 32));
+      if (dists) {
+        if (dist_mode == 1) {
+          dists[o] = -s;
+        } else if (l2) {
+          float v = qn - s;  // reference src/knn.cpp:126-129
+          dists[o] = v > 0.0f ? v : 0.0f;
+        } else {
+          dists[o] = s;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace mlxvs::kern

@@ -1,0 +1,184 @@
+"""Python access to the CPU restatement (oracle/knn_oracle.c) and float64 helpers.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the engine (mlxvs_amd/).
+
+Two layers:
+  * restated(...) functions call liboracle.so, the float32 restatement of the
+    reference's semantics (see the header of knn_oracle.c for file:line
+    citations).  They are bit-exact against the reference on integer-valued
+    inputs and follow its tie rule (lowest id) everywhere.
+  * exact_*(...) functions are independent float64 NumPy brute force with an
+    np.lexsort tie-break, used to pin the restatement and to compute recall.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.oracle_knn_f32.argtypes = [vp, i64, vp, i64, ci, ci, ci, ci, vp, vp]
+        L.oracle_self_graph_f32.argtypes = [vp, i64, ci, ci, ci, ci, vp, vp]
+        L.oracle_hamming.argtypes = [vp, i64, vp, i64, ci, ci, ci, vp, vp]
+        L.oracle_f16_to_f32.argtypes = [vp, i64, vp]
+        L.oracle_pack_words.argtypes = [vp, i64, ci, vp]
+        L.oracle_key.argtypes = [ctypes.c_float]
+        L.oracle_key.restype = ctypes.c_uint32
+        for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_hamming",
+                  "oracle_f16_to_f32", "oracle_pack_words"):
+            getattr(L, f).restype = ci
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def threads() -> int:
+    return int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1))
+
+
+METRICS = {"inner_product": 0, "l2": 1, "cosine": 2}
+
+
+def _m(metric) -> int:
+    return METRICS[metric] if isinstance(metric, str) else int(metric)
+
+
+# ---- the restatement ----------------------------------------------------------
+
+def knn(base, queries, k, metric="l2", nthreads=None):
+    """float32 restatement of brute_force_knn (src/knn.cpp:71-142)."""
+    b = np.ascontiguousarray(base, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq = q.shape[0]
+    ids = np.empty((nq, k), np.int32)
+    dist = np.empty((nq, k), np.float32)
+    rc = lib().oracle_knn_f32(_p(b), b.shape[0], _p(q), nq, b.shape[1], k, _m(metric),
+                              nthreads or threads(), _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_knn_f32 rejected the arguments ({rc})")
+    return ids, dist
+
+
+def self_graph(rows, k, metric="l2", nthreads=None):
+    """Restated single-cluster all_neighbors (src/all_neighbors.cpp:250-263, 56-95)."""
+    x = np.ascontiguousarray(rows, dtype=np.float32)
+    n = x.shape[0]
+    ids = np.empty((n, k), np.int32)
+    dist = np.empty((n, k), np.float32)
+    rc = lib().oracle_self_graph_f32(_p(x), n, x.shape[1], k, _m(metric),
+                                     nthreads or threads(), _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_self_graph_f32 rejected the arguments ({rc})")
+    return ids, dist
+
+
+def hamming(rows, queries, k, nthreads=None):
+    """Restated hamming_knn (src/ivf.cpp:1343-1403)."""
+    r = np.ascontiguousarray(rows, dtype=np.uint8)
+    q = np.ascontiguousarray(queries, dtype=np.uint8)
+    nq = q.shape[0]
+    ids = np.empty((nq, k), np.int32)
+    dist = np.empty((nq, k), np.float32)
+    rc = lib().oracle_hamming(_p(r), r.shape[0], _p(q), nq, r.shape[1], k,
+                              nthreads or threads(), _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_hamming rejected the arguments ({rc})")
+    return ids, dist
+
+
+def f16_to_f32(x):
+    h = np.ascontiguousarray(x, dtype=np.float16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_f16_to_f32(_p(h.view(np.uint16)), h.size, _p(out))
+    return out
+
+
+def pack_words(rows):
+    r = np.ascontiguousarray(rows, dtype=np.uint8)
+    w = (r.shape[1] + 3) // 4
+    out = np.empty((r.shape[0], w), np.uint32)
+    lib().oracle_pack_words(_p(r), r.shape[0], r.shape[1], _p(out))
+    return out
+
+
+def key(v: float) -> int:
+    return int(lib().oracle_key(ctypes.c_float(v)))
+
+
+# ---- independent float64 brute force -------------------------------------------
+
+def exact_scores(queries, base, metric="l2"):
+    """float64 scores, larger is closer (-squared distance for L2), as
+    python/tests/test_mlxvs.py:13-20 and tests/test_knn.cpp:35-52."""
+    q = np.asarray(queries, dtype=np.float64)
+    b = np.asarray(base, dtype=np.float64)
+    m = _m(metric)
+    if m == 1:
+        qq = (q * q).sum(1)[:, None]
+        bb = (b * b).sum(1)[None, :]
+        return -(qq + bb - 2.0 * (q @ b.T))
+    if m == 2:
+        q = q / np.maximum(np.linalg.norm(q, axis=1, keepdims=True), 1e-300)
+        b = b / np.maximum(np.linalg.norm(b, axis=1, keepdims=True), 1e-300)
+    return q @ b.T
+
+
+def exact_topk(scores, k):
+    """ids of the k best per row by (score desc, id asc), -1 padded."""
+    nq, n = scores.shape
+    keff = min(k, n)
+    ids = np.full((nq, k), -1, np.int64)
+    col = np.arange(n)
+    for i in range(nq):
+        order = np.lexsort((col, -scores[i]))[:keff]
+        ids[i, :keff] = order
+    return ids
+
+
+def hamming_distances(queries, rows):
+    """popcount(q ^ r) for every pair (python/tests/test_cuvs.py:772-773)."""
+    q = np.asarray(queries, dtype=np.uint8)
+    r = np.asarray(rows, dtype=np.uint8)
+    lut = np.array([bin(i).count("1") for i in range(256)], dtype=np.int32)
+    out = np.empty((q.shape[0], r.shape[0]), dtype=np.int32)
+    for i in range(q.shape[0]):
+        out[i] = lut[q[i][None, :] ^ r].sum(1)
+    return out
+
+
+def recall(ids, scores, k, tol=1e-4):
+    """Tie-tolerant recall@k (tests/test_knn.cpp:54-56, 85): an id counts when
+    its exact score reaches the exact k-th minus tol * max(1, |kth|)."""
+    n = scores.shape[1]
+    keff = min(k, n)
+    kth = -np.partition(-scores, keff - 1, axis=1)[:, keff - 1: keff]
+    ok = ids[:, :keff] >= 0
+    got = np.take_along_axis(scores, np.maximum(ids[:, :keff], 0), axis=1)
+    hit = (got >= kth - tol * np.maximum(1.0, np.abs(kth))) & ok
+    return hit.sum() / (ids.shape[0] * keff)

@@ -1,0 +1,285 @@
+"""GPU parity of the float exact k-NN path (brute_force_knn) with the oracle.
+
+Bars:
+  * integer-valued inputs (configurations c1, c2): ids and distances
+    bit-exact against the CPU restatement and the float64 golden fixtures;
+  * float inputs: recall@k = 1.0 against float64 (tie-tolerant as the
+    reference's tests/test_knn.cpp:54-56, 85), distances within
+    1e-4 * max(1, |exact|) (fp32) or 2e-3 (fp16), rows sorted nearest first.
+Cases follow the reference's tests/test_knn.cpp:156-207 and
+python/tests/test_mlxvs.py:30-87, 206-245.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from mlxvs_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rows(n, d, seed):
+    return np.random.default_rng(seed).standard_normal((n, d), dtype=np.float32)
+
+
+def check_float(oracle, ids, dist, base, q, k, metric, tol=1e-4):
+    """recall 1.0 vs float64 (tie-tolerant), distances within tol, sorted,
+    -1 / +-inf padding."""
+    n = base.shape[0]
+    keff = min(k, n)
+    s = oracle.exact_scores(q, base, metric)
+    assert ids.shape == (q.shape[0], k) and dist.shape == (q.shape[0], k)
+    assert (ids[:, keff:] == -1).all()
+    if keff < k:
+        pad = np.inf if metric == "l2" else -np.inf
+        assert (dist[:, keff:] == pad).all()
+    assert (ids[:, :keff] >= 0).all() and (ids[:, :keff] < n).all()
+    assert oracle.recall(ids, s, k, tol) == 1.0
+    exact = np.take_along_axis(s, ids[:, :keff], 1)
+    exact = -exact if metric == "l2" else exact
+    err = np.abs(exact - dist[:, :keff]) / np.maximum(1.0, np.abs(exact))
+    assert err.max() < tol, err.max()
+    step = np.diff(dist[:, :keff], axis=1)
+    if metric == "l2":
+        assert (step >= -1e-5 * np.maximum(1, np.abs(dist[:, 1:keff]))).all()
+    else:
+        assert (step <= 1e-5 * np.maximum(1, np.abs(dist[:, 1:keff]))).all()
+    # distinct ids per row
+    for r in ids[:, :keff]:
+        assert len(set(r.tolist())) == keff
+
+
+# ---- integer-valued configurations: bit-exact -----------------------------------
+
+def test_c1_bit_exact(engine, oracle):
+    base = synth.c1_rows(1, 0, 10_000)
+    q = synth.c1_rows(2, 0, 100)
+    ids, dist = engine.brute_force_knn(base, q, 10, "l2")
+    oid, odist = oracle.knn(base, q, 10, "l2")
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(dist, odist)
+    g = np.load(GOLDEN / "c1_full.npz")
+    assert np.array_equal(ids, g["ids"])
+    assert np.array_equal(dist, g["dist"].astype(np.float32))
+
+
+@pytest.fixture(scope="module")
+def c2_data():
+    cen = synth.c2_centres()
+    base = synth.chunked(lambda lo, hi: synth.c2_rows(1, lo, hi, centres=cen), 1_000_000)
+    q = synth.chunked(lambda lo, hi: synth.c2_rows(2, lo, hi, centres=cen), 10_000)
+    return base, q
+
+
+def test_c2_full_bit_exact(engine, oracle, c2_data):
+    base, q = c2_data
+    ids, dist = engine.brute_force_knn(base, q, 10, "l2")
+    g = np.load(GOLDEN / "c2_subset.npz")
+    assert np.array_equal(ids[:64], g["ids"])
+    assert np.array_equal(dist[:64], g["dist"].astype(np.float32))
+    # a strided sample of all queries against the CPU restatement
+    sel = np.arange(0, 10_000, 97)
+    oid, odist = oracle.knn(base, q[sel], 10, "l2")
+    assert np.array_equal(ids[sel], oid)
+    assert np.array_equal(dist[sel], odist)
+    # every returned distance is the exact integer squared distance
+    diff = base[ids.astype(np.int64)] - q[:, None, :]
+    assert np.array_equal(dist, (diff.astype(np.float64) ** 2).sum(-1).astype(np.float32))
+    assert (np.diff(dist, axis=1) >= 0).all()
+
+
+def test_c2_device_api_matches_host_api(engine, c2_data):
+    from mlxvs_amd import _hip
+
+    base, q = c2_data
+    q = q[:2000]
+    db, dq = _hip.DeviceBuffer.from_array(base), _hip.DeviceBuffer.from_array(q)
+    di, dd = _hip.DeviceBuffer(q.shape[0] * 10 * 4), _hip.DeviceBuffer(q.shape[0] * 10 * 4)
+    engine.brute_force_knn_device(db.value, base.shape[0], dq.value, q.shape[0], 128, 10,
+                                  "l2", di.value, dd.value)
+    _hip.synchronize()
+    ids = di.download((q.shape[0], 10), np.int32)
+    dist = dd.download((q.shape[0], 10), np.float32)
+    hid, hdist = engine.brute_force_knn(base, q, 10, "l2")
+    assert np.array_equal(ids, hid) and np.array_equal(dist, hdist)
+
+
+# ---- reference test cases (float data) ------------------------------------------
+
+CASES = [  # tests/test_knn.cpp:197-207 (metric, name, n, nq, d, k)
+    ("inner_product", 5000, 64, 64, 10),
+    ("inner_product", 5000, 64, 64, 100),
+    ("cosine", 5000, 64, 96, 96),
+    ("l2", 5000, 64, 128, 32),
+    ("l2", 3000, 16, 32, 256),
+    ("inner_product", 50, 8, 16, 100),
+    ("cosine", 4000, 32, 64, 1),
+    ("l2", 5000, 61, 64, 16),
+    ("cosine", 3000, 29, 32, 10),
+]
+
+
+@pytest.mark.parametrize("metric,n,nq,d,k", CASES)
+def test_reference_cases(engine, oracle, metric, n, nq, d, k):
+    base, q = rows(n, d, 1), rows(nq, d, 2)
+    ids, dist = engine.brute_force_knn(base, q, k, metric)
+    check_float(oracle, ids, dist, base, q, k, metric)
+
+
+@pytest.mark.parametrize("metric", ["inner_product", "l2", "cosine"])
+@pytest.mark.parametrize("k", [10, 100, 256])
+def test_python_grid(engine, oracle, metric, k):
+    # python/tests/test_mlxvs.py:30-48
+    base, q = rows(3000, 48, 1), rows(32, 48, 2)
+    ids, dist = engine.brute_force_knn(base, q, k, metric)
+    check_float(oracle, ids, dist, base, q, k, metric)
+
+
+@pytest.mark.parametrize("d", [1, 3, 7, 8, 13, 31, 64, 100, 129, 200, 256, 257, 300])
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_dimensions(engine, oracle, d, metric):
+    base, q = rows(20_000, d, 3), rows(300, d, 4)
+    ids, dist = engine.brute_force_knn(base, q, 10, metric)
+    check_float(oracle, ids, dist, base, q, 10, metric)
+
+
+@pytest.mark.parametrize("k", [1, 4, 5, 8, 9, 10, 11, 16, 17, 32, 64, 65, 128, 256])
+def test_k_values_large_n(engine, oracle, k):
+    # exercises every list length and the k > T check of the merge
+    base, q = rows(200_000, 32, 5), rows(200, 32, 6)
+    ids, dist = engine.brute_force_knn(base, q, k, "l2")
+    check_float(oracle, ids, dist, base, q, k, "l2")
+
+
+def test_float_data_vs_restatement(engine, oracle):
+    # ids equal to the float32 restatement wherever its k-th and (k+1)-th
+    # scores are not within rounding of each other
+    base, q = rows(50_000, 64, 7), rows(128, 64, 8)
+    ids, dist = engine.brute_force_knn(base, q, 10, "l2")
+    oid, odist = oracle.knn(base, q, 10, "l2")
+    np.testing.assert_allclose(dist, odist, rtol=1e-4, atol=1e-4)
+    same = (ids == oid).all(1).mean()
+    assert same > 0.95
+
+
+def test_ties_keep_lowest_ids(engine):
+    # tests/test_knn.cpp:156-192
+    g = np.load(GOLDEN / "kat_ties.npz")
+    first, _ = engine.brute_force_knn(g["base"], g["queries"], 10, "l2")
+    for _ in range(20):
+        again, _ = engine.brute_force_knn(g["base"], g["queries"], 10, "l2")
+        assert np.array_equal(again, first)
+    assert np.array_equal(first, g["ids"])
+
+
+def test_massive_ties_large_k(engine):
+    # every row at the same distance: the k lowest ids, for k above the
+    # register list length (the merge's check sends these to the
+    # exhaustive select)
+    x = np.ones((100_000, 16), np.float32)
+    ids, dist = engine.brute_force_knn(x, x[:5], 100, "l2")
+    assert (ids == np.arange(100)[None, :]).all()
+    assert (dist == 0).all()
+
+
+def test_sorted_data_forces_exhaustive_check(engine, oracle):
+    # consecutive ids are nearest: one segment holds the whole answer
+    x = np.arange(300_000, dtype=np.float32)[:, None] * 0.5
+    q = np.array([[1000.3], [77777.1], [149999.0]], np.float32)
+    for k in (50, 256):
+        ids, dist = engine.brute_force_knn(x, q, k, "l2")
+        oid, odist = oracle.knn(x, q, k, "l2")
+        assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+
+
+def test_fewer_rows_than_k(engine):
+    # python/tests/test_mlxvs.py:63-69
+    b, q = rows(5, 8, 3), rows(4, 8, 4)
+    ids, dist = engine.brute_force_knn(b, q, 8, "l2")
+    assert (ids[:, :5] >= 0).all() and (ids[:, 5:] == -1).all()
+    assert np.isinf(dist[:, 5:]).all() and (dist[:, 5:] > 0).all()
+    assert sorted(ids[0, :5].tolist()) == list(range(5))
+    ids, dist = engine.brute_force_knn(b, q, 8, "inner_product")
+    assert (ids[:, 5:] == -1).all() and (dist[:, 5:] == -np.inf).all()
+
+
+def test_tiny_shapes(engine, oracle):
+    # python/tests/test_mlxvs.py:51-60
+    b, q = rows(100, 8, 21), rows(2, 8, 22)
+    ids, _ = engine.brute_force_knn(b, q, 3, "cosine")
+    s = oracle.exact_scores(q, b, "cosine")
+    assert oracle.recall(ids, s, 3) == 1.0
+    ids, _ = engine.brute_force_knn(b, q, 1, "l2", tile_rows=7)
+    assert ids.shape == (2, 1)
+
+
+def test_empty_inputs(engine):
+    ids, dist = engine.brute_force_knn(np.zeros((0, 4), np.float32), rows(3, 4, 1), 5, "l2")
+    assert (ids == -1).all() and (dist == np.inf).all()
+    ids, dist = engine.brute_force_knn(np.zeros((0, 4), np.float32), rows(3, 4, 1), 5, "cosine")
+    assert (ids == -1).all() and (dist == -np.inf).all()
+    ids, dist = engine.brute_force_knn(rows(10, 4, 1), np.zeros((0, 4), np.float32), 5, "l2")
+    assert ids.shape == (0, 5)
+
+
+def test_non_contiguous_input(engine):
+    # python/tests/test_mlxvs.py:81-87
+    b = rows(500, 64, 5)
+    bt = np.ascontiguousarray(b.T).T
+    q = rows(8, 64, 6)
+    a1, _ = engine.brute_force_knn(bt, q, 10, "l2")
+    a2, _ = engine.brute_force_knn(b, q, 10, "l2")
+    assert np.array_equal(a1, a2)
+
+
+@pytest.mark.parametrize("convert", [
+    lambda x: x, lambda x: x.astype(np.float64), lambda x: x.tolist(),
+    lambda x: x.astype(np.float16)], ids=["numpy", "float64", "list", "float16"])
+def test_array_likes_and_dtypes(engine, convert):
+    # python/tests/test_mlxvs.py:206-226
+    x = rows(500, 16, 15)
+    want, _ = engine.brute_force_knn(x, x, 5, "l2")
+    got, _ = engine.brute_force_knn(convert(x), convert(x), 5, "l2")
+    assert (got[:, 0] == np.arange(500)).all()
+    assert (got == want).mean() > 0.9
+
+
+def test_metric_names(engine):
+    # python/tests/test_mlxvs.py:228-237
+    x = rows(300, 8, 16)
+    for name in ["l2", "cosine", "inner_product"]:
+        a, _ = engine.brute_force_knn(x, x, 3, name)
+        b, _ = engine.brute_force_knn(x, x, 3, getattr(engine.Metric, name))
+        assert (a == b).all()
+
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("d", [64, 128, 200, 256])
+def test_fp16_path(engine, oracle, metric, d):
+    # binary16 storage, fp16 MFMA with fp32 accumulation: the products are
+    # exact, so the result is the float32 computation on upcast rows
+    b = rows(30_000, d, 9).astype(np.float16)
+    q = rows(100, d, 10).astype(np.float16)
+    ids, dist = engine.brute_force_knn(b, q, 16, metric)
+    check_float(oracle, ids, dist, oracle.f16_to_f32(b), oracle.f16_to_f32(q), 16, metric,
+                tol=2e-3)
+
+
+def test_c3_subset(engine, oracle):
+    cen = synth.c3_centres()
+    base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen), 100_000,
+                         chunk=5_000)
+    q = synth.c3_rows(2, 0, 16, centres=cen)
+    g = np.load(GOLDEN / "c3_subset.npz")
+    for metric, key in (("inner_product", "ip"), ("cosine", "cos")):
+        ids, dist = engine.brute_force_knn(base, q, 10, metric)
+        s = oracle.exact_scores(q, base, metric)
+        assert oracle.recall(ids, s, 10) == 1.0
+        exact = np.take_along_axis(s, ids, 1)
+        assert np.abs(exact - dist).max() < 1e-4
+        np.testing.assert_allclose(dist, g["score_" + key], atol=1e-4)
+        assert (ids == g["ids_" + key]).mean() > 0.95

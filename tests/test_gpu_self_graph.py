@@ -1,0 +1,59 @@
+"""GPU parity of the self k-NN graph (single-cluster brute-force all_neighbors).
+
+Reference: src/all_neighbors.cpp:250-263 (k + 1 neighbours) and 56-95
+(merge_lists: drop -1 and the row itself, order by distance, keep k).
+Configuration c5 (float16 storage, L2, k = 64) against float64 golden rows,
+and small cases against the CPU restatement.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from mlxvs_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rows(n, d, seed):
+    return np.random.default_rng(seed).standard_normal((n, d), dtype=np.float32)
+
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_small_vs_restatement(engine, oracle, metric):
+    x = rows(3000, 24, 1)
+    ids, dist = engine.all_neighbors(x, 8, metric)
+    oid, odist = oracle.self_graph(x, 8, metric)
+    assert (ids != np.arange(3000)[:, None]).all()
+    np.testing.assert_allclose(dist, odist, rtol=1e-4, atol=1e-4)
+    assert (ids == oid).mean() > 0.99
+
+
+def test_fewer_rows_than_k(engine, oracle):
+    x = rows(5, 4, 2)
+    ids, dist = engine.all_neighbors(x, 8, "l2")
+    oid, odist = oracle.self_graph(x, 8, "l2")
+    assert np.array_equal(ids, oid)
+    assert (ids[:, 4:] == -1).all() and np.isinf(dist[:, 4:]).all()
+
+
+def test_c5_subset(engine, oracle):
+    cen = synth.c5_centres()
+    x = synth.chunked(lambda lo, hi: synth.c5_rows(1, lo, hi, centres=cen), 200_000)
+    ids, dist = engine.all_neighbors(x, 64, "l2")
+    assert ids.shape == (200_000, 64)
+    assert (ids != np.arange(200_000)[:, None]).all()
+    assert (ids >= 0).all()
+    assert (np.diff(dist, axis=1) >= 0).all()
+    g = np.load(GOLDEN / "c5_subset.npz")
+    xf = oracle.f16_to_f32(x)
+    s = oracle.exact_scores(xf[:32], xf, "l2")
+    s[np.arange(32), np.arange(32)] = -np.inf
+    assert oracle.recall(ids[:32], s, 64, tol=2e-3) == 1.0
+    exact = -np.take_along_axis(s, ids[:32], 1)
+    assert (np.abs(exact - dist[:32]) / np.maximum(1, exact)).max() < 2e-3
+    np.testing.assert_allclose(dist[:32], g["dist"], rtol=2e-3)
+    assert (ids[:32] == g["ids"]).mean() > 0.95
