@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Benchmark of the exact k-NN hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 2] [--workload c2]
+
+Default workload (BASELINE.json metric): configuration c2, exact L2 k-NN,
+k = 10, 1,000,000 x 128 float32 base rows (1,024-component mixture, integer
+values in [0, 255]) and 10,000 queries.  Inputs are generated with
+mlxvs_amd.synth, copied to HBM before timing, and one step is one
+mlxvs_brute_force_knn_device call over all 10,000 queries (norms, fused
+MFMA distance + top-k, merge).  W warm-up steps, then exactly K timed steps
+between two device synchronisations; value = queries answered per second.
+
+The same JSON line carries:
+  roofline      the fused kernel's achieved FP32 MFMA rate, from HIP events
+                recorded around each of its launches inside the timed steps
+                (2 nq n d flops per launch over its mean duration), against
+                MI355X's 157.3 TFLOP/s; traffic = HBM bytes per launch from the
+                committed rocprofv3 counter summary when present;
+  cpu_baseline  the CPU restatement of the reference path (oracle/, a port:
+                the reference itself runs only on Apple GPUs) timed on this
+                host's cores over a bounded query sample;
+  check         the last step's answers for the first 64 queries against the
+                float64 golden fixture (bit-exact, integer-valued data).
+
+Other workloads (c1, c3, c4, c5) are for measurement runs; the driver's line
+is the default.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("queries/s, exact kNN k=10 on 1M×128 fp32 (10k queries); "
+          "% of MFMA/HBM roofline")
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense FP32 matrix
+PEAK_FP16_MFMA = 2516.6  # TFLOP/s, MI355X dense FP16 matrix
+PEAK_HBM = 8000.0        # GB/s
+VALU_LANE_OPS = 256 * 64 * 2.4e9  # non-packed VALU lane-ops per second
+
+
+def workload(name: str):
+    from mlxvs_amd import synth
+
+    if name == "c1":
+        base = synth.c1_rows(1, 0, 10_000)
+        q = synth.c1_rows(2, 0, 100)
+        return dict(kind="float", base=base, q=q, k=10, metric="l2",
+                    desc="c1: exact L2 kNN k=10, 10k x 128 fp32 (int-valued), 100 queries")
+    if name == "c2":
+        cen = synth.c2_centres()
+        base = synth.chunked(lambda lo, hi: synth.c2_rows(1, lo, hi, centres=cen), 1_000_000)
+        q = synth.chunked(lambda lo, hi: synth.c2_rows(2, lo, hi, centres=cen), 10_000)
+        return dict(kind="float", base=base, q=q, k=10, metric="l2",
+                    desc="c2: exact L2 kNN k=10, 1M x 128 fp32 base (1024-component "
+                         "mixture, int-valued in [0,255]), 10k queries")
+    if name in ("c3", "c3cos"):
+        cen = synth.c3_centres()
+        base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen),
+                             1_000_000, chunk=4096)
+        q = synth.chunked(lambda lo, hi: synth.c3_rows(2, lo, hi, centres=cen), 10_000,
+                          chunk=4096)
+        metric = "cosine" if name == "c3cos" else "inner_product"
+        return dict(kind="float", base=base, q=q, k=10, metric=metric,
+                    desc=f"c3: exact {metric} kNN k=10, 1M x 1536 unit rows, 10k queries")
+    if name == "c4":
+        gen = lambda lo, hi: synth.c4_codes(1, lo, hi)  # noqa: E731
+        base = synth.chunked(gen, 1_000_000)
+        q, _ = synth.c4_queries(gen, 1_000_000, 2, 0, 10_000)
+        return dict(kind="hamming", base=base, q=q, k=100, metric="hamming",
+                    desc="c4: exact Hamming kNN k=100, 1M x 1024-bit codes, 10k queries")
+    if name == "c5":
+        cen = synth.c5_centres()
+        x = synth.chunked(lambda lo, hi: synth.c5_rows(1, lo, hi, centres=cen), 200_000)
+        return dict(kind="self", base=x, q=x, k=64, metric="l2",
+                    desc="c5: self kNN graph, 200k x 256 fp16, L2, k=64, self excluded")
+    raise SystemExit(f"unknown workload {name}")
+
+
+def cpu_baseline(w, sample: int):
+    """The CPU restatement on the first `sample` queries, all host cores."""
+    import oracle
+
+    threads = os.cpu_count() or 1
+    base, q = w["base"], w["q"][:sample]
+    t0 = time.perf_counter()
+    if w["kind"] == "hamming":
+        oracle.hamming(base, q, w["k"], nthreads=threads)
+    elif w["kind"] == "self":
+        x = oracle.f16_to_f32(base)
+        oracle.knn(x, x[:sample], w["k"] + 1, w["metric"], nthreads=threads)
+    else:
+        oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(sample / dt, 2), "unit": "queries/s", "cores": threads,
+            "kind": "port",
+            "sample": f"first {sample} of {w['q'].shape[0]} queries against all "
+                      f"{base.shape[0]} rows, {dt:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c2")
+    ap.add_argument("--cpu-sample", type=int, default=None,
+                    help="queries timed on the CPU restatement (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        return 2
+
+    import mlxvs_amd
+    from mlxvs_amd import _hip
+
+    w = workload(args.workload)
+    base, q, k = w["base"], w["q"], w["k"]
+    n, nq = base.shape[0], q.shape[0]
+    d = base.shape[1]
+    db = _hip.DeviceBuffer.from_array(base)
+    dq = db if w["kind"] == "self" else _hip.DeviceBuffer.from_array(q)
+    di = _hip.DeviceBuffer(nq * k * 4)
+    dd = _hip.DeviceBuffer(nq * k * 4)
+
+    def step():
+        if w["kind"] == "float":
+            mlxvs_amd.brute_force_knn_device(db.value, n, dq.value, nq, d, k, w["metric"],
+                                             di.value, dd.value,
+                                             f16=base.dtype == np.float16)
+        elif w["kind"] == "hamming":
+            mlxvs_amd.hamming_knn_device(db.value, n, dq.value, nq, d, k, di.value, dd.value)
+        else:
+            mlxvs_amd.knn_self_graph_device(db.value, n, d, k, w["metric"], di.value,
+                                            dd.value, f16=base.dtype == np.float16)
+
+    for _ in range(args.warmup):
+        step()
+    _hip.synchronize()
+    mlxvs_amd.profile(True)
+    _hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    _hip.synchronize()
+    dt = time.perf_counter() - t0
+    stages = mlxvs_amd.profile_report()
+    mlxvs_amd.profile(False)
+    ms_per_step = dt * 1e3 / args.steps
+
+    ids = di.download((nq, k), np.int32)
+    dist = dd.download((nq, k), np.float32)
+    check = None
+    if args.workload in ("c1", "c2", "c4"):
+        fx = {"c1": "c1_full.npz", "c2": "c2_subset.npz", "c4": "c4_subset.npz"}[args.workload]
+        g = np.load(ROOT / "tests" / "golden" / fx)
+        m = g["ids"].shape[0]
+        ok = np.array_equal(ids[:m], g["ids"]) and np.array_equal(
+            dist[:m], g["dist"].astype(np.float32))
+        check = f"first {m} queries vs float64 golden: {'bit-exact' if ok else 'MISMATCH'}"
+
+    # roofline of the dominant kernel
+    if w["kind"] == "hamming":
+        kname = "hamming"
+        words = (d + 3) // 4
+        work = nq * n * words * 2.0  # XOR + popcount per word
+        cnt, tot = stages.get(kname, (0, 0.0))
+        per = tot / max(cnt, 1) / 1e3
+        roof = {"bound": "valu", "achieved": round(work / per / 1e12, 3),
+                "peak": round(VALU_LANE_OPS / 1e12, 2), "unit": "Tlane-op/s"}
+    else:
+        f16 = base.dtype == np.float16 and w["metric"] != "cosine"
+        kname = "fused_f16" if f16 else "fused_f32"
+        cnt, tot = stages.get(kname, (0, 0.0))
+        per = tot / max(cnt, 1) / 1e3
+        rows_q = nq
+        flops = 2.0 * rows_q * n * d
+        peak = PEAK_FP16_MFMA if f16 else PEAK_FP32_MFMA
+        roof = {"bound": "mfma", "achieved": round(flops / per / 1e12, 2), "peak": peak,
+                "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["kernel"] = kname
+    roof["kernel_ms"] = round(per * 1e3, 4)
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        t = json.loads(tfile.read_text()).get(args.workload, {})
+        traffic = t.get("hbm_bytes_per_launch")
+    roof["traffic"] = traffic
+
+    sample = args.cpu_sample
+    if sample is None:
+        sample = {"c1": 100, "c2": 10000, "c3": 16, "c3cos": 16, "c4": 256, "c5": 512}[args.workload]
+    cpu = cpu_baseline(w, min(sample, nq)) if sample else None
+
+    line = {
+        "metric": METRIC if args.workload == "c2" else w["desc"],
+        "value": round(nq / (ms_per_step / 1e3), 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if base.dtype == np.float16 else ("u32" if w["kind"] == "hamming" else "f32"),
+        "data": "synthetic (mlxvs_amd.synth, seeded splitmix64)",
+        "config": {"workload": w["desc"], "n": n, "nq": nq, "d": d, "k": k,
+                   "metric": w["metric"], "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "stages_ms_per_step": {s: round(v[1] / args.steps, 4) for s, v in stages.items()},
+        "check": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if (check is None or "bit-exact" in check) else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

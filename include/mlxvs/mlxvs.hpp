@@ -10,6 +10,7 @@
 
 #include <cstdint>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #define MLXVS_API __attribute__((visibility("default")))
@@ -100,5 +101,11 @@ MLXVS_API void release_workspace();
 
 /** "0.16.1-mi355x". */
 MLXVS_API const char* version();
+
+/** Per-stage kernel timing with HIP events (off by default).  Enabling or
+ * disabling clears the totals. */
+MLXVS_API void profile(bool enable);
+/** "stage count total_ms" lines for the launches since the last report. */
+MLXVS_API std::string profile_report();
 
 }  // namespace mlxvs

@@ -193,6 +193,21 @@ MLXVS_C_API int mlxvs_knn_self_graph_device(
  */
 MLXVS_C_API int mlxvs_release_workspace(void);
 
+/**
+ * Per-stage kernel timing: with enable != 0 every kernel launch of later
+ * calls is bracketed by HIP events on its stream (stages: prep, fused_f32,
+ * fused_f16, hamming, merge, scores, select, pack, fill, self_drop).
+ * Enabling or disabling clears the totals.
+ */
+MLXVS_C_API int mlxvs_profile(int enable);
+
+/**
+ * Writes "stage launches total_ms" lines for the launches since the last
+ * report into buf (NUL-terminated, truncated to len), waiting for their
+ * events, and clears the totals.
+ */
+MLXVS_C_API int mlxvs_profile_report(char* buf, int64_t len);
+
 #ifdef __cplusplus
 }
 #endif

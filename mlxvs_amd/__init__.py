@@ -60,6 +60,8 @@ def _load():
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_release_workspace": [],
+        "mlxvs_profile": [ctypes.c_int],
+        "mlxvs_profile_report": [ctypes.c_char_p, i64],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -236,6 +238,22 @@ def knn_self_graph_device(rows_ptr, n, d, k, metric, ids_ptr, dist_ptr, *, f16=F
     """mlxvs_knn_self_graph_device on device pointers (ints)."""
     _check(_L().mlxvs_knn_self_graph_device(rows_ptr, n, d, int(bool(f16)), int(k),
                                             int(_metric(metric)), ids_ptr, dist_ptr, stream))
+
+
+def profile(enable: bool = True) -> None:
+    """Enable (or disable) per-stage kernel timing with HIP events."""
+    _check(_L().mlxvs_profile(int(bool(enable))))
+
+
+def profile_report() -> dict:
+    """{stage: (launches, total_ms)} since the last report (waits for the events)."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(_L().mlxvs_profile_report(buf, len(buf)))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        out[name] = (int(cnt), float(ms))
+    return out
 
 
 def release_workspace() -> None:

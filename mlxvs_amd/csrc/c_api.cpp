@@ -4,6 +4,8 @@
 // -> MLXVS_ERROR_INVALID_ARGUMENT, any other exception -> MLXVS_ERROR_INTERNAL,
 // message kept per thread and cleared on success.  Host input checks follow
 // reference src/c_api.cpp:84-91 (host_rows) and :468-489 in the same order.
+#include <algorithm>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 
@@ -143,6 +145,20 @@ int mlxvs_knn_self_graph_device(const void* rows, int64_t n, int32_t d, int32_t 
     require(ids != nullptr, "ids must not be NULL.");
     auto x = host_rows(rows, n, d, f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32);
     mlxvs::knn_self_graph_device(x, k, to_metric(metric), ids, distances, stream);
+  });
+}
+
+int mlxvs_profile(int enable) {
+  return guarded([&] { mlxvs::profile(enable != 0); });
+}
+
+int mlxvs_profile_report(char* buf, int64_t len) {
+  return guarded([&] {
+    require(buf != nullptr && len > 0, "buf must hold at least one byte.");
+    const std::string r = mlxvs::profile_report();
+    const size_t n = std::min<size_t>(r.size(), (size_t)len - 1);
+    std::memcpy(buf, r.data(), n);
+    buf[n] = 0;
   });
 }
 

@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -41,6 +42,55 @@ void check_hip(hipError_t e, const char* what) {
     throw std::runtime_error(std::string("[mlxvs] ") + what + ": " +
                              hipGetErrorString(e));
   }
+}
+
+// ---- stage timing ------------------------------------------------------------------
+//
+// When enabled (mlxvs_profile), every kernel launch is bracketed by two HIP
+// events on the launch stream; mlxvs_profile_report waits for them and sums
+// the elapsed times per stage name.  Off by default: no events are created.
+std::mutex g_prof_mutex;
+bool g_prof_on = false;
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+std::vector<ProfRec> g_prof_pending;
+std::map<std::string, std::pair<int64_t, double>> g_prof_totals;
+
+template <typename F>
+void launch(hipStream_t s, const char* stage, F&& f) {
+  bool prof;
+  {
+    std::lock_guard<std::mutex> g(g_prof_mutex);
+    prof = g_prof_on;
+  }
+  hipEvent_t a = nullptr, b = nullptr;
+  if (prof) {
+    check_hip(hipEventCreate(&a), "hipEventCreate");
+    check_hip(hipEventCreate(&b), "hipEventCreate");
+    check_hip(hipEventRecord(a, s), "hipEventRecord");
+  }
+  check_hip(f(), stage);
+  if (prof) {
+    check_hip(hipEventRecord(b, s), "hipEventRecord");
+    std::lock_guard<std::mutex> g(g_prof_mutex);
+    g_prof_pending.push_back({stage, a, b});
+  }
+}
+
+void prof_collect() {
+  for (auto& r : g_prof_pending) {
+    float ms = 0.0f;
+    hipEventSynchronize(r.b);
+    hipEventElapsedTime(&ms, r.a, r.b);
+    auto& t = g_prof_totals[r.name];
+    t.first += 1;
+    t.second += ms;
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  g_prof_pending.clear();
 }
 
 int current_device() {
@@ -236,22 +286,24 @@ struct FloatInputs {
 };
 
 // Exhaustive exact k-NN for the queries listed in qsel (device ints), on
-// prepared fp32 rows.
+// fp32 rows of stride ld.
 void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
-                      const float* queries, const float* bnorm, const float* qnorm,
-                      int64_t n, int d, int metric, const int* qsel_dev, int rows,
-                      int k, int32_t* ids, float* dists) {
+                      const float* queries, int ld, const float* bnorm,
+                      const float* qnorm, int64_t n, int d, int metric,
+                      const int* qsel_dev, int rows, int k, int32_t* ids, float* dists) {
   if (rows <= 0) return;
   const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t(1) << 28) / std::max<int64_t>(n, 1)));
   float* S = ar.take<float>((size_t)per_block * (size_t)std::max<int64_t>(n, 1));
   for (int64_t r0 = 0; r0 < rows; r0 += per_block) {
     const int cnt = (int)std::min<int64_t>(per_block, rows - r0);
-    kern::ScoresArgs sa{base, queries, qsel_dev + r0, bnorm, n, cnt, d, metric, S};
-    check_hip(kern::launch_scores(sa, s), "scores kernel");
+    kern::ScoresArgs sa{base, queries, qsel_dev + r0, bnorm, n, cnt, d, ld, metric, S};
+    launch(s, "scores", [&] { return kern::launch_scores(sa, s); });
     kern::SelectArgs se{S, n, cnt, k, qsel_dev + r0, metric, qnorm, 0, ids, dists};
-    check_hip(kern::launch_select(se, s), "select kernel");
+    launch(s, "select", [&] { return kern::launch_select(se, s); });
   }
 }
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* ids,
                float* dists) {
@@ -261,54 +313,90 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int d = in.d;
   if (nq == 0 || k == 0) return;
   if (n == 0) {
-    check_hip(kern::launch_fill(ids, dists, nq * k,
-                                metric == kern::kL2 ? INFINITY : -INFINITY, s),
-              "fill kernel");
+    launch(s, "fill", [&] {
+      return kern::launch_fill(ids, dists, nq * k, metric == kern::kL2 ? INFINITY : -INFINITY, s);
+    });
     return;
   }
-  // Operand preparation.  Cosine: unit rows in fp32 (reference normalises
-  // in float32, src/knn.cpp:30-33, even for float16 input, src/utils.h:28).
+  // Operand preparation.  Cosine: unit rows in fp32 (the reference
+  // normalises in float32, src/knn.cpp:30-33, also for float16 input,
+  // src/utils.h:28).  Otherwise the rows are used in place when they are
+  // 16-byte aligned with a row length that is a multiple of 16 bytes, else
+  // through a zero-padded copy.
   const bool cosine = metric == kern::kCosine;
   const bool l2 = metric == kern::kL2;
-  const bool f16_kernel = in.f16 && !cosine;
+  const bool kf16 = in.f16 && !cosine;
+  const int esize = kf16 ? 2 : 4;
+  const int vmul = kf16 ? 8 : 4;
   const void* kbase = in.base;
   const void* kq = in.queries;
+  int kld = d;
   float* bnorm = nullptr;
   float* qnorm = nullptr;
-  float* ub = nullptr;
-  float* uq = nullptr;
+  const int f16 = in.f16 ? 1 : 0;
   if (cosine) {
-    ub = ar.take<float>((size_t)n * d);
-    uq = ar.take<float>((size_t)nq * d);
-    check_hip(kern::launch_prep({in.base, n, d, in.f16, nullptr, ub, nullptr}, s), "prep");
-    check_hip(kern::launch_prep({in.queries, nq, d, in.f16, nullptr, uq, nullptr}, s), "prep");
+    kld = round_up(d, 4);
+    float* nb = ar.take<float>((size_t)n);
+    float* nqv = ar.take<float>((size_t)nq);
+    float* ub = ar.take<float>((size_t)n * kld);
+    float* uq = ar.take<float>((size_t)nq * kld);
+    kern::PrepArgs pb{in.base, n, d, d, f16, nb, nullptr, nullptr, 0, 0};
+    kern::PrepArgs pq{in.queries, nq, d, d, f16, nqv, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+    launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
+    kern::PrepArgs tb{in.base, n, d, d, f16, nullptr, nb, ub, kld, 0};
+    kern::PrepArgs tq{in.queries, nq, d, d, f16, nullptr, nqv, uq, kld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(tb, s); });
+    launch(s, "prep", [&] { return kern::launch_transform(tq, s); });
     kbase = ub;
     kq = uq;
-  } else if (l2) {
-    bnorm = ar.take<float>((size_t)n);
-    qnorm = ar.take<float>((size_t)nq);
-    check_hip(kern::launch_prep({in.base, n, d, in.f16, bnorm, nullptr, nullptr}, s), "prep");
-    check_hip(kern::launch_prep({in.queries, nq, d, in.f16, qnorm, nullptr, nullptr}, s), "prep");
+  } else {
+    if (l2) {
+      bnorm = ar.take<float>((size_t)n);
+      qnorm = ar.take<float>((size_t)nq);
+      kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
+      kern::PrepArgs pq{in.queries, nq, d, d, f16, qnorm, nullptr, nullptr, 0, 0};
+      launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+      launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
+    }
+    const bool aligned = ((uintptr_t)in.base % 16 == 0) && ((uintptr_t)in.queries % 16 == 0);
+    if (!aligned || d % vmul != 0) {
+      kld = round_up(d, vmul);
+      void* pb = ar.take_bytes((size_t)n * kld * esize);
+      void* pq = ar.take_bytes((size_t)nq * kld * esize);
+      kern::PrepArgs tb{in.base, n, d, d, f16, nullptr, nullptr, pb, kld, f16};
+      kern::PrepArgs tq{in.queries, nq, d, d, f16, nullptr, nullptr, pq, kld, f16};
+      launch(s, "prep", [&] { return kern::launch_transform(tb, s); });
+      launch(s, "prep", [&] { return kern::launch_transform(tq, s); });
+      kbase = pb;
+      kq = pq;
+    }
   }
 
   const int T = list_len_float(k);
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
-  if (kern::fused_supported(d, T, f16_kernel) && nq < (int64_t(1) << 31))
+  if (kern::fused_supported(kld, T, kf16) && nq < (int64_t(1) << 31)) {
     plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows);
+    // a split's rows must stay inside one 32-bit buffer range
+    if (plan.ok && (plan.rows_per_split + kern::kTileRows) * kld * esize >= (int64_t(1) << 31))
+      plan.ok = false;
+  }
 
-  // fp32 copies for the exhaustive path (only when it may run)
-  auto fp32_rows = [&](const void* x, int64_t rows, float** out) {
-    if (!in.f16 || cosine) {
-      *out = (float*)x;  // already fp32 (cosine: unit rows)
+  // fp32 rows for the exhaustive path (only when it runs)
+  auto fp32_rows = [&](const void* x, int64_t rows, const float** out) {
+    if (!kf16) {
+      *out = (const float*)x;
       return;
     }
-    *out = ar.take<float>((size_t)rows * d);
-    check_hip(kern::launch_prep({x, rows, d, 1, nullptr, nullptr, *out}, s), "prep");
+    float* p = ar.take<float>((size_t)rows * kld);
+    kern::PrepArgs t{x, rows, kld, kld, 1, nullptr, nullptr, p, kld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(t, s); });
+    *out = p;
   };
 
   if (!plan.ok) {
-    float *eb, *eq;
+    const float *eb, *eq;
     fp32_rows(kbase, n, &eb);
     fp32_rows(kq, nq, &eq);
     std::vector<int> all((size_t)nq);
@@ -316,25 +404,23 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     int* qsel = ar.take<int>((size_t)nq);
     check_hip(hipMemcpyAsync(qsel, all.data(), sizeof(int) * nq, hipMemcpyHostToDevice, s),
               "hipMemcpyAsync");
-    // the host vector must outlive the copy
-    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-    exhaustive_float(ar, s, eb, eq, bnorm, qnorm, n, d, metric, qsel, (int)nq, k, ids, dists);
+    exhaustive_float(ar, s, eb, eq, kld, bnorm, qnorm, n, d, metric, qsel, (int)nq, k, ids,
+                     dists);
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // `all` is released next
     return;
   }
 
   const int nseg = 2 * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
-  const int vmul = f16_kernel ? 8 : 4;
-  const bool aligned = ((uintptr_t)kbase % 16 == 0) && ((uintptr_t)kq % 16 == 0);
-  kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, d, cosine ? kern::kInnerProduct : metric,
-                     plan.rows_per_split, plan.nsplit, T, part,
-                     (d % vmul == 0 && aligned) ? 1 : 0};
-  check_hip(f16_kernel ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s),
-            "fused kernel");
+  kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
+                     plan.rows_per_split, plan.nsplit, T, part};
+  launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
+    return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
+  });
   int* flags = nullptr;
   if (T < k) flags = ar.take<int>((size_t)nq);
   kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};
-  check_hip(kern::launch_merge(ma, s), "merge kernel");
+  launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
   if (T >= k) return;
 
   // k > T: queries whose lists may have dropped a member go exhaustive.
@@ -346,13 +432,13 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   for (int64_t i = 0; i < nq; ++i)
     if (hflags[(size_t)i]) redo.push_back((int)i);
   if (redo.empty()) return;
-  float *eb, *eq;
+  const float *eb, *eq;
   fp32_rows(kbase, n, &eb);
   fp32_rows(kq, nq, &eq);
   int* qsel = ar.take<int>(redo.size());
   check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
             "hipMemcpyAsync");
-  exhaustive_float(ar, s, eb, eq, bnorm, qnorm, n, d, metric, qsel, (int)redo.size(), k,
+  exhaustive_float(ar, s, eb, eq, kld, bnorm, qnorm, n, d, metric, qsel, (int)redo.size(), k,
                    ids, dists);
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
@@ -365,7 +451,7 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   hipStream_t s = ss.stream();
   if (nq == 0) return;
   if (n == 0) {
-    check_hip(kern::launch_fill(ids, dists, nq * k, INFINITY, s), "fill kernel");
+    launch(s, "fill", [&] { return kern::launch_fill(ids, dists, nq * k, INFINITY, s); });
     return;
   }
   const int W = (nbytes + 3) / 4;
@@ -377,17 +463,17 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   const int wstride = plan.ok ? Wp : W;
   uint32_t* bw = ar.take<uint32_t>((size_t)n * wstride);
   uint32_t* qw = ar.take<uint32_t>((size_t)nq * wstride);
-  check_hip(kern::launch_pack({rows, n, nbytes, bw, wstride}, s), "pack kernel");
-  check_hip(kern::launch_pack({queries, nq, nbytes, qw, wstride}, s), "pack kernel");
+  launch(s, "pack", [&] { return kern::launch_pack({rows, n, nbytes, bw, wstride}, s); });
+  launch(s, "pack", [&] { return kern::launch_pack({queries, nq, nbytes, qw, wstride}, s); });
 
   std::vector<int> redo;
   if (plan.ok) {
     uint64_t* part = ar.take<uint64_t>((size_t)nq * plan.nsplit * T);
     kern::HammingArgs ha{bw, qw, n, (int)nq, Wp, plan.rows_per_split, plan.nsplit, T, part};
-    check_hip(kern::launch_hamming(ha, s), "hamming kernel");
+    launch(s, "hamming", [&] { return kern::launch_hamming(ha, s); });
     int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
     kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags};
-    check_hip(kern::launch_merge(ma, s), "merge kernel");
+    launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     if (T >= k) return;
     std::vector<int> hflags((size_t)nq);
     check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
@@ -409,9 +495,9 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   for (int64_t r0 = 0; r0 < rcount; r0 += per_block) {
     const int cnt = (int)std::min<int64_t>(per_block, rcount - r0);
     kern::HammingScoresArgs hs{bw, qw, qsel + r0, n, cnt, wstride, S};
-    check_hip(kern::launch_hamming_scores(hs, s), "hamming scores kernel");
+    launch(s, "hamming_scores", [&] { return kern::launch_hamming_scores(hs, s); });
     kern::SelectArgs se{S, n, cnt, k, qsel + r0, kern::kL2, nullptr, 1, ids, dists};
-    check_hip(kern::launch_select(se, s), "select kernel");
+    launch(s, "select", [&] { return kern::launch_select(se, s); });
   }
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
@@ -494,7 +580,7 @@ void self_graph(Session& ss, const void* rows, int64_t n, int d, bool f16, int k
   float_knn(ss, {rows, rows, n, n, d, f16}, kin, metric, tid, tds);
   float* out_d = dists ? dists : ar.take<float>((size_t)n * k);
   kern::SelfDropArgs sd{tid, tds, n, kin, k, metric, ids, out_d};
-  check_hip(kern::launch_self_drop(sd, ss.stream()), "self drop kernel");
+  launch(ss.stream(), "self_drop", [&] { return kern::launch_self_drop(sd, ss.stream()); });
 }
 
 }  // namespace
@@ -596,5 +682,25 @@ void release_workspace() {
 }
 
 const char* version() { return "0.16.1-mi355x"; }
+
+void profile(bool enable) {
+  std::lock_guard<std::mutex> g(g_prof_mutex);
+  prof_collect();
+  g_prof_totals.clear();
+  g_prof_on = enable;
+}
+
+std::string profile_report() {
+  std::lock_guard<std::mutex> g(g_prof_mutex);
+  prof_collect();
+  std::string out;
+  char line[160];
+  for (auto& [name, t] : g_prof_totals) {
+    snprintf(line, sizeof line, "%s %lld %.6f\n", name.c_str(), (long long)t.first, t.second);
+    out += line;
+  }
+  g_prof_totals.clear();
+  return out;
+}
 
 }  // namespace mlxvs

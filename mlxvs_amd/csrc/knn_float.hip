@@ -6,8 +6,8 @@
 // with a radix-select Metal kernel per query row (src/kernels.h:37-229),
 // synchronising with the host after every tile (:120).  Here instead:
 //
-//  * prep_rows: one pass per input computing |x|^2 (L2), unit rows (cosine)
-//    or an fp32 copy, in the summation order of the CPU restatement.
+//  * row_norms / rows_transform: |x|^2 in the summation order of the CPU
+//    restatement (L2, cosine), unit rows (cosine), padded or fp32 copies.
 //  * fused_*: one kernel streams 32-row base tiles through LDS and multiplies
 //    them against register-resident query fragments on the MFMA units; the
 //    L2 epilogue and a per-lane top-T list live in registers, so the score
@@ -22,6 +22,8 @@
 //    k best of each row.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+
+#include <type_traits>
 
 #include "knn_kernels.h"
 #include "topk_common.h"
@@ -39,63 +41,102 @@ __device__ __forceinline__ float load_elem(const void* x, int f16, int64_t i) {
   return ((const float*)x)[i];
 }
 
-// One thread per row.  Sum of squares with eight interleaved partial sums
-// (element j into sum j % 8) added pairwise, as oracle/knn_oracle.c dot8,
-// so norms and unit rows are bit-identical to the CPU restatement.
-__global__ __launch_bounds__(256) void prep_rows_kernel(PrepArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= a.n) return;
-  const int d = a.d;
-  const int64_t o = r * d;
+// Squared norms of 256 rows per block.  The block stages [256 rows x 32
+// dims] in LDS with coalesced reads (32 lanes per 128-byte row segment), then
+// every thread sums its own row: element j into partial sum j % 8, partial
+// sums added pairwise -- the order of oracle/knn_oracle.c dot8, so the norms
+// are bit-identical to the CPU restatement's.
+__global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
+  __shared__ float sh[256 * 33];  // odd stride: row r, dim j hits bank (r + j) % 32
+  const int tid = threadIdx.x;
+  const int64_t row0 = (int64_t)blockIdx.x * 256;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int j = 0; j < d; j += 8) {
+  for (int c0 = 0; c0 < a.d; c0 += 32) {
+    for (int e = tid; e < 256 * 32; e += 256) {
+      const int r = e >> 5, j = e & 31;
+      const int64_t row = row0 + r;
+      sh[r * 33 + j] = (row < a.n && c0 + j < a.d) ? load_elem(a.x, a.f16, row * a.ld + c0 + j) : 0.0f;
+    }
+    __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      if (j + t < d) {
-        float v = load_elem(a.x, a.f16, o + j + t);
-        acc[t] += v * v;
+    for (int j8 = 0; j8 < 32; j8 += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (c0 + j8 + u < a.d) {
+          const float v = sh[tid * 33 + j8 + u];
+          acc[u] += v * v;
+        }
       }
     }
+    __syncthreads();
   }
-  float s01 = acc[0] + acc[1], s23 = acc[2] + acc[3];
-  float s45 = acc[4] + acc[5], s67 = acc[6] + acc[7];
-  float ss = (s01 + s23) + (s45 + s67);
-  if (a.norm) a.norm[r] = ss;
-  if (a.unit) {
-    // reference src/knn.cpp:30-33: x / max(sqrt(sum x^2), 1e-30)
-    float nrm = sqrtf(ss);
-    float den = nrm > 1e-30f ? nrm : 1e-30f;
-    for (int j = 0; j < d; ++j) a.unit[o + j] = load_elem(a.x, a.f16, o + j) / den;
-  }
-  if (a.upcast) {
-    for (int j = 0; j < d; ++j) a.upcast[o + j] = load_elem(a.x, a.f16, o + j);
+  if (row0 + tid < a.n) {
+    float s01 = acc[0] + acc[1], s23 = acc[2] + acc[3];
+    float s45 = acc[4] + acc[5], s67 = acc[6] + acc[7];
+    a.norm[row0 + tid] = (s01 + s23) + (s45 + s67);
   }
 }
 
-// ---- fused fp32 MFMA distance + per-lane top-T ------------------------------
+// Element-wise row copy into an [n, out_ld] buffer, zero-padded past d:
+// fp32 or binary16 out, optionally divided by max(sqrt(norm), 1e-30)
+// (unit rows, reference src/knn.cpp:30-33).
+__global__ __launch_bounds__(256) void rows_transform_kernel(PrepArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.n * a.out_ld) return;
+  const int64_t r = e / a.out_ld;
+  const int j = (int)(e % a.out_ld);
+  float v = j < a.d ? load_elem(a.x, a.f16, r * a.ld + j) : 0.0f;
+  if (a.unit_norms) {
+    const float nrm = sqrtf(a.unit_norms[r]);
+    v = v / (nrm > 1e-30f ? nrm : 1e-30f);
+  }
+  if (a.out_f16)
+    ((_Float16*)a.out)[e] = (_Float16)v;
+  else
+    ((float*)a.out)[e] = v;
+}
+
+// ---- fused MFMA distance + per-lane top-T -------------------------------------
 //
-// v_mfma_f32_32x32x2_f32 layout (checked on gfx950): lane l supplies
+// fp32: v_mfma_f32_32x32x2_f32 (checked on gfx950): lane l supplies
 // A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator register i of lane l
-// holds D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].  A = 32 base rows, B = the
-// wavefront's 32 queries.  The K dimension is permuted so that lane half h
-// owns the dims [h DH, h DH + DH): step s multiplies dim s (half 0) and
-// dim DH + s (half 1), so a lane reads 4 consecutive dims of its base row
-// with one ds_read_b128 and holds its query's DH dims in registers.  A lane
-// therefore sees 16 base rows of every tile for its own query.
+// holds D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
+// fp16: v_mfma_f32_32x32x16_f16 (checked on gfx950): lane l supplies the
+// eight halves A[l % 32][8 (l / 32) .. +7] and B[8 (l / 32) .. +7][l % 32];
+// accumulators as above.  Products of binary16 values are exact in fp32.
+//
+// A = 32 base rows of the current tile, B = the wavefront's 32 queries.  The
+// K dimension is permuted so that lane half h owns the dims
+// [h DH, h DH + DH): per 16-byte chunk of its base row a lane issues 4 fp32
+// (one dim each) or 1 fp16 (eight dims) MFMAs, and its query's DH dims stay
+// in registers for the whole kernel.  Output register i of lane l is the
+// score of the lane's own query (l % 32) against tile row
+// 8 (i / 4) + 4 (l / 32) + i % 4, so every lane keeps a private sorted top-T
+// list of its query over the rows it sees (one "segment" per lane half and
+// split).
+//
+// Streaming: tile t + 1 is fetched with buffer loads into registers while the
+// MFMAs of tile t run (scheduling barriers keep the loads ahead of the MFMA
+// chain), then written to the other LDS buffer; one barrier per tile.  Rows
+// past the split and dims past ld read as zero through the buffer range check.
 
-// Workgroups per CU the register budget allows: the d = 256 instance keeps
-// 128 query registers per lane and needs the full 512-register file.
-template <int DH>
-constexpr int fused_f32_min_blocks() { return DH >= 128 ? 1 : 2; }
+template <bool F16, int DH>
+constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
-template <int DH, int T>
-__global__ __launch_bounds__(256, fused_f32_min_blocks<DH>()) void fused_f32_kernel(FusedArgs a) {
-  constexpr int D = 2 * DH;
-  constexpr int STRIDE = D + 4;  // floats per LDS row: 8 rows hit distinct bank quads
-  constexpr int F4_ROW = D / 4;
-  constexpr int F4_TILE = kTileRows * F4_ROW;
-  constexpr int NPF = (F4_TILE + 255) / 256;
-  __shared__ __align__(16) float tile[2][kTileRows * STRIDE];
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool F16, int DH, int T>
+__global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kernel(FusedArgs a) {
+  using E = typename std::conditional<F16, _Float16, float>::type;
+  constexpr int EPV = F16 ? 8 : 4;    // elements per 16-byte vector
+  constexpr int D = 2 * DH;           // padded dims of an LDS row
+  constexpr int VROW = D / EPV;       // 16-byte vectors per LDS row
+  constexpr int VTILE = kTileRows * VROW;
+  constexpr int NPF = (VTILE + 255) / 256;
+  constexpr int STRIDE = D + EPV;     // 16-byte pad: 8 rows hit distinct bank quads
+  constexpr int QV = DH / EPV;        // query vectors per lane
+  __shared__ __align__(16) E tile[2][kTileRows * STRIDE];
   __shared__ __align__(16) float tnorm[2][kTileRows];
 
   const int tid = threadIdx.x;
@@ -106,64 +147,75 @@ __global__ __launch_bounds__(256, fused_f32_min_blocks<DH>()) void fused_f32_ker
   const int q = q0w + col;
   const bool wave_on = q0w < a.nq;
   const bool qvalid = q < a.nq;
-  const int d = a.d;
-  const bool vec = a.vec != 0;
+  const int ld = a.ld;
   const bool l2 = a.metric == kL2;
-  const float* base = (const float*)a.base;
 
   const int64_t r0 = (int64_t)split * a.rows_per_split;
   const int64_t r1 = min(a.n, r0 + a.rows_per_split);
-  const int64_t ntiles = r1 > r0 ? (r1 - r0 + kTileRows - 1) / kTileRows : 0;
+  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
 
-  float qf[DH];
-  {
-    const float* qr = (const float*)a.queries + (int64_t)(qvalid ? q : 0) * d;
+  // buffer resources over this split's rows and norms
+  const E* sbase = (const E*)a.base + r0 * ld;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)sbase, (short)0, nrows * ld * (int)sizeof(E), 0x00020000);
+  const float* snorm = l2 ? a.bnorm + r0 : (const float*)a.base;
+  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)snorm, (short)0, l2 ? nrows * 4 : 0, 0x00020000);
+  // Byte offsets of this thread's 16-byte vectors in the next tile to
+  // fetch.  They are carried from tile to tile (+tile_bytes), so they stay
+  // live across the MFMA chain and never share registers with the
+  // accumulators (a VMEM address register overwritten by an MFMA forces a
+  // wait for the load).  Vectors past ld start at 2^31, beyond every range
+  // (ranges are < 2^31 bytes), and read zero.
+  const uint32_t tile_bytes = kTileRows * ld * (uint32_t)sizeof(E);
+  uint32_t voff[NPF];
 #pragma unroll
-    for (int s = 0; s < DH; ++s) {
-      const int dim = h * DH + s;
-      qf[s] = (qvalid && dim < d) ? qr[dim] : 0.0f;
+  for (int j = 0; j < NPF; ++j) {
+    const int e = tid + 256 * j;
+    const int r = e / VROW, c = (e % VROW) * EPV;
+    voff[j] = (e < VTILE && c < ld) ? (uint32_t)((r * ld + c) * (int)sizeof(E)) : 0x80000000u;
+  }
+  uint32_t noff = tid * 4u;  // norm word of this thread (threads < 32)
+
+  // the lane's query dims [h DH, h DH + DH): 16-byte buffer loads of the
+  // query row, zero past ld and for lanes without a query
+  typedef E vecq __attribute__((ext_vector_type(EPV)));
+  vecq qf[QV];
+  {
+    const E* qr = (const E*)a.queries + (int64_t)(qvalid ? q : 0) * ld;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)qr, (short)0, qvalid ? ld * (int)sizeof(E) : 0, 0x00020000);
+#pragma unroll
+    for (int v = 0; v < QV; ++v) {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (h * DH + v * EPV) * (int)sizeof(E), 0, 0);
+      qf[v] = __builtin_bit_cast(vecq, w);
     }
   }
 
-  float4 pf[NPF];
-  float pn = 0.0f;
-  auto load_tile = [&](int64_t t0) {
+  // raw bits: the tile and norm words are moved, not converted
+  u32x4 pf[NPF];
+  uint32_t pn = 0;
+  auto issue_loads = [&]() {
 #pragma unroll
     for (int j = 0; j < NPF; ++j) {
-      const int e = tid + 256 * j;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (e < F4_TILE) {
-        const int r = e / F4_ROW, c = (e % F4_ROW) * 4;
-        const int64_t row = t0 + r;
-        if (row < r1 && c < d) {
-          const float* src = base + row * d + c;
-          if (vec) {
-            v = *(const float4*)src;
-          } else {
-            v.x = src[0];
-            v.y = c + 1 < d ? src[1] : 0.f;
-            v.z = c + 2 < d ? src[2] : 0.f;
-            v.w = c + 3 < d ? src[3] : 0.f;
-          }
-        }
-      }
-      pf[j] = v;
+      pf[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, voff[j], 0, 0);
+      voff[j] += tile_bytes;
     }
-    if (l2 && tid < kTileRows) {
-      const int64_t row = t0 + tid;
-      pn = row < r1 ? a.bnorm[row] : 0.0f;
-    }
+    if (l2 && tid < kTileRows) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+    noff += kTileRows * 4;
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NPF; ++j) {
       const int e = tid + 256 * j;
-      if (e < F4_TILE) {
-        const int r = e / F4_ROW, c = (e % F4_ROW) * 4;
-        *(float4*)&tile[buf][r * STRIDE + c] = pf[j];
+      if (e < VTILE) {
+        const int r = e / VROW, c = (e % VROW) * EPV;
+        *(u32x4*)&tile[buf][r * STRIDE + c] = pf[j];
       }
     }
-    if (l2 && tid < kTileRows) tnorm[buf][tid] = pn;
+    if (l2 && tid < kTileRows) tnorm[buf][tid] = __uint_as_float(pn);
   };
 
   uint64_t L[T];
@@ -172,41 +224,49 @@ __global__ __launch_bounds__(256, fused_f32_min_blocks<DH>()) void fused_f32_ker
   float thr = score_of_key(0u);  // NaN: every candidate passes until full
 
   if (ntiles > 0) {
-    load_tile(r0);
+    issue_loads();
     store_tile(0);
   }
+  // nothing may be outstanding at the loop head: the query fragments are
+  // read in every iteration, and a pending prologue load would otherwise
+  // make each iteration wait for its own tile prefetch as well
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const int buf = (int)(t & 1);
-    const int64_t t0 = r0 + t * kTileRows;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
     const bool more = t + 1 < ntiles;
-    if (more) load_tile(t0 + kTileRows);
+    if (more) issue_loads();
+    __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
       floatx16 acc;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-      const float* arow = &tile[buf][col * STRIDE + h * DH];
+      const E* arow = &tile[buf][col * STRIDE + h * DH];
 #pragma unroll
-      for (int s = 0; s < DH; s += 4) {
-        const float4 av = *(const float4*)(arow + s);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qf[s + 0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qf[s + 1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qf[s + 2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qf[s + 3], acc, 0, 0, 0);
+      for (int v = 0; v < QV; ++v) {
+        if constexpr (F16) {
+          const halfx8 av = *(const halfx8*)(arow + 8 * v);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[v], acc, 0, 0, 0);
+        } else {
+          const floatx4 av = *(const floatx4*)(arow + 4 * v);
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], qf[v][0], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], qf[v][1], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[2], qf[v][2], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], qf[v][3], acc, 0, 0, 0);
+        }
       }
       // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2
       float sc[16];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float4 nb = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (l2) nb = *(const float4*)&tnorm[buf][8 * j + 4 * h];
-        sc[4 * j + 0] = l2 ? 2.0f * acc[4 * j + 0] - nb.x : acc[4 * j + 0];
-        sc[4 * j + 1] = l2 ? 2.0f * acc[4 * j + 1] - nb.y : acc[4 * j + 1];
-        sc[4 * j + 2] = l2 ? 2.0f * acc[4 * j + 2] - nb.z : acc[4 * j + 2];
-        sc[4 * j + 3] = l2 ? 2.0f * acc[4 * j + 3] - nb.w : acc[4 * j + 3];
+        floatx4 nb = {0.f, 0.f, 0.f, 0.f};
+        if (l2) nb = *(const floatx4*)&tnorm[buf][8 * j + 4 * h];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          sc[4 * j + u] = l2 ? 2.0f * acc[4 * j + u] - nb[u] : acc[4 * j + u];
       }
-      const int64_t lim = r1 - t0;
+      const int lim = nrows - t * kTileRows;
       bool any = false;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -214,171 +274,18 @@ __global__ __launch_bounds__(256, fused_f32_min_blocks<DH>()) void fused_f32_ker
         any |= (m < lim) & !(sc[i] < thr);
       }
       if (any) {
+        const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int m = 8 * (i >> 2) + 4 * h + (i & 3);
           if (m < lim && !(sc[i] < thr)) {
-            list_insert<T>(L, rank_of(sc[i], (uint32_t)(t0 + m)));
+            list_insert<T>(L, rank_of(sc[i], id0 + m));
             thr = score_of_key((uint32_t)(L[T - 1] >> 32));
           }
         }
       }
     }
-    if (more) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (qvalid) {
-    uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
-#pragma unroll
-    for (int i = 0; i < T; ++i) dst[i] = L[i];
-  }
-}
-
-// ---- fused fp16 MFMA (fp32 accumulate) --------------------------------------
-//
-// v_mfma_f32_32x32x16_f16 (checked on gfx950): lane l supplies the eight
-// halves A[l % 32][8 (l / 32) .. +7] and B[8 (l / 32) .. +7][l % 32];
-// accumulators as the fp32 instruction.  K permutation: lane half h owns the
-// dims [h DH, h DH + DH); step s takes dims h DH + 8 s .. +7.  Products of
-// binary16 values are exact in fp32.
-
-template <int DH, int T>
-__global__ __launch_bounds__(256, 2) void fused_f16_kernel(FusedArgs a) {
-  constexpr int D = 2 * DH;
-  constexpr int STRIDE = D + 8;  // halves per LDS row (16-byte pad)
-  constexpr int V_ROW = D / 8;   // 16-byte vectors per row
-  constexpr int V_TILE = kTileRows * V_ROW;
-  constexpr int NPF = (V_TILE + 255) / 256;
-  constexpr int QV = DH / 8;     // 16-byte query vectors per lane
-  __shared__ __align__(16) _Float16 tile[2][kTileRows * STRIDE];
-  __shared__ __align__(16) float tnorm[2][kTileRows];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int h = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x;
-  const int q0w = blockIdx.y * kQueriesPerBlock + wave * 32;
-  const int q = q0w + col;
-  const bool wave_on = q0w < a.nq;
-  const bool qvalid = q < a.nq;
-  const int d = a.d;
-  const bool vec = a.vec != 0;
-  const bool l2 = a.metric == kL2;
-  const _Float16* base = (const _Float16*)a.base;
-
-  const int64_t r0 = (int64_t)split * a.rows_per_split;
-  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
-  const int64_t ntiles = r1 > r0 ? (r1 - r0 + kTileRows - 1) / kTileRows : 0;
-
-  halfx8 qf[QV];
-  {
-    const _Float16* qr = (const _Float16*)a.queries + (int64_t)(qvalid ? q : 0) * d;
-#pragma unroll
-    for (int v = 0; v < QV; ++v) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int dim = h * DH + 8 * v + e;
-        qf[v][e] = (qvalid && dim < d) ? qr[dim] : (_Float16)0.0f;
-      }
-    }
-  }
-
-  uint4 pf[NPF];
-  float pn = 0.0f;
-  auto load_tile = [&](int64_t t0) {
-#pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-      const int e = tid + 256 * j;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (e < V_TILE) {
-        const int r = e / V_ROW, c = (e % V_ROW) * 8;
-        const int64_t row = t0 + r;
-        if (row < r1 && c < d) {
-          const _Float16* src = base + row * d + c;
-          if (vec) {
-            v = *(const uint4*)src;
-          } else {
-            _Float16 tmp[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) tmp[u] = c + u < d ? src[u] : (_Float16)0.0f;
-            v = *(const uint4*)tmp;
-          }
-        }
-      }
-      pf[j] = v;
-    }
-    if (l2 && tid < kTileRows) {
-      const int64_t row = t0 + tid;
-      pn = row < r1 ? a.bnorm[row] : 0.0f;
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-      const int e = tid + 256 * j;
-      if (e < V_TILE) {
-        const int r = e / V_ROW, c = (e % V_ROW) * 8;
-        *(uint4*)&tile[buf][r * STRIDE + c] = pf[j];
-      }
-    }
-    if (l2 && tid < kTileRows) tnorm[buf][tid] = pn;
-  };
-
-  uint64_t L[T];
-#pragma unroll
-  for (int i = 0; i < T; ++i) L[i] = 0;
-  float thr = score_of_key(0u);
-
-  if (ntiles > 0) {
-    load_tile(r0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const int buf = (int)(t & 1);
-    const int64_t t0 = r0 + t * kTileRows;
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t0 + kTileRows);
-    if (wave_on) {
-      floatx16 acc;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-      const _Float16* arow = &tile[buf][col * STRIDE + h * DH];
-#pragma unroll
-      for (int v = 0; v < QV; ++v) {
-        const halfx8 av = *(const halfx8*)(arow + 8 * v);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[v], acc, 0, 0, 0);
-      }
-      float sc[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float4 nb = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (l2) nb = *(const float4*)&tnorm[buf][8 * j + 4 * h];
-        sc[4 * j + 0] = l2 ? 2.0f * acc[4 * j + 0] - nb.x : acc[4 * j + 0];
-        sc[4 * j + 1] = l2 ? 2.0f * acc[4 * j + 1] - nb.y : acc[4 * j + 1];
-        sc[4 * j + 2] = l2 ? 2.0f * acc[4 * j + 2] - nb.z : acc[4 * j + 2];
-        sc[4 * j + 3] = l2 ? 2.0f * acc[4 * j + 3] - nb.w : acc[4 * j + 3];
-      }
-      const int64_t lim = r1 - t0;
-      bool any = false;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-        any |= (m < lim) & !(sc[i] < thr);
-      }
-      if (any) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-          if (m < lim && !(sc[i] < thr)) {
-            list_insert<T>(L, rank_of(sc[i], (uint32_t)(t0 + m)));
-            thr = score_of_key((uint32_t)(L[T - 1] >> 32));
-          }
-        }
-      }
-    }
+    __builtin_amdgcn_sched_barrier(0);
     if (more) store_tile(buf ^ 1);
     __syncthreads();
   }
@@ -434,9 +341,9 @@ __global__ __launch_bounds__(256) void scores_kernel(ScoresArgs a) {
       const int kk = e & 15, ii = e >> 4;
       const int i = i0 + ii, dim = k0 + kk;
       As[kk][ii] = (i < a.rows && dim < a.d)
-                       ? a.queries[(int64_t)a.qsel[i] * a.d + dim] : 0.0f;
+                       ? a.queries[(int64_t)a.qsel[i] * a.ld + dim] : 0.0f;
       const int64_t j = j0 + ii;
-      Bs[kk][ii] = (j < a.n && dim < a.d) ? a.base[j * a.d + dim] : 0.0f;
+      Bs[kk][ii] = (j < a.n && dim < a.d) ? a.base[j * a.ld + dim] : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -582,88 +489,72 @@ __global__ void self_drop_kernel(SelfDropArgs a) {
   }
 }
 
-template <int DH, int T>
-hipError_t launch_f32_inst(const FusedArgs& a, hipStream_t s) {
+template <bool F16, int DH, int T>
+hipError_t launch_inst(const FusedArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, (a.nq + kQueriesPerBlock - 1) / kQueriesPerBlock);
-  hipLaunchKernelGGL((fused_f32_kernel<DH, T>), grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((fused_kernel<F16, DH, T>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
-template <int DH, int T>
-hipError_t launch_f16_inst(const FusedArgs& a, hipStream_t s) {
-  dim3 grid(a.nsplit, (a.nq + kQueriesPerBlock - 1) / kQueriesPerBlock);
-  hipLaunchKernelGGL((fused_f16_kernel<DH, T>), grid, dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
-int dh_f32(int d) {
-  if (d <= 32) return 16;
-  if (d <= 64) return 32;
-  if (d <= 128) return 64;
-  if (d <= 256) return 128;
-  return 0;
-}
-
-int dh_f16(int d) {
-  if (d <= 64) return 32;
-  if (d <= 128) return 64;
-  if (d <= 256) return 128;
+// Instances: padded row length 2 DH >= ld; list lengths 4, 8, 10, 16
+// (k <= T is exact, k > T goes through the merge's check).
+int dh_for(int ld, bool f16) {
+  if (!f16 && ld <= 32) return 16;
+  if (ld <= 64) return 32;
+  if (ld <= 128) return 64;
+  if (ld <= 256) return 128;
   return 0;
 }
 
 bool t_ok(int T) { return T == 4 || T == 8 || T == 10 || T == 16; }
 
-template <int DH>
-hipError_t dispatch_f32_t(const FusedArgs& a, hipStream_t s) {
+template <bool F16, int DH>
+hipError_t dispatch_t(const FusedArgs& a, hipStream_t s) {
   switch (a.T) {
-    case 4: return launch_f32_inst<DH, 4>(a, s);
-    case 8: return launch_f32_inst<DH, 8>(a, s);
-    case 10: return launch_f32_inst<DH, 10>(a, s);
-    case 16: return launch_f32_inst<DH, 16>(a, s);
-  }
-  return hipErrorInvalidValue;
-}
-
-template <int DH>
-hipError_t dispatch_f16_t(const FusedArgs& a, hipStream_t s) {
-  switch (a.T) {
-    case 4: return launch_f16_inst<DH, 4>(a, s);
-    case 8: return launch_f16_inst<DH, 8>(a, s);
-    case 10: return launch_f16_inst<DH, 10>(a, s);
-    case 16: return launch_f16_inst<DH, 16>(a, s);
+    case 4: return launch_inst<F16, DH, 4>(a, s);
+    case 8: return launch_inst<F16, DH, 8>(a, s);
+    case 10: return launch_inst<F16, DH, 10>(a, s);
+    case 16: return launch_inst<F16, DH, 16>(a, s);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-bool fused_supported(int d, int T, bool f16) {
-  if (!t_ok(T) || d < 1) return false;
-  return f16 ? dh_f16(d) != 0 : dh_f32(d) != 0;
+bool fused_supported(int ld, int T, bool f16) {
+  return t_ok(T) && ld >= 1 && dh_for(ld, f16) != 0;
 }
 
-hipError_t launch_prep(const PrepArgs& a, hipStream_t s) {
+hipError_t launch_norms(const PrepArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   const int64_t blocks = (a.n + 255) / 256;
-  hipLaunchKernelGGL(prep_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_transform(const PrepArgs& a, hipStream_t s) {
+  const int64_t total = a.n * a.out_ld;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rows_transform_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                     0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s) {
-  switch (dh_f32(a.d)) {
-    case 16: return dispatch_f32_t<16>(a, s);
-    case 32: return dispatch_f32_t<32>(a, s);
-    case 64: return dispatch_f32_t<64>(a, s);
-    case 128: return dispatch_f32_t<128>(a, s);
+  switch (dh_for(a.ld, false)) {
+    case 16: return dispatch_t<false, 16>(a, s);
+    case 32: return dispatch_t<false, 32>(a, s);
+    case 64: return dispatch_t<false, 64>(a, s);
+    case 128: return dispatch_t<false, 128>(a, s);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s) {
-  switch (dh_f16(a.d)) {
-    case 32: return dispatch_f16_t<32>(a, s);
-    case 64: return dispatch_f16_t<64>(a, s);
-    case 128: return dispatch_f16_t<128>(a, s);
+  switch (dh_for(a.ld, true)) {
+    case 32: return dispatch_t<true, 32>(a, s);
+    case 64: return dispatch_t<true, 64>(a, s);
+    case 128: return dispatch_t<true, 128>(a, s);
   }
   return hipErrorInvalidValue;
 }

@@ -24,17 +24,21 @@ constexpr int kMaxMergeCandidates = 4096;
 // Largest k of the exact selection.
 constexpr int kMaxK = 256;
 
-// Row preparation: squared norms (L2), unit rows (cosine), fp16 -> fp32.
+// Row preparation.
 struct PrepArgs {
-  const void* x;   // rows [n, d], fp32 or binary16
+  const void* x;            // rows [n, ld], first d used; fp32 or binary16
   int64_t n;
   int d;
-  int f16;         // x holds binary16
-  float* norm;     // out: sum of squares [n] (may be null)
-  float* unit;     // out: x / max(|x|, 1e-30) as fp32 [n, d] (may be null)
-  float* upcast;   // out: x as fp32 [n, d] (may be null)
+  int ld;
+  int f16;                  // x holds binary16
+  float* norm;              // launch_norms: out sum of squares [n]
+  const float* unit_norms;  // launch_transform: divide rows by max(sqrt(norm), 1e-30)
+  void* out;                // launch_transform: out rows [n, out_ld], zero past d
+  int out_ld;
+  int out_f16;              // out is binary16 (else fp32)
 };
-hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
+hipError_t launch_norms(const PrepArgs& a, hipStream_t s);
+hipError_t launch_transform(const PrepArgs& a, hipStream_t s);
 
 // Fused distance + per-lane top-T selection.
 //   grid (nsplit, ceil(nq / 128)); workgroup 256 threads.
@@ -43,24 +47,23 @@ hipError_t launch_prep(const PrepArgs& a, hipStream_t s);
 // has bit 2 equal to l/32 ("segment" 2*split + l/32).  Output part
 // [nq][nseg = 2*nsplit][T] of ranks (see rank_of); 0 marks an empty slot.
 struct FusedArgs {
-  const void* base;      // [n, d] fp32 or binary16 (prepared: unit rows for cosine)
-  const void* queries;   // [nq, d]
+  const void* base;      // [n, ld] fp32 or binary16, 16-byte aligned, ld a multiple
+                         // of 4 (fp32) / 8 (fp16); zero past the real dims
+  const void* queries;   // [nq, ld]
   const float* bnorm;    // [n] squared norms (L2), else null
   int64_t n;
   int nq;
-  int d;
+  int ld;
   int metric;            // kInnerProduct / kL2 / kCosine (cosine == IP on unit rows)
   int64_t rows_per_split;
   int nsplit;
   int T;                 // list length per lane
   uint64_t* part;        // [nq][2*nsplit][T]
-  int vec;               // rows may be read as 16-byte vectors (d multiple of
-                         // 4 (fp32) / 8 (fp16) and 16-byte aligned pointers)
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
-// true when the fused kernels have an instance for (d, T)
-bool fused_supported(int d, int T, bool f16);
+// true when the fused kernels have an instance for (ld, T)
+bool fused_supported(int ld, int T, bool f16);
 
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.
@@ -91,6 +94,7 @@ struct ScoresArgs {
   int64_t n;
   int rows;
   int d;
+  int ld;                // row stride of base and queries
   int metric;
   float* S;              // [rows][n]
 };
