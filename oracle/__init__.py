@@ -42,12 +42,14 @@ def lib():
         vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         L.oracle_knn_f32.argtypes = [vp, i64, vp, i64, ci, ci, ci, ci, vp, vp]
         L.oracle_self_graph_f32.argtypes = [vp, i64, ci, ci, ci, ci, vp, vp]
+        L.oracle_self_graph_rows.argtypes = [vp, i64, ci, ci, ci, ci, i64, vp, vp]
         L.oracle_hamming.argtypes = [vp, i64, vp, i64, ci, ci, ci, vp, vp]
         L.oracle_f16_to_f32.argtypes = [vp, i64, vp]
         L.oracle_pack_words.argtypes = [vp, i64, ci, vp]
         L.oracle_key.argtypes = [ctypes.c_float]
         L.oracle_key.restype = ctypes.c_uint32
-        for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_hamming",
+        for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_self_graph_rows",
+                  "oracle_hamming",
                   "oracle_f16_to_f32", "oracle_pack_words"):
             getattr(L, f).restype = ci
         _lib = L
@@ -95,6 +97,18 @@ def self_graph(rows, k, metric="l2", nthreads=None):
                                      nthreads or threads(), _p(ids), _p(dist))
     if rc:
         raise ValueError(f"oracle_self_graph_f32 rejected the arguments ({rc})")
+    return ids, dist
+
+
+def self_graph_rows(rows, k, first, metric="l2", nthreads=None):
+    """self_graph for the first `first` rows only (all rows are candidates)."""
+    x = np.ascontiguousarray(rows, dtype=np.float32)
+    ids = np.empty((first, k), np.int32)
+    dist = np.empty((first, k), np.float32)
+    rc = lib().oracle_self_graph_rows(_p(x), x.shape[0], x.shape[1], k, _m(metric),
+                                      nthreads or threads(), first, _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_self_graph_rows rejected the arguments ({rc})")
     return ids, dist
 
 

@@ -321,25 +321,26 @@ static int dist_cmp_asc(const void* pa, const void* pb) {
 }
 
 /*
- * The k-NN graph of x [n, d] against itself: brute force with k + 1
- * neighbours (src/all_neighbors.cpp:259-260), then merge_lists
- * (src/all_neighbors.cpp:56-95): drop -1 and the row itself, order by
- * nearness (L2 ascending distance, otherwise descending similarity; equal
- * values by lowest id), keep k, pad -1 and +inf (L2) / -inf.
+ * The k-NN graph of x [n, d] against itself, for its first `rows` rows:
+ * brute force with k + 1 neighbours (src/all_neighbors.cpp:259-260), then
+ * merge_lists (src/all_neighbors.cpp:56-95): drop -1 and the row itself,
+ * order by nearness (L2 ascending distance, otherwise descending similarity;
+ * equal values by lowest id), keep k, pad -1 and +inf (L2) / -inf.
  */
-int oracle_self_graph_f32(const float* x, int64_t n, int d, int k, int metric,
-                          int threads, int32_t* ids, float* dists) {
-  if (k < 1 || k > 255 || n < 2 || d < 1 || metric < 0 || metric > 2)
+int oracle_self_graph_rows(const float* x, int64_t n, int d, int k, int metric,
+                           int threads, int64_t rows, int32_t* ids, float* dists) {
+  if (k < 1 || k > 255 || n < 2 || d < 1 || metric < 0 || metric > 2 ||
+      rows < 0 || rows > n)
     return ORACLE_EINVAL;
   int kk = (int)(k + 1 < n ? k + 1 : n);
-  int32_t* tid = (int32_t*)malloc(sizeof(int32_t) * (size_t)n * kk);
-  float* tds = (float*)malloc(sizeof(float) * (size_t)n * kk);
+  int32_t* tid = (int32_t*)malloc(sizeof(int32_t) * (size_t)(rows ? rows : 1) * kk);
+  float* tds = (float*)malloc(sizeof(float) * (size_t)(rows ? rows : 1) * kk);
   dpair_t* buf = (dpair_t*)malloc(sizeof(dpair_t) * (size_t)kk);
   if (!tid || !tds || !buf) { free(tid); free(tds); free(buf); return ORACLE_ENOMEM; }
-  int rc = oracle_knn_f32(x, n, x, n, d, kk, metric, threads, tid, tds);
+  int rc = oracle_knn_f32(x, n, x, rows, d, kk, metric, threads, tid, tds);
   if (rc) { free(tid); free(tds); free(buf); return rc; }
   float pad = metric == M_L2 ? INFINITY : -INFINITY;
-  for (int64_t r = 0; r < n; ++r) {
+  for (int64_t r = 0; r < rows; ++r) {
     int m = 0;
     for (int j = 0; j < kk; ++j) {
       int32_t id = tid[(size_t)r * kk + j];
@@ -363,6 +364,11 @@ int oracle_self_graph_f32(const float* x, int64_t n, int d, int k, int metric,
   }
   free(tid); free(tds); free(buf);
   return ORACLE_OK;
+}
+
+int oracle_self_graph_f32(const float* x, int64_t n, int d, int k, int metric,
+                          int threads, int32_t* ids, float* dists) {
+  return oracle_self_graph_rows(x, n, d, k, metric, threads, n, ids, dists);
 }
 
 /* ---- Hamming ------------------------------------------------------------ */

@@ -1,0 +1,229 @@
+"""Pins the CPU restatement (oracle/) before it is trusted as the checker.
+
+Each check is independent of the restatement's own arithmetic: float64 NumPy
+brute force with an np.lexsort (score desc, id asc) tie-break, scipy's cdist,
+an 8-bit popcount table, the committed float64 golden fixtures
+(tests/golden/make_golden.py) and the reference's known-answer tests.  Each
+is chosen so that a plausible mistake (a flipped sign in the L2 epilogue, a
+dropped |b|^2 term, highest-id instead of lowest-id ties, a transposed
+operand, an off-by-one in padding) fails at least one of them.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from mlxvs_amd import synth
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def int_rows(n, d, seed, hi=16):
+    return np.random.default_rng(seed).integers(0, hi, (n, d)).astype(np.float32)
+
+
+def rows(n, d, seed):
+    return np.random.default_rng(seed).standard_normal((n, d), dtype=np.float32)
+
+
+# ---- ordering key (src/kernels.h:16-19) ---------------------------------------
+
+def test_key_orders_floats(oracle):
+    vals = [-np.inf, -1e30, -1.0, -1e-30, -0.0, 0.0, 1e-30, 1.0, 1e30, np.inf]
+    keys = [oracle.key(v) for v in vals]
+    assert keys == sorted(keys) and len(set(keys)) == len(keys)
+    assert oracle.key(-0.0) + 1 == oracle.key(0.0)
+    assert oracle.key(float("nan")) > oracle.key(np.inf)
+
+
+# ---- exact integer data: bit-exact against float64 ---------------------------
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("n,nq,d,k", [(500, 20, 8, 10), (3000, 16, 32, 64),
+                                      (50, 8, 16, 100), (1000, 5, 3, 256)])
+def test_integer_data_exact(oracle, metric, n, nq, d, k):
+    b, q = int_rows(n, d, 1), int_rows(nq, d, 2)  # heavy ties
+    ids, dist = oracle.knn(b, q, k, metric)
+    s = oracle.exact_scores(q, b, metric)
+    want = oracle.exact_topk(s, k)
+    assert np.array_equal(ids, want)
+    keff = min(k, n)
+    got = np.take_along_axis(s, want[:, :keff], 1)
+    exp = -got if metric == "l2" else got
+    assert np.array_equal(dist[:, :keff], exp.astype(np.float32))
+    pad = np.inf if metric == "l2" else -np.inf
+    assert (dist[:, keff:] == pad).all() and (ids[:, keff:] == -1).all()
+
+
+def test_l2_matches_scipy_cdist(oracle):
+    from scipy.spatial.distance import cdist
+
+    b, q = int_rows(800, 24, 3, hi=256), int_rows(30, 24, 4, hi=256)
+    ids, dist = oracle.knn(b, q, 15, "l2")
+    full = cdist(q.astype(np.float64), b.astype(np.float64), "sqeuclidean")
+    assert np.array_equal(dist, np.take_along_axis(full, ids.astype(np.int64), 1))
+    assert np.array_equal(np.sort(full, 1)[:, :15], dist)
+
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_float_data_recall(oracle, metric):
+    b, q = rows(4000, 48, 5), rows(40, 48, 6)
+    ids, dist = oracle.knn(b, q, 20, metric)
+    s = oracle.exact_scores(q, b, metric)
+    assert oracle.recall(ids, s, 20) == 1.0
+    exact = np.take_along_axis(s, ids, 1)
+    exact = -exact if metric == "l2" else exact
+    assert (np.abs(exact - dist) / np.maximum(1, np.abs(exact))).max() < 1e-4
+
+
+def test_cosine_zero_query_and_rows(oracle):
+    # unit_rows divides by max(|x|, 1e-30): a zero row stays zero and scores 0
+    b = rows(100, 8, 7)
+    b[::7] = 0
+    q = np.zeros((2, 8), np.float32)
+    ids, dist = oracle.knn(b, q, 5, "cosine")
+    assert (dist == 0).all() and (ids == np.arange(5)).all()
+
+
+def test_ties_kat(oracle):
+    # tests/test_knn.cpp:156-192
+    g = np.load(GOLDEN / "kat_ties.npz")
+    ids, dist = oracle.knn(g["base"], g["queries"], 10, "l2")
+    assert np.array_equal(ids, g["ids"]) and (dist == 0).all()
+
+
+def test_fewer_rows_than_k(oracle):
+    # python/tests/test_mlxvs.py:63-69
+    b, q = rows(5, 8, 3), rows(4, 8, 4)
+    ids, dist = oracle.knn(b, q, 8, "l2")
+    assert (ids[:, :5] >= 0).all() and (ids[:, 5:] == -1).all()
+    assert np.isinf(dist[:, 5:]).all() and (dist[:, 5:] > 0).all()
+    assert sorted(ids[0, :5].tolist()) == list(range(5))
+
+
+def test_argument_checks(oracle):
+    b = rows(10, 4, 1)
+    with pytest.raises(ValueError):
+        oracle.knn(b, b, 300, "l2")
+    with pytest.raises(ValueError):
+        oracle.knn(b, b, 0, "l2")
+    ids, dist = oracle.knn(np.zeros((0, 4), np.float32), b[:2], 3, "l2")
+    assert (ids == -1).all() and (dist == np.inf).all()
+
+
+# ---- golden fixtures ---------------------------------------------------------------
+
+def test_c1_golden(oracle):
+    base = synth.c1_rows(1, 0, 10_000)
+    q = synth.c1_rows(2, 0, 100)
+    g = np.load(GOLDEN / "c1_full.npz")
+    ids, dist = oracle.knn(base, q, 10, "l2")
+    assert np.array_equal(ids, g["ids"])
+    assert np.array_equal(dist, g["dist"].astype(np.float32))
+
+
+def test_c2_golden(oracle):
+    cen = synth.c2_centres()
+    base = synth.chunked(lambda lo, hi: synth.c2_rows(1, lo, hi, centres=cen), 1_000_000)
+    q = synth.c2_rows(2, 0, 64, centres=cen)
+    g = np.load(GOLDEN / "c2_subset.npz")
+    ids, dist = oracle.knn(base, q, 10, "l2")
+    assert np.array_equal(ids, g["ids"])
+    assert np.array_equal(dist, g["dist"].astype(np.float32))
+
+
+def test_c3_golden(oracle):
+    cen = synth.c3_centres()
+    base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen), 100_000,
+                         chunk=5_000)
+    q = synth.c3_rows(2, 0, 16, centres=cen)
+    g = np.load(GOLDEN / "c3_subset.npz")
+    for metric, key in (("inner_product", "ip"), ("cosine", "cos")):
+        ids, dist = oracle.knn(base, q, 10, metric)
+        np.testing.assert_allclose(dist, g["score_" + key], atol=1e-4)
+        s = oracle.exact_scores(q, base, metric)
+        assert oracle.recall(ids, s, 10) == 1.0
+
+
+def test_c4_golden(oracle):
+    gen = lambda lo, hi: synth.c4_codes(1, lo, hi)  # noqa: E731
+    base = synth.chunked(gen, 1_000_000)
+    q, src = synth.c4_queries(gen, 1_000_000, 2, 0, 32)
+    g = np.load(GOLDEN / "c4_subset.npz")
+    ids, dist = oracle.hamming(base, q, 100)
+    assert np.array_equal(ids, g["ids"])
+    assert np.array_equal(dist, g["dist"].astype(np.float32))
+    assert (ids[:, 0] == src).all() and (dist[:, 0] == 51).all()
+
+
+def test_c5_golden(oracle):
+    cen = synth.c5_centres()
+    x = synth.chunked(lambda lo, hi: synth.c5_rows(1, lo, hi, centres=cen), 200_000)
+    xf = oracle.f16_to_f32(x)
+    g = np.load(GOLDEN / "c5_subset.npz")
+    ids, dist = oracle.self_graph_rows(xf, 64, 32, "l2")
+    assert (ids != np.arange(32)[:, None]).all()
+    np.testing.assert_allclose(dist, g["dist"], rtol=1e-4)
+    assert (ids == g["ids"]).mean() > 0.98
+
+
+# ---- Hamming (src/ivf.cpp:1343-1403) ------------------------------------------------
+
+def test_hamming_tiny_kat(oracle):
+    # python/tests/test_cuvs.py:840-848
+    codes = np.array([[0b1111, 0], [0b1, 0]], dtype=np.uint8)
+    ids, dist = oracle.hamming(codes, codes[:1], 2)
+    assert ids[0].tolist() == [0, 1] and dist[0].tolist() == [0.0, 3.0]
+
+
+@pytest.mark.parametrize("nbytes", [1, 3, 16, 128])
+def test_hamming_vs_popcount_table(oracle, nbytes):
+    # python/tests/test_cuvs.py:772-793
+    rng = np.random.default_rng(11)
+    data = rng.integers(0, 256, (700, nbytes), dtype=np.uint8)
+    q = rng.integers(0, 256, (40, nbytes), dtype=np.uint8)
+    ids, dist = oracle.hamming(data, q, 7)
+    h = oracle.hamming_distances(q, data)
+    order = np.lexsort((np.broadcast_to(np.arange(700), h.shape), h), axis=1)[:, :7]
+    assert np.array_equal(ids, order)
+    assert np.array_equal(dist, np.take_along_axis(h, order, 1).astype(np.float32))
+
+
+def test_hamming_padding_and_empty(oracle):
+    x = np.arange(24, dtype=np.uint8).reshape(6, 4)
+    ids, dist = oracle.hamming(x, x[:2], 10)
+    assert (ids[:, 6:] == -1).all() and (dist[:, 6:] == np.inf).all()
+    ids, dist = oracle.hamming(np.zeros((0, 4), np.uint8), x[:2], 3)
+    assert (ids == -1).all() and (dist == np.inf).all()
+    with pytest.raises(ValueError):
+        oracle.hamming(x, x, 0)
+
+
+def test_pack_words_little_endian(oracle):
+    r = np.arange(1, 8, dtype=np.uint8).reshape(1, 7)
+    w = oracle.pack_words(r)
+    assert w.tolist() == [[0x04030201, 0x00070605]]
+
+
+# ---- self graph (src/all_neighbors.cpp:56-95, 250-263) --------------------------------
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_self_graph_vs_float64(oracle, metric):
+    x = int_rows(400, 6, 9, hi=8)  # many ties and duplicate rows
+    ids, dist = oracle.self_graph(x, 7, metric)
+    s = oracle.exact_scores(x, x, metric)
+    np.fill_diagonal(s, -np.inf)
+    want = oracle.exact_topk(s, 7)
+    if metric != "cosine":  # cosine: float32 rounding decides near-ties
+        assert np.array_equal(ids, want)
+    assert (ids != np.arange(400)[:, None]).all()
+
+
+def test_f16_to_f32_all_patterns(oracle):
+    h = np.arange(65536, dtype=np.uint16).view(np.float16)
+    got = oracle.f16_to_f32(h)
+    want = h.astype(np.float32)
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+    assert np.array_equal(np.signbit(got), np.signbit(want))
