@@ -23,13 +23,15 @@ The same JSON line carries:
   check         the last step's answers for the first 64 queries against the
                 float64 golden fixture (bit-exact, integer-valued data).
 
-Other workloads (c1, c3, c4, c5) are for measurement runs; the driver's line
-is the default.
+Other workloads (c1, c3, c3cos, c4, c5) are for measurement runs; the
+driver's line is the default.  --workload copy times a 1 GiB device copy, the
+reference reading for scaling HBM byte counters.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -87,6 +89,25 @@ def workload(name: str):
     raise SystemExit(f"unknown workload {name}")
 
 
+def copy_probe(steps: int) -> int:
+    """A plain device-to-device copy of 1 GiB (the runtime's copy kernel),
+    timed; its FETCH_SIZE / WRITE_SIZE counter readings per byte copied are
+    the scale factors for the fused kernel's counter readings."""
+    from mlxvs_amd import _hip
+
+    nbytes = 1 << 30
+    src, dst = _hip.DeviceBuffer(nbytes), _hip.DeviceBuffer(nbytes)
+    lib = _hip.lib()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _hip.check(lib.hipMemcpy(dst.ptr, src.ptr, ctypes.c_size_t(nbytes), 3), "hipMemcpy D2D")
+    _hip.synchronize()
+    dt = time.perf_counter() - t0
+    print(json.dumps({"workload": "copy", "bytes_per_copy": nbytes, "copies": steps,
+                      "GB/s": round(2 * nbytes * steps / dt / 1e9, 1)}), flush=True)
+    return 0
+
+
 def cpu_baseline(w, sample: int):
     """The CPU restatement on the first `sample` queries, all host cores."""
     import oracle
@@ -121,6 +142,9 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         return 2
+
+    if args.workload == "copy":
+        return copy_probe(args.steps)
 
     import mlxvs_amd
     from mlxvs_amd import _hip

@@ -23,6 +23,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "knn_kernels.h"
@@ -210,9 +211,14 @@ class Session {
 
 // ---- planning ------------------------------------------------------------------
 
-// Workgroups one fused launch should have: 256 CUs x 2 resident x 4 waves of
-// workgroups, so the last partial wave costs little.
-constexpr int64_t kTargetBlocks = 2048;
+// Workgroups that run at once: CUs x resident blocks of the kernel instance.
+int64_t device_slots(int blocks_per_cu) {
+  int dev = 0, cus = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+            "hipDeviceGetAttribute");
+  return (int64_t)std::max(cus, 1) * std::max(blocks_per_cu, 1);
+}
 
 int list_len_float(int k) {
   if (k <= 4) return 4;
@@ -234,27 +240,50 @@ struct SplitPlan {
 };
 
 // Splits of the base for a fused launch with `lanes` segment lists per split
-// and query and lists of length T.  For k > T the merge sees nseg * T
-// candidates per query; at least 4k of them keep the chance that one
-// segment holds more than T of the k best small (such queries are redone
-// exhaustively).  Returns !ok when the merge cannot hold that many.
+// and query and lists of length T, for a grid of nq_blocks x nsplit
+// workgroups on `slots` resident workgroup slots.  Every workgroup does the
+// same work, so they run in rounds: the split count is the smallest, from at
+// least one full round up, whose last round is >= 97% full (else the fullest).
+// For k > T the merge sees nseg * T candidates per query; at least 4k of them
+// keep the chance that one segment holds more than T of the k best small
+// (such queries are redone exhaustively).  !ok when the merge cannot hold
+// that many.
 SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
-                      int64_t align) {
+                      int64_t align, int64_t slots) {
   SplitPlan p;
   if (n <= 0) return p;
-  const int64_t cap = kern::kMaxMergeCandidates / ((int64_t)lanes * T);
-  int64_t want = (kTargetBlocks + nq_blocks - 1) / nq_blocks;
+  const int64_t cap = std::min<int64_t>(kern::kMaxMergeCandidates / ((int64_t)lanes * T),
+                                        (n + align - 1) / align);
   const int64_t need = k > T ? (4 * (int64_t)k + lanes * T - 1) / (lanes * T) : 1;
-  want = std::max(want, need);
-  int64_t ns = std::clamp<int64_t>(want, 1, cap);
-  ns = std::min<int64_t>(ns, (n + align - 1) / align);
-  int64_t rps = (n + ns - 1) / ns;
-  rps = (rps + align - 1) / align * align;
-  ns = (n + rps - 1) / rps;
-  if (ns < need) return p;
+  const int64_t lo = std::max<int64_t>(need, (slots + nq_blocks - 1) / nq_blocks);
+  const int64_t hi = std::min<int64_t>(cap, 6 * lo);
+  auto round_fill = [&](int64_t ns) {
+    const int64_t w = ns * nq_blocks;
+    const int64_t rounds = (w + slots - 1) / slots;
+    return (double)w / (double)(rounds * slots);
+  };
+  auto realised = [&](int64_t ns) {  // split count after rounding rows up to `align`
+    int64_t rps = (n + ns - 1) / ns;
+    rps = (rps + align - 1) / align * align;
+    return std::make_pair((n + rps - 1) / rps, rps);
+  };
+  int64_t best = std::min(lo, cap), best_rps = 0;
+  double best_fill = -1.0;
+  for (int64_t want = std::min(lo, cap); want <= std::max(hi, std::min(lo, cap)); ++want) {
+    auto [ns, rps] = realised(want);
+    const double f = round_fill(ns);
+    if (f > best_fill + 1e-9) {
+      best_fill = f;
+      best = ns;
+      best_rps = rps;
+    }
+    if (f >= 0.97) break;
+  }
+  if (best_rps == 0) std::tie(best, best_rps) = realised(best);
+  if (best < need) return p;
   p.ok = true;
-  p.nsplit = (int)ns;
-  p.rows_per_split = rps;
+  p.nsplit = (int)best;
+  p.rows_per_split = best_rps;
   return p;
 }
 
@@ -377,7 +406,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   if (kern::fused_supported(kld, T, kf16) && nq < (int64_t(1) << 31)) {
-    plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows);
+    plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows,
+                       device_slots(kern::fused_blocks_per_cu(kld, T, kf16)));
     // a split's rows must stay inside one 32-bit buffer range
     if (plan.ok && (plan.rows_per_split + kern::kTileRows) * kld * esize >= (int64_t(1) << 31))
       plan.ok = false;
@@ -412,8 +442,10 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
 
   const int nseg = 2 * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
+  uint32_t* gkey = ar.take<uint32_t>((size_t)nq);
+  launch(s, "prep", [&] { return kern::launch_zero_u32(gkey, nq, s); });
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
-                     plan.rows_per_split, plan.nsplit, T, part};
+                     plan.rows_per_split, plan.nsplit, T, k, part, gkey};
   launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
     return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
   });
@@ -459,7 +491,8 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   const int Wp = kern::hamming_padded_words(W);
   const int64_t qblocks = (nq + kern::kHammingQueriesPerBlock - 1) / kern::kHammingQueriesPerBlock;
   SplitPlan plan;
-  if (Wp != 0 && kern::hamming_supported(Wp, T)) plan = plan_splits(n, qblocks, k, T, 1, 2);
+  if (Wp != 0 && kern::hamming_supported(Wp, T))
+    plan = plan_splits(n, qblocks, k, T, 1, 2, device_slots(kern::hamming_blocks_per_cu(Wp, T)));
   const int wstride = plan.ok ? Wp : W;
   uint32_t* bw = ar.take<uint32_t>((size_t)n * wstride);
   uint32_t* qw = ar.take<uint32_t>((size_t)nq * wstride);

@@ -33,6 +33,8 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---- row preparation -------------------------------------------------------
 
@@ -120,13 +122,49 @@ __global__ __launch_bounds__(256) void rows_transform_kernel(PrepArgs a) {
 // chain), then written to the other LDS buffer; one barrier per tile.  Rows
 // past the split and dims past ld read as zero through the buffer range check.
 
+// Filters one tile's 16 scores of a lane (rows 8 (i / 4) + 4 h + i % 4 of
+// the tile, ids id0 + row) against the lane's float threshold and inserts the
+// survivors into its stream list.  Every lane drains its own bitmask of
+// survivors in a loop that runs as many times as the busiest lane needs
+// (lanes that are done insert the empty key); the scores go through the
+// lane's 16-float LDS slot `stage` so that a lane can pick its own position.
+// FULL: all 32 rows of the tile exist.  Returns whether the lane kept any.
+template <int T, bool FULL>
+__device__ __forceinline__ bool select_tile(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                            const float (&sc)[16], int h, uint32_t id0,
+                                            int lim, float* stage) {
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    any |= (FULL || m < lim) & !(sc[i] < thr);
+  }
+  if (__builtin_amdgcn_ballot_w64(any) == 0) return false;
+  uint32_t pm = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    pm |= ((FULL || m < lim) & !(sc[i] < thr)) ? (1u << i) : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    *(floatx4*)(stage + 4 * j) = floatx4{sc[4 * j], sc[4 * j + 1], sc[4 * j + 2], sc[4 * j + 3]};
+  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+    const int i = pm ? __builtin_ctz(pm) : 0;
+    const float v = stage[i];
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    stream_insert<T>(K, I, pm ? key_nz(v) : 0u, id0 + m);
+    pm &= pm - 1u;
+  }
+  thr = fmaxf(thr, score_of_key(K[T - 1]));  // NaN while the list has room
+  return any;
+}
+
 template <bool F16, int DH>
 constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <bool F16, int DH, int T>
+template <bool F16, int DH, int T, bool L2>
 __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kernel(FusedArgs a) {
   using E = typename std::conditional<F16, _Float16, float>::type;
   constexpr int EPV = F16 ? 8 : 4;    // elements per 16-byte vector
@@ -138,6 +176,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int QV = DH / EPV;        // query vectors per lane
   __shared__ __align__(16) E tile[2][kTileRows * STRIDE];
   __shared__ __align__(16) float tnorm[2][kTileRows];
+  __shared__ __align__(16) float stage[256 * 16];  // each lane's scores, for its inserts
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -148,7 +187,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const bool wave_on = q0w < a.nq;
   const bool qvalid = q < a.nq;
   const int ld = a.ld;
-  const bool l2 = a.metric == kL2;
+  constexpr bool l2 = L2;
 
   const int64_t r0 = (int64_t)split * a.rows_per_split;
   const int64_t r1 = min(a.n, r0 + a.rows_per_split);
@@ -176,7 +215,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     const int r = e / VROW, c = (e % VROW) * EPV;
     voff[j] = (e < VTILE && c < ld) ? (uint32_t)((r * ld + c) * (int)sizeof(E)) : 0x80000000u;
   }
-  uint32_t noff = tid * 4u;  // norm word of this thread (threads < 32)
+  // norm word of this thread (threads past the tile read beyond the range)
+  uint32_t noff = tid < kTileRows ? tid * 4u : 0x80000000u;
 
   // the lane's query dims [h DH, h DH + DH): 16-byte buffer loads of the
   // query row, zero past ld and for lanes without a query
@@ -203,7 +243,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       pf[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, voff[j], 0, 0);
       voff[j] += tile_bytes;
     }
-    if (l2 && tid < kTileRows) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+    if (l2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
     noff += kTileRows * 4;
   };
   auto store_tile = [&](int buf) {
@@ -218,10 +258,18 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     if (l2 && tid < kTileRows) tnorm[buf][tid] = __uint_as_float(pn);
   };
 
-  uint64_t L[T];
+  uint32_t K[T], I[T];
 #pragma unroll
-  for (int i = 0; i < T; ++i) L[i] = 0;
-  float thr = score_of_key(0u);  // NaN: every candidate passes until full
+  for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  // the filter: the score of K[T-1] or better (NaN -- every candidate
+  // passes -- while the list has room and nothing better is known)
+  float thr = score_of_key(0u);
+  // With T >= k every lane's T-th best is a lower bound on its query's k-th
+  // best score, so all lanes of a query -- in every workgroup -- filter with
+  // the best such bound any of them has published (a per-query key, raised
+  // with a relaxed atomic max; a stale read is only a weaker bound).
+  const bool share = a.k <= T;
+  uint32_t* gk = a.gkey + (qvalid ? q : 0);
 
   if (ntiles > 0) {
     issue_loads();
@@ -235,8 +283,12 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    if (more) issue_loads();
+    // the shared key is read before the tile prefetch, so that waiting for
+    // it (in the epilogue) does not wait for the prefetch
+    const uint32_t gseen = __hip_atomic_load(gk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // unconditional (past the last tile the offsets are out of range and
+    // read zero), so the wait counts after the shared key stay static
+    issue_loads();
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
       floatx16 acc;
@@ -256,44 +308,41 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
           acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], qf[v][3], acc, 0, 0, 0);
         }
       }
-      // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2
+      __builtin_amdgcn_sched_barrier(0);
+      // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2;
+      // 2 q.b is exact, so fma(2, q.b, -|b|^2) rounds exactly as that form
       float sc[16];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        floatx4 nb = {0.f, 0.f, 0.f, 0.f};
-        if (l2) nb = *(const floatx4*)&tnorm[buf][8 * j + 4 * h];
+        if constexpr (L2) {
+          const floatx4 nb = *(const floatx4*)&tnorm[buf][8 * j + 4 * h];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          sc[4 * j + u] = l2 ? 2.0f * acc[4 * j + u] - nb[u] : acc[4 * j + u];
-      }
-      const int lim = nrows - t * kTileRows;
-      bool any = false;
+          for (int u = 0; u < 4; ++u) sc[4 * j + u] = __builtin_fmaf(2.0f, acc[4 * j + u], -nb[u]);
+        } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-        any |= (m < lim) & !(sc[i] < thr);
-      }
-      if (any) {
-        const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-          if (m < lim && !(sc[i] < thr)) {
-            list_insert<T>(L, rank_of(sc[i], id0 + m));
-            thr = score_of_key((uint32_t)(L[T - 1] >> 32));
-          }
+          for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[4 * j + u];
         }
       }
+      if (share) thr = fmaxf(thr, score_of_key(gseen));
+      const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
+      bool inserted;
+      if (t + 1 < ntiles || (nrows & (kTileRows - 1)) == 0)
+        inserted = select_tile<T, true>(K, I, thr, sc, h, id0, kTileRows, stage + 16 * tid);
+      else
+        inserted = select_tile<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows,
+                                         stage + 16 * tid);
+      if (share && qvalid && inserted && K[T - 1] > gseen)
+        __hip_atomic_fetch_max(gk, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (more) store_tile(buf ^ 1);
+    store_tile(buf ^ 1);
     __syncthreads();
   }
 
   if (qvalid) {
     uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
 #pragma unroll
-    for (int i = 0; i < T; ++i) dst[i] = L[i];
+    for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
   }
 }
 
@@ -435,6 +484,11 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   emit_topk<256>(sel, work, a.k, orow, a.metric, qn, a.dist_mode, a.ids, a.dists);
 }
 
+__global__ void zero_u32_kernel(uint32_t* p, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = 0u;
+}
+
 __global__ void fill_kernel(int32_t* ids, float* dists, int64_t count, float pad) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < count) {
@@ -490,9 +544,32 @@ __global__ void self_drop_kernel(SelfDropArgs a) {
 }
 
 template <bool F16, int DH, int T>
+int occupancy_inst() {
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fused_kernel<F16, DH, T, true>, 256,
+                                                   0) != hipSuccess)
+    return 1;
+  return blocks;
+}
+
+template <bool F16, int DH>
+int occupancy_t(int T) {
+  switch (T) {
+    case 4: return occupancy_inst<F16, DH, 4>();
+    case 8: return occupancy_inst<F16, DH, 8>();
+    case 10: return occupancy_inst<F16, DH, 10>();
+    case 16: return occupancy_inst<F16, DH, 16>();
+  }
+  return 1;
+}
+
+template <bool F16, int DH, int T>
 hipError_t launch_inst(const FusedArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, (a.nq + kQueriesPerBlock - 1) / kQueriesPerBlock);
-  hipLaunchKernelGGL((fused_kernel<F16, DH, T>), grid, dim3(256), 0, s, a);
+  if (a.metric == kL2)
+    hipLaunchKernelGGL((fused_kernel<F16, DH, T, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((fused_kernel<F16, DH, T, false>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -523,6 +600,16 @@ hipError_t dispatch_t(const FusedArgs& a, hipStream_t s) {
 
 bool fused_supported(int ld, int T, bool f16) {
   return t_ok(T) && ld >= 1 && dh_for(ld, f16) != 0;
+}
+
+int fused_blocks_per_cu(int ld, int T, bool f16) {
+  switch (dh_for(ld, f16)) {
+    case 16: return occupancy_t<false, 16>(T);
+    case 32: return f16 ? occupancy_t<true, 32>(T) : occupancy_t<false, 32>(T);
+    case 64: return f16 ? occupancy_t<true, 64>(T) : occupancy_t<false, 64>(T);
+    case 128: return f16 ? occupancy_t<true, 128>(T) : occupancy_t<false, 128>(T);
+  }
+  return 1;
 }
 
 hipError_t launch_norms(const PrepArgs& a, hipStream_t s) {
@@ -583,6 +670,13 @@ hipError_t launch_fill(int32_t* ids, float* dists, int64_t count, float pad,
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256),
                      0, s, ids, dists, count, pad);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_u32(uint32_t* p, int64_t count, hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
+                     p, count);
   return hipGetLastError();
 }
 

@@ -120,6 +120,25 @@ hipError_t launch_inst(const HammingArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int W, int T>
+int occupancy_inst() {
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, hamming_kernel<W, T>, 256, 0) !=
+      hipSuccess)
+    return 1;
+  return blocks;
+}
+
+template <int W>
+int occupancy_t(int T) {
+  switch (T) {
+    case 4: return occupancy_inst<W, 4>();
+    case 8: return occupancy_inst<W, 8>();
+    case 16: return occupancy_inst<W, 16>();
+  }
+  return 1;
+}
+
 template <int W>
 hipError_t dispatch_t(const HammingArgs& a, hipStream_t s) {
   switch (a.T) {
@@ -150,6 +169,19 @@ bool hamming_supported(int W, int T) {
 }
 
 int hamming_padded_words(int W) { return hamming_w(W); }
+
+int hamming_blocks_per_cu(int W, int T) {
+  switch (W) {
+    case 2: return occupancy_t<2>(T);
+    case 4: return occupancy_t<4>(T);
+    case 8: return occupancy_t<8>(T);
+    case 16: return occupancy_t<16>(T);
+    case 32: return occupancy_t<32>(T);
+    case 48: return occupancy_t<48>(T);
+    case 64: return occupancy_t<64>(T);
+  }
+  return 1;
+}
 
 hipError_t launch_hamming(const HammingArgs& a, hipStream_t s) {
   switch (a.W) {

@@ -58,12 +58,16 @@ struct FusedArgs {
   int64_t rows_per_split;
   int nsplit;
   int T;                 // list length per lane
+  int k;                 // neighbours wanted (k <= T: lanes share thresholds)
   uint64_t* part;        // [nq][2*nsplit][T]
+  uint32_t* gkey;        // [nq] shared threshold keys, zeroed before the launch
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
 // true when the fused kernels have an instance for (ld, T)
 bool fused_supported(int ld, int T, bool f16);
+// resident workgroups per CU of that instance (HIP occupancy query)
+int fused_blocks_per_cu(int ld, int T, bool f16);
 
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.
@@ -114,6 +118,9 @@ struct SelectArgs {
 };
 hipError_t launch_select(const SelectArgs& a, hipStream_t s);
 
+// Zero a uint32 array (a kernel, so that the call stays graph-capturable).
+hipError_t launch_zero_u32(uint32_t* p, int64_t count, hipStream_t s);
+
 // Output fill for empty inputs: ids -1, distances `pad`.
 hipError_t launch_fill(int32_t* ids, float* dists, int64_t count, float pad,
                        hipStream_t s);
@@ -141,6 +148,7 @@ struct HammingArgs {
 };
 hipError_t launch_hamming(const HammingArgs& a, hipStream_t s);
 bool hamming_supported(int W, int T);
+int hamming_blocks_per_cu(int W, int T);
 // The padded word count the fused Hamming kernel takes for W words (0: none).
 int hamming_padded_words(int W);
 constexpr int kHammingQueriesPerBlock = 256;

@@ -58,6 +58,39 @@ __device__ __forceinline__ void list_insert(uint64_t (&L)[T], uint64_t c) {
   }
 }
 
+// A lane's private list for a stream of candidates in increasing id order:
+// keys K (descending) and ids I, K = 0 marks an empty slot.  Because every
+// new candidate has a larger id than every kept one, "better" is simply a
+// larger key (equal keys keep the earlier, lower id), so one 32-bit compare
+// per slot decides.  Real candidates use key_nz (never 0); the one float whose
+// key is 0 (the NaN 0xffffffff) ranks with key 1, next to it.
+__device__ __forceinline__ uint32_t key_nz(float v) {
+  const uint32_t k = key_of(v);
+  return k > 1u ? k : 1u;
+}
+
+// Inserts (kc, ic); kc = 0 is a no-op, so lanes that have nothing to insert
+// pass 0 instead of branching.  The candidate walks down the list and swaps
+// with every entry it beats: one 32-bit compare and four selects per slot.
+template <int T>
+__device__ __forceinline__ void stream_insert(uint32_t (&K)[T], uint32_t (&I)[T], uint32_t kc,
+                                              uint32_t ic) {
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const bool b = kc > K[j];
+    const uint32_t tk = K[j], ti = I[j];
+    K[j] = b ? kc : tk;
+    I[j] = b ? ic : ti;
+    kc = b ? tk : kc;
+    ic = b ? ti : ic;
+  }
+}
+
+// The rank (see rank_of) of a stream-list slot, 0 for an empty one.
+__device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
+  return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
+}
+
 // In-LDS bitonic sort of P (a power of two) values, descending by `ord`.
 // All threads of the workgroup call it; it ends with a barrier.
 template <int NT, typename Ord>
