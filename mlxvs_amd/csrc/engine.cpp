@@ -237,6 +237,7 @@ struct SplitPlan {
   bool ok = false;
   int nsplit = 0;
   int64_t rows_per_split = 0;
+  bool xcd = false;  // XCD-major workgroup order (nsplit % 8 == 0)
 };
 
 // Splits of the base for a fused launch with `lanes` segment lists per split
@@ -244,12 +245,14 @@ struct SplitPlan {
 // workgroups on `slots` resident workgroup slots.  Every workgroup does the
 // same work, so they run in rounds: the split count is the smallest, from at
 // least one full round up, whose last round is >= 97% full (else the fullest).
+// With `xcd`, split counts are multiples of 8 and rounds are counted per XCD
+// (the kernel then gives each XCD whole splits, see FusedArgs::xcd_major).
 // For k > T the merge sees nseg * T candidates per query; at least 4k of them
 // keep the chance that one segment holds more than T of the k best small
 // (such queries are redone exhaustively).  !ok when the merge cannot hold
 // that many.
 SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
-                      int64_t align, int64_t slots) {
+                      int64_t align, int64_t slots, bool xcd = false) {
   SplitPlan p;
   if (n <= 0) return p;
   const int64_t cap = std::min<int64_t>(kern::kMaxMergeCandidates / ((int64_t)lanes * T),
@@ -257,21 +260,39 @@ SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
   const int64_t need = k > T ? (4 * (int64_t)k + lanes * T - 1) / (lanes * T) : 1;
   const int64_t lo = std::max<int64_t>(need, (slots + nq_blocks - 1) / nq_blocks);
   const int64_t hi = std::min<int64_t>(cap, 6 * lo);
-  auto round_fill = [&](int64_t ns) {
-    const int64_t w = ns * nq_blocks;
-    const int64_t rounds = (w + slots - 1) / slots;
-    return (double)w / (double)(rounds * slots);
-  };
   auto realised = [&](int64_t ns) {  // split count after rounding rows up to `align`
     int64_t rps = (n + ns - 1) / ns;
     rps = (rps + align - 1) / align * align;
     return std::make_pair((n + rps - 1) / rps, rps);
   };
+  auto fill = [&](int64_t ns, bool per_xcd) {
+    const int64_t w = per_xcd ? ns / 8 * nq_blocks : ns * nq_blocks;
+    const int64_t sl = per_xcd ? std::max<int64_t>(1, slots / 8) : slots;
+    return (double)w / (double)(((w + sl - 1) / sl) * sl);
+  };
+  if (xcd) {
+    double best_fill = -1.0;
+    for (int64_t want = (std::max<int64_t>(lo, 8) + 7) / 8 * 8; want <= hi; want += 8) {
+      auto [ns, rps] = realised(want);
+      if (ns % 8 != 0 || ns < need) continue;
+      const double f = fill(ns, true);
+      if (f > best_fill + 1e-9) {
+        best_fill = f;
+        p.ok = true;
+        p.nsplit = (int)ns;
+        p.rows_per_split = rps;
+        p.xcd = true;
+      }
+      if (f >= 0.97) break;
+    }
+    if (p.ok && best_fill >= 0.9) return p;
+    p = SplitPlan{};
+  }
   int64_t best = std::min(lo, cap), best_rps = 0;
   double best_fill = -1.0;
   for (int64_t want = std::min(lo, cap); want <= std::max(hi, std::min(lo, cap)); ++want) {
     auto [ns, rps] = realised(want);
-    const double f = round_fill(ns);
+    const double f = fill(ns, false);
     if (f > best_fill + 1e-9) {
       best_fill = f;
       best = ns;
@@ -407,7 +428,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   SplitPlan plan;
   if (kern::fused_supported(kld, T, kf16) && nq < (int64_t(1) << 31)) {
     plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows,
-                       device_slots(kern::fused_blocks_per_cu(kld, T, kf16)));
+                       device_slots(kern::fused_blocks_per_cu(kld, T, kf16)), true);
     // a split's rows must stay inside one 32-bit buffer range
     if (plan.ok && (plan.rows_per_split + kern::kTileRows) * kld * esize >= (int64_t(1) << 31))
       plan.ok = false;
@@ -445,7 +466,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq);
   launch(s, "prep", [&] { return kern::launch_zero_u32(gkey, nq, s); });
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
-                     plan.rows_per_split, plan.nsplit, T, k, part, gkey};
+                     plan.rows_per_split, plan.nsplit, T, k, part, gkey, (int)qblocks,
+                     plan.xcd ? 1 : 0};
   launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
     return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
   });

@@ -176,13 +176,30 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int QV = DH / EPV;        // query vectors per lane
   __shared__ __align__(16) E tile[2][kTileRows * STRIDE];
   __shared__ __align__(16) float tnorm[2][kTileRows];
-  __shared__ __align__(16) float stage[256 * 16];  // each lane's scores, for its inserts
+  // each lane's scores for its inserts; a 20-float lane stride keeps the
+  // 16-byte writes of 16 consecutive lanes on distinct bank quads
+  __shared__ __align__(16) float stage[256 * 20];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x;
-  const int q0w = blockIdx.y * kQueriesPerBlock + wave * 32;
+  // Workgroup -> (split, query block).  Workgroups are dealt to the 8 XCDs
+  // round-robin by id; with xcd_major, XCD j gets splits j, j + 8, ... for
+  // every query block, split-major, so the workgroups that stream the same
+  // base rows run together on one XCD and share its L2.
+  int split, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_major) {
+      const int slot = id >> 3;
+      split = (id & 7) + 8 * (slot / a.nqb);
+      qb = slot % a.nqb;
+    } else {
+      split = id % a.nsplit;
+      qb = id / a.nsplit;
+    }
+  }
+  const int q0w = qb * kQueriesPerBlock + wave * 32;
   const int q = q0w + col;
   const bool wave_on = q0w < a.nq;
   const bool qvalid = q < a.nq;
@@ -327,10 +344,10 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
       bool inserted;
       if (t + 1 < ntiles || (nrows & (kTileRows - 1)) == 0)
-        inserted = select_tile<T, true>(K, I, thr, sc, h, id0, kTileRows, stage + 16 * tid);
+        inserted = select_tile<T, true>(K, I, thr, sc, h, id0, kTileRows, stage + 20 * tid);
       else
         inserted = select_tile<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows,
-                                         stage + 16 * tid);
+                                         stage + 20 * tid);
       if (share && qvalid && inserted && K[T - 1] > gseen)
         __hip_atomic_fetch_max(gk, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -565,7 +582,7 @@ int occupancy_t(int T) {
 
 template <bool F16, int DH, int T>
 hipError_t launch_inst(const FusedArgs& a, hipStream_t s) {
-  dim3 grid(a.nsplit, (a.nq + kQueriesPerBlock - 1) / kQueriesPerBlock);
+  const dim3 grid(a.nsplit * a.nqb);
   if (a.metric == kL2)
     hipLaunchKernelGGL((fused_kernel<F16, DH, T, true>), grid, dim3(256), 0, s, a);
   else

@@ -41,7 +41,7 @@ hipError_t launch_norms(const PrepArgs& a, hipStream_t s);
 hipError_t launch_transform(const PrepArgs& a, hipStream_t s);
 
 // Fused distance + per-lane top-T selection.
-//   grid (nsplit, ceil(nq / 128)); workgroup 256 threads.
+//   grid nsplit * nqb (nqb = ceil(nq / 128)); workgroup 256 threads.
 // Lane l of wavefront w of block (split, qb) keeps the best T candidates of
 // query qb*128 + 32w + l%32 among base rows of the split whose tile position
 // has bit 2 equal to l/32 ("segment" 2*split + l/32).  Output part
@@ -61,6 +61,8 @@ struct FusedArgs {
   int k;                 // neighbours wanted (k <= T: lanes share thresholds)
   uint64_t* part;        // [nq][2*nsplit][T]
   uint32_t* gkey;        // [nq] shared threshold keys, zeroed before the launch
+  int nqb;               // query blocks, ceil(nq / 128)
+  int xcd_major;         // nsplit % 8 == 0: XCD-major workgroup order (see kernel)
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
