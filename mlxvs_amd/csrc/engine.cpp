@@ -377,7 +377,10 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const bool l2 = metric == kern::kL2;
   const bool kf16 = in.f16 && !cosine;
   const int esize = kf16 ? 2 : 4;
-  const int vmul = kf16 ? 8 : 4;
+  // fp32 rows longer than the register-resident kernels take go through the
+  // deep kernel, which reads them in 32-dim chunks
+  const bool deep = !kf16 && d > kern::kMaxFusedDimF32;
+  const int vmul = kf16 ? 8 : deep ? 32 : 4;
   const void* kbase = in.base;
   const void* kq = in.queries;
   int kld = d;
@@ -385,7 +388,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   float* qnorm = nullptr;
   const int f16 = in.f16 ? 1 : 0;
   if (cosine) {
-    kld = round_up(d, 4);
+    kld = round_up(d, vmul);
     float* nb = ar.take<float>((size_t)n);
     float* nqv = ar.take<float>((size_t)nq);
     float* ub = ar.take<float>((size_t)n * kld);
@@ -426,11 +429,14 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int T = list_len_float(k);
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
-  if (kern::fused_supported(kld, T, kf16) && nq < (int64_t(1) << 31)) {
-    plan = plan_splits(n, qblocks, k, T, 2, kern::kTileRows,
-                       device_slots(kern::fused_blocks_per_cu(kld, T, kf16)), true);
-    // a split's rows must stay inside one 32-bit buffer range
-    if (plan.ok && (plan.rows_per_split + kern::kTileRows) * kld * esize >= (int64_t(1) << 31))
+  const bool use_deep = deep && kern::deep_supported(kld, T, false);
+  const int tile_rows = use_deep ? kern::kDeepRows : kern::kTileRows;
+  if ((use_deep || kern::fused_supported(kld, T, kf16)) && nq < (int64_t(1) << 31)) {
+    const int bpc = use_deep ? kern::deep_blocks_per_cu(T) : kern::fused_blocks_per_cu(kld, T, kf16);
+    plan = plan_splits(n, qblocks, k, T, 2, tile_rows, device_slots(bpc), true);
+    // a split's rows (and one tile past them) must stay inside one 32-bit
+    // buffer range
+    if (plan.ok && (plan.rows_per_split + tile_rows) * kld * esize >= (int64_t(1) << 31))
       plan.ok = false;
   }
 
@@ -468,9 +474,12 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, (int)qblocks,
                      plan.xcd ? 1 : 0};
-  launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
-    return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
-  });
+  if (use_deep)
+    launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });
+  else
+    launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
+      return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
+    });
   int* flags = nullptr;
   if (T < k) flags = ar.take<int>((size_t)nq);
   kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};

@@ -363,6 +363,242 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   }
 }
 
+// ---- fused kernel for deep rows (fp32, ld > 256) ----------------------------------
+//
+// Rows too long to keep a query in registers.  A workgroup again owns 128
+// queries (wavefront w: queries 32 w .. 32 w + 31) and walks the base rows of
+// its split, now 128 rows per tile: for each tile it runs a K loop over
+// 32-dim chunks, staging the chunk of the 128 rows AND of its 128 queries in
+// LDS (double-buffered, the next chunk fetched into registers while the
+// current one is multiplied), and accumulates a 128 x 32 score block per
+// wavefront in four 32 x 32 MFMA accumulators.  Within a chunk lane half h
+// takes dims [16 h, 16 h + 16), so one 16-byte LDS read of a row or of the
+// query feeds four v_mfma_f32_32x32x2_f32 steps.  After the last chunk of a
+// tile the lane filters its 64 scores (4 blocks x 16) into its stream list;
+// selection work per tile is fixed while MFMA work grows with ld, so at
+// ld >= 512 it is a few percent of the tile.  Lane (h, col) of row block rb
+// holds rows 32 rb + 8 (i / 4) + 4 h + i % 4: tile position bit 2 is h, so
+// the segments are those of fused_kernel (2 split + h).
+
+// Inserts the scores of one 32-row block (rows id0 + 8 (i / 4) + 4 h + i % 4,
+// the first `lim` of the block real) that pass the lane's threshold.  One
+// position at a time, skipped when no lane of the wavefront passes it, so the
+// ids reach the list in increasing order.
+template <int T>
+__device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                             const float (&sc)[16], int h, uint32_t id0,
+                                             int lim) {
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    any |= (m < lim) & !(sc[i] < thr);
+  }
+  if (__builtin_amdgcn_ballot_w64(any) == 0) return false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    const bool p = (m < lim) & !(sc[i] < thr);
+    if (__builtin_amdgcn_ballot_w64(p) != 0) stream_insert<T>(K, I, p ? key_nz(sc[i]) : 0u, id0 + m);
+  }
+  thr = fmaxf(thr, score_of_key(K[T - 1]));
+  return any;
+}
+
+constexpr int kDeepChunk = 32;                 // dims per LDS stage
+constexpr int kDeepStride = kDeepChunk + 4;    // 16-byte pad: 8 rows hit distinct bank quads
+constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
+
+template <int T, bool L2>
+__global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
+  __shared__ __align__(16) float tA[2][kDeepRows * kDeepStride];
+  __shared__ __align__(16) float tQ[2][kQueriesPerBlock * kDeepStride];
+  __shared__ __align__(16) float tnorm[2][kDeepRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  int split, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_major) {
+      const int slot = id >> 3;
+      split = (id & 7) + 8 * (slot / a.nqb);
+      qb = slot % a.nqb;
+    } else {
+      split = id % a.nsplit;
+      qb = id / a.nsplit;
+    }
+  }
+  const int qb0 = qb * kQueriesPerBlock;
+  const int q = qb0 + wave * 32 + col;
+  const bool wave_on = qb0 + wave * 32 < a.nq;
+  const bool qvalid = q < a.nq;
+  const int ld = a.ld;
+  const int NC = ld / kDeepChunk;
+
+  const int64_t r0 = (int64_t)split * a.rows_per_split;
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+  const int ntiles = (nrows + kDeepRows - 1) / kDeepRows;
+  const int nsteps = ntiles * NC;
+
+  // buffer ranges: the split's rows, the block's queries, the split's norms;
+  // reads past them return zero
+  const float* sbase = (const float*)a.base + r0 * ld;
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)sbase, (short)0, nrows * ld * 4, 0x00020000);
+  const int qrows = min(kQueriesPerBlock, a.nq - qb0);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const float*)a.queries + (int64_t)qb0 * ld), (short)0, qrows * ld * 4,
+      0x00020000);
+  const float* snorm = L2 ? a.bnorm + r0 : (const float*)a.base;
+  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)snorm, (short)0, L2 ? nrows * 4 : 0, 0x00020000);
+
+  // Thread's 16-byte vectors of a chunk: e = tid + 256 j -> row e / 8,
+  // vector e % 8, for the base rows and the queries alike.  Offsets of the
+  // next chunk to fetch are carried: +128 bytes per chunk, and at a tile end
+  // the row offsets move on by one tile while the query offsets return to
+  // chunk 0.
+  constexpr int NV = kDeepRows * (kDeepChunk / 4) / 256;  // 4
+  uint32_t aoff[NV], qoff[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = tid + 256 * j;
+    const uint32_t o = (uint32_t)(((e >> 3) * ld + 4 * (e & 7)) * 4);
+    aoff[j] = o;
+    qoff[j] = o;
+  }
+  uint32_t noff = tid < kDeepRows ? tid * 4u : 0x80000000u;
+  const uint32_t row_wrap = (uint32_t)(kDeepRows * ld * 4) - (uint32_t)(NC * kDeepChunk * 4);
+  const uint32_t q_wrap = (uint32_t)(NC * kDeepChunk * 4);
+
+  u32x4 pa[NV], pq[NV];
+  uint32_t pn = 0;
+  int pc = 0;  // chunk index of the next fetch
+  auto issue_loads = [&]() {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      pa[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, aoff[j], 0, 0);
+      pq[j] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[j], 0, 0);
+    }
+    if (L2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+  };
+  // stores the fetched chunk (chunk pc of its tile) and advances the offsets
+  auto store_chunk = [&](int buf, int tpar) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = tid + 256 * j;
+      const int off = (e >> 3) * kDeepStride + 4 * (e & 7);
+      *(u32x4*)&tA[buf][off] = pa[j];
+      *(u32x4*)&tQ[buf][off] = pq[j];
+    }
+    if (L2 && pc == 0 && tid < kDeepRows) tnorm[tpar][tid] = __uint_as_float(pn);
+    const bool wrap = ++pc == NC;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      aoff[j] += wrap ? row_wrap + kDeepChunk * 4 : kDeepChunk * 4;
+      qoff[j] += wrap ? kDeepChunk * 4 - q_wrap : kDeepChunk * 4;
+    }
+    if (wrap) {
+      pc = 0;
+      noff += kDeepRows * 4;
+    }
+  };
+
+  uint32_t K[T], I[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  float thr = score_of_key(0u);
+  const bool share = a.k <= T;
+  uint32_t* gk = a.gkey + (qvalid ? q : 0);
+
+  if (nsteps > 0) {
+    issue_loads();
+    store_chunk(0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  floatx16 acc[kDeepRB];
+#pragma unroll
+  for (int r = 0; r < kDeepRB; ++r)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
+
+  int c = 0, t = 0;
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    const uint32_t gseen = __hip_atomic_load(gk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the fetched tile's parity, read before store_chunk advances pc
+    const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
+    issue_loads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave_on) {
+      const float* qrow = &tQ[buf][(wave * 32 + col) * kDeepStride + 16 * h];
+      const float* arow = &tA[buf][col * kDeepStride + 16 * h];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const floatx4 bq = *(const floatx4*)(qrow + 4 * v);
+        floatx4 av[kDeepRB];
+#pragma unroll
+        for (int r = 0; r < kDeepRB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * kDeepStride + 4 * v);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int r = 0; r < kDeepRB; ++r)
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], bq[u], acc[r], 0, 0, 0);
+      }
+    }
+    if (c + 1 == NC) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (wave_on) {
+        if (share) thr = fmaxf(thr, score_of_key(gseen));
+        const int lim0 = nrows - t * kDeepRows;
+        const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kDeepRows);
+        bool inserted = false;
+#pragma unroll
+        for (int r = 0; r < kDeepRB; ++r) {
+          float sc[16];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (L2) {
+              const floatx4 nb = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * j + 4 * h];
+#pragma unroll
+              for (int u = 0; u < 4; ++u)
+                sc[4 * j + u] = __builtin_fmaf(2.0f, acc[r][4 * j + u], -nb[u]);
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
+            }
+          }
+          inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+        }
+        if (share && qvalid && inserted && K[T - 1] > gseen)
+          __hip_atomic_fetch_max(gk, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int r = 0; r < kDeepRB; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store_chunk(buf ^ 1, ftpar);
+    __syncthreads();
+    if (++c == NC) {
+      c = 0;
+      ++t;
+    }
+  }
+
+  if (qvalid) {
+    uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
+#pragma unroll
+    for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
+  }
+}
+
 // ---- merge of segment lists ---------------------------------------------------
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
@@ -613,7 +849,51 @@ hipError_t dispatch_t(const FusedArgs& a, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+template <int T>
+int deep_occupancy() {
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true>, 256, 0) !=
+      hipSuccess)
+    return 1;
+  return blocks;
+}
+
+template <int T>
+hipError_t deep_inst(const FusedArgs& a, hipStream_t s) {
+  const dim3 grid(a.nsplit * a.nqb);
+  if (a.metric == kL2)
+    hipLaunchKernelGGL((deep_kernel<T, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((deep_kernel<T, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool deep_supported(int ld, int T, bool f16) {
+  return !f16 && t_ok(T) && ld > kMaxFusedDimF32 && ld % kDeepChunk == 0;
+}
+
+int deep_blocks_per_cu(int T) {
+  switch (T) {
+    case 4: return deep_occupancy<4>();
+    case 8: return deep_occupancy<8>();
+    case 10: return deep_occupancy<10>();
+    case 16: return deep_occupancy<16>();
+  }
+  return 1;
+}
+
+hipError_t launch_deep(const FusedArgs& a, hipStream_t s) {
+  if (!deep_supported(a.ld, a.T, false)) return hipErrorInvalidValue;
+  switch (a.T) {
+    case 4: return deep_inst<4>(a, s);
+    case 8: return deep_inst<8>(a, s);
+    case 10: return deep_inst<10>(a, s);
+    case 16: return deep_inst<16>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
 
 bool fused_supported(int ld, int T, bool f16) {
   return t_ok(T) && ld >= 1 && dh_for(ld, f16) != 0;

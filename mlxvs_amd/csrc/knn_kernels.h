@@ -71,6 +71,14 @@ bool fused_supported(int ld, int T, bool f16);
 // resident workgroups per CU of that instance (HIP occupancy query)
 int fused_blocks_per_cu(int ld, int T, bool f16);
 
+// Deep rows (fp32, ld > kMaxFusedDimF32, ld a multiple of 32): the same
+// arguments, segments and output as the fused kernels, with kDeepRows rows
+// per tile and a K loop over 32-dim chunks staged in LDS.
+constexpr int kDeepRows = 128;
+hipError_t launch_deep(const FusedArgs& a, hipStream_t s);
+bool deep_supported(int ld, int T, bool f16);
+int deep_blocks_per_cu(int T);
+
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.
 struct MergeArgs {

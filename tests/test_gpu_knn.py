@@ -269,6 +269,54 @@ def test_fp16_path(engine, oracle, metric, d):
                 tol=2e-3)
 
 
+# ---- deep rows (d > 256): the K-looped kernel --------------------------------------
+
+@pytest.mark.parametrize("d", [288, 512, 1000, 1536, 2048])
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_deep_dimensions(engine, oracle, d, metric):
+    base, q = rows(6_000, d, 21), rows(300, d, 22)
+    ids, dist = engine.brute_force_knn(base, q, 10, metric)
+    check_float(oracle, ids, dist, base, q, 10, metric)
+
+
+@pytest.mark.parametrize("k", [1, 4, 10, 16, 17, 32, 100, 256])
+def test_deep_integer_bit_exact(engine, oracle, k):
+    # integer values in [0, 16): every score is an integer below 2^24, exact
+    # in any summation order, so ids (ties to the lowest id) and distances
+    # equal the CPU restatement's bit for bit; n and nq leave partial tiles
+    # and a query block with one query
+    rng = np.random.default_rng(31)
+    base = rng.integers(0, 16, (20_000, 768)).astype(np.float32)
+    q = rng.integers(0, 16, (257, 768)).astype(np.float32)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(base, q, k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
+
+
+@pytest.mark.parametrize("n", [1, 9, 127, 128, 129, 1_000])
+def test_deep_small_n(engine, oracle, n):
+    base, q = rows(n, 320, 23), rows(40, 320, 24)
+    for k in (1, 10, 64):
+        ids, dist = engine.brute_force_knn(base, q, k, "l2")
+        check_float(oracle, ids, dist, base, q, k, "l2")
+
+
+def test_deep_device_api_matches_host_api(engine):
+    from mlxvs_amd import _hip
+
+    base, q = rows(30_000, 640, 25), rows(130, 640, 26)
+    ids, dist = engine.brute_force_knn(base, q, 10, "l2")
+    db, dq = _hip.DeviceBuffer.from_array(base), _hip.DeviceBuffer.from_array(q)
+    di, dd = _hip.DeviceBuffer(130 * 10 * 4), _hip.DeviceBuffer(130 * 10 * 4)
+    engine.brute_force_knn_device(db.value, 30_000, dq.value, 130, 640, 10, "l2", di.value,
+                                  dd.value)
+    _hip.synchronize()
+    assert np.array_equal(di.download((130, 10), np.int32), ids)
+    assert np.array_equal(dd.download((130, 10), np.float32), dist)
+
+
 def test_c3_subset(engine, oracle):
     cen = synth.c3_centres()
     base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen), 100_000,
