@@ -469,10 +469,12 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
 
   const int nseg = 2 * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
-  uint32_t* gkey = ar.take<uint32_t>((size_t)nq);
-  launch(s, "prep", [&] { return kern::launch_zero_u32(gkey, nq, s); });
+  const int slots = kern::bound_slots_for(T);
+  const int mslots = (k + T - 1) / T <= slots ? (k + T - 1) / T : 0;
+  uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
+  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
-                     plan.rows_per_split, plan.nsplit, T, k, part, gkey, (int)qblocks,
+                     plan.rows_per_split, plan.nsplit, T, k, part, gkey, mslots, (int)qblocks,
                      plan.xcd ? 1 : 0};
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });

@@ -281,12 +281,13 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   // the filter: the score of K[T-1] or better (NaN -- every candidate
   // passes -- while the list has room and nothing better is known)
   float thr = score_of_key(0u);
-  // With T >= k every lane's T-th best is a lower bound on its query's k-th
-  // best score, so all lanes of a query -- in every workgroup -- filter with
-  // the best such bound any of them has published (a per-query key, raised
-  // with a relaxed atomic max; a stale read is only a weaker bound).
-  const bool share = a.k <= T;
-  uint32_t* gk = a.gkey + (qvalid ? q : 0);
+  // All lanes of a query -- in every workgroup -- filter with the shared
+  // lower bound on its k-th best score (SharedBound), raised with relaxed
+  // atomic max operations as the segment lists fill.
+  constexpr int S = bound_slots<T>();
+  const bool share = a.mslots > 0;
+  uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
+  const int myslot = share ? (2 * split + h) % a.mslots : 0;
 
   if (ntiles > 0) {
     issue_loads();
@@ -300,9 +301,10 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    // the shared key is read before the tile prefetch, so that waiting for
+    // the shared bound is read before the tile prefetch, so that waiting for
     // it (in the epilogue) does not wait for the prefetch
-    const uint32_t gseen = __hip_atomic_load(gk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    SharedBound<S> seen;
+    seen.load(gk);
     // unconditional (past the last tile the offsets are out of range and
     // read zero), so the wait counts after the shared key stay static
     issue_loads();
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
           for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[4 * j + u];
         }
       }
-      if (share) thr = fmaxf(thr, score_of_key(gseen));
+      if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
       const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
       bool inserted;
       if (t + 1 < ntiles || (nrows & (kTileRows - 1)) == 0)
@@ -348,8 +350,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       else
         inserted = select_tile<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows,
                                          stage + 20 * tid);
-      if (share && qvalid && inserted && K[T - 1] > gseen)
-        __hip_atomic_fetch_max(gk, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
+        __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_sched_barrier(0);
     store_tile(buf ^ 1);
@@ -511,8 +513,10 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
   float thr = score_of_key(0u);
-  const bool share = a.k <= T;
-  uint32_t* gk = a.gkey + (qvalid ? q : 0);
+  constexpr int S = bound_slots<T>();
+  const bool share = a.mslots > 0;
+  uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
+  const int myslot = share ? (2 * split + h) % a.mslots : 0;
 
   if (nsteps > 0) {
     issue_loads();
@@ -530,7 +534,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   int c = 0, t = 0;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
-    const uint32_t gseen = __hip_atomic_load(gk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    SharedBound<S> seen;
+    seen.load(gk);
     // the fetched tile's parity, read before store_chunk advances pc
     const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
     issue_loads();
@@ -554,7 +559,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     if (c + 1 == NC) {
       __builtin_amdgcn_sched_barrier(0);
       if (wave_on) {
-        if (share) thr = fmaxf(thr, score_of_key(gseen));
+        if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
         const int lim0 = nrows - t * kDeepRows;
         const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kDeepRows);
         bool inserted = false;
@@ -575,8 +580,9 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
           }
           inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
         }
-        if (share && qvalid && inserted && K[T - 1] > gseen)
-          __hip_atomic_fetch_max(gk, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
+          __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
       }
 #pragma unroll
       for (int r = 0; r < kDeepRB; ++r)
@@ -735,6 +741,11 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   const int orow = a.qsel[row];
   const float qn = (a.metric == kL2 && a.dist_mode == 0) ? a.qnorm[orow] : 0.0f;
   emit_topk<256>(sel, work, a.k, orow, a.metric, qn, a.dist_mode, a.ids, a.dists);
+}
+
+__global__ void bounds_init_kernel(uint32_t* p, int64_t count, int S, int m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = (int)(i % S) < m ? 0u : 0xffffffffu;
 }
 
 __global__ void zero_u32_kernel(uint32_t* p, int64_t count) {
@@ -967,6 +978,24 @@ hipError_t launch_fill(int32_t* ids, float* dists, int64_t count, float pad,
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256),
                      0, s, ids, dists, count, pad);
+  return hipGetLastError();
+}
+
+int bound_slots_for(int T) {
+  switch (T) {
+    case 4: return bound_slots<4>();
+    case 8: return bound_slots<8>();
+    case 10: return bound_slots<10>();
+    case 16: return bound_slots<16>();
+  }
+  return 1;
+}
+
+hipError_t launch_bounds_init(uint32_t* gkey, int64_t nq, int S, int m, hipStream_t s) {
+  const int64_t count = nq * S;
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(bounds_init_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
+                     s, gkey, count, S, m);
   return hipGetLastError();
 }
 

@@ -58,9 +58,10 @@ struct FusedArgs {
   int64_t rows_per_split;
   int nsplit;
   int T;                 // list length per lane
-  int k;                 // neighbours wanted (k <= T: lanes share thresholds)
+  int k;                 // neighbours wanted
   uint64_t* part;        // [nq][2*nsplit][T]
-  uint32_t* gkey;        // [nq] shared threshold keys, zeroed before the launch
+  uint32_t* gkey;        // [nq][bound_slots_for(T)] shared bounds (launch_bounds_init)
+  int mslots;            // ceil(k / T) when <= bound_slots_for(T), else 0 (no sharing)
   int nqb;               // query blocks, ceil(nq / 128)
   int xcd_major;         // nsplit % 8 == 0: XCD-major workgroup order (see kernel)
 };
@@ -127,6 +128,13 @@ struct SelectArgs {
   float* dists;
 };
 hipError_t launch_select(const SelectArgs& a, hipStream_t s);
+
+// Shared per-query bounds of the fused kernels: slots per query for list
+// length T, and their initial state for m = ceil(k / T) used slots (0 in the
+// used ones, 0xffffffff in the others).  A kernel, not a memset, so that the
+// call stays graph-capturable.
+int bound_slots_for(int T);
+hipError_t launch_bounds_init(uint32_t* gkey, int64_t nq, int S, int m, hipStream_t s);
 
 // Zero a uint32 array (a kernel, so that the call stays graph-capturable).
 hipError_t launch_zero_u32(uint32_t* p, int64_t count, hipStream_t s);

@@ -91,6 +91,55 @@ __device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
   return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
 }
 
+// Per-query shared lower bounds on the k-th best score, kept in S slots of
+// gkey[q S .. q S + S).  Segment g publishes its list's T-th best key into
+// slot g % m (m = ceil(k / T) <= S; slots m .. S - 1 hold 0xffffffff and never
+// win a min).  Every slot holds the T-th best key of one segment and the m
+// slots are fed by disjoint classes of segments, which cover disjoint rows,
+// so at least m T >= k candidates score at least the smallest slot: the
+// query's k-th best does too, and a candidate below it is never needed.  Keys
+// only grow, so a stale read is merely a weaker bound.  S = 1 serves k <= T.
+template <int T>
+constexpr int bound_slots() { return T == 16 ? 8 : 1; }
+
+template <int S>
+struct SharedBound;
+
+template <>
+struct SharedBound<1> {
+  uint32_t v;
+  __device__ __forceinline__ void load(const uint32_t* p) {
+    v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ __forceinline__ uint32_t bound() const { return v; }
+  __device__ __forceinline__ uint32_t slot(int) const { return v; }
+};
+
+template <>
+struct SharedBound<8> {
+  uint64_t w[4];
+  __device__ __forceinline__ void load(const uint32_t* p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = __hip_atomic_load((const uint64_t*)p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ __forceinline__ uint32_t bound() const {
+    uint32_t m = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m = min(m, (uint32_t)w[i]);
+      m = min(m, (uint32_t)(w[i] >> 32));
+    }
+    return m;
+  }
+  __device__ __forceinline__ uint32_t slot(int j) const {
+    uint32_t r = 0;  // a select chain: a dynamic index would go through scratch
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r = j == i ? (uint32_t)(w[i >> 1] >> (32 * (i & 1))) : r;
+    return r;
+  }
+};
+
 // In-LDS bitonic sort of P (a power of two) values, descending by `ord`.
 // All threads of the workgroup call it; it ends with a barrier.
 template <int NT, typename Ord>

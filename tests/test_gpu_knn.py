@@ -317,6 +317,20 @@ def test_deep_device_api_matches_host_api(engine):
     assert np.array_equal(dd.download((130, 10), np.float32), dist)
 
 
+@pytest.mark.parametrize("k", [10, 17, 65, 128])
+def test_fp16_integer_bit_exact(engine, oracle, k):
+    # binary16 integers in [0, 16), d = 256: scores are exact in fp32, so the
+    # fp16 MFMA path must equal the restatement bit for bit, also for k > 16
+    # where the lists share multi-slot bounds
+    rng = np.random.default_rng(41)
+    base = rng.integers(0, 16, (50_000, 256)).astype(np.float16)
+    q = rng.integers(0, 16, (300, 256)).astype(np.float16)
+    ids, dist = engine.brute_force_knn(base, q, k, "l2")
+    oid, odist = oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), k, "l2")
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(dist, odist)
+
+
 def test_c3_subset(engine, oracle):
     cen = synth.c3_centres()
     base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen), 100_000,
