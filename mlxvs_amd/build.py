@@ -56,7 +56,7 @@ def build(verbose: bool = False) -> Path:
         objs = list(pool.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs),
-           f"-Wl,--version-script={CSRC / 'exports.map'}", "-o", str(tmp)]
+           f"-Wl,--version-script={CSRC / 'exports.map'}", "-Wl,-z,defs", "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -510,6 +510,85 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
 
 // ---- Hamming path --------------------------------------------------------------------
 
+// Exact select of the listed queries over all rows, from packed words with
+// row stride `wstride` (queries the fused path cannot finish, or all).
+void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint32_t* qw,
+                        int wstride, int64_t n, const std::vector<int>& redo, int k,
+                        int32_t* ids, float* dists) {
+  int* qsel = ar.take<int>(redo.size());
+  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
+            "hipMemcpyAsync");
+  const int64_t rcount = (int64_t)redo.size();
+  const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rcount, (int64_t(1) << 28) / n));
+  float* S = ar.take<float>((size_t)per_block * n);
+  for (int64_t r0 = 0; r0 < rcount; r0 += per_block) {
+    const int cnt = (int)std::min<int64_t>(per_block, rcount - r0);
+    kern::HammingScoresArgs hs{bw, qw, qsel + r0, n, cnt, wstride, S};
+    launch(s, "hamming_scores", [&] { return kern::launch_hamming_scores(hs, s); });
+    kern::SelectArgs se{S, n, cnt, k, qsel + r0, kern::kL2, nullptr, 1, ids, dists};
+    launch(s, "select", [&] { return kern::launch_select(se, s); });
+  }
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // `redo` is released next
+}
+
+// Queries whose merge flag is set (the flags array has nq entries).
+std::vector<int> flagged(hipStream_t s, const int* flags, int64_t nq) {
+  std::vector<int> hflags((size_t)nq), redo;
+  check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
+            "hipMemcpyAsync");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  for (int64_t i = 0; i < nq; ++i)
+    if (hflags[(size_t)i]) redo.push_back((int)i);
+  return redo;
+}
+
+// Int8 MFMA route: the deep fused kernel reads packed codes and unpacks them
+// to {0, 1} bytes, whose squared L2 distance is the Hamming distance (bnorm =
+// popcounts), then the float merge finishes (L2 finalise: qpop - s = the
+// distance, exact).  Returns false when the route does not apply.
+bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
+                  int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int T = list_len_float(k);
+  // packed row: whole 16-byte chunks (128 bits), zero padded
+  const int ldb = kern::bits_row_bytes(nbytes);
+  if (ldb == 0 || nq >= (int64_t(1) << 31) || !kern::deep_bits_supported(ldb, T)) return false;
+  const int ldw = ldb / 4;
+  const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  SplitPlan plan = plan_splits(n, qblocks, k, T, 2, kern::kDeepRows,
+                               device_slots(kern::deep_bits_blocks_per_cu(T)), true);
+  // the kernel fetches up to two tiles past a split's rows
+  if (!plan.ok || (plan.rows_per_split + 2 * kern::kDeepRows) * ldb >= (int64_t(1) << 31))
+    return false;
+
+  uint32_t* bw = ar.take<uint32_t>((size_t)n * ldw);
+  uint32_t* qw = ar.take<uint32_t>((size_t)nq * ldw);
+  launch(s, "pack", [&] { return kern::launch_pack({rows, n, nbytes, bw, ldw}, s); });
+  launch(s, "pack", [&] { return kern::launch_pack({queries, nq, nbytes, qw, ldw}, s); });
+  float* bpop = ar.take<float>((size_t)n);
+  float* qpop = ar.take<float>((size_t)nq);
+  launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, s); });
+  launch(s, "pack", [&] { return kern::launch_popcount_rows(qw, nq, ldw, qpop, s); });
+
+  const int nseg = 2 * plan.nsplit;
+  uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
+  const int slots = kern::bound_slots_for(T);
+  const int mslots = (k + T - 1) / T <= slots ? (k + T - 1) / T : 0;
+  uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
+  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
+  kern::FusedArgs fa{bw, qw, bpop, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,
+                     plan.nsplit, T, k, part, gkey, mslots, (int)qblocks, plan.xcd ? 1 : 0};
+  launch(s, "hamming_mfma", [&] { return kern::launch_deep_bits(fa, s); });
+  int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
+  kern::MergeArgs ma{part, nseg, T, k, (int)nq, kern::kL2, qpop, 0, ids, dists, flags};
+  launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+  if (T >= k) return true;
+  const std::vector<int> redo = flagged(s, flags, nq);
+  if (!redo.empty()) hamming_exhaustive(ar, s, bw, qw, ldw, n, redo, k, ids, dists);
+  return true;
+}
+
 void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
              int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
   Arena& ar = ss.arena();
@@ -519,6 +598,7 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
     launch(s, "fill", [&] { return kern::launch_fill(ids, dists, nq * k, INFINITY, s); });
     return;
   }
+  if (hamming_bits(ss, rows, n, queries, nq, nbytes, k, ids, dists)) return;
   const int W = (nbytes + 3) / 4;
   const int T = list_len_hamming(k);
   const int Wp = kern::hamming_padded_words(W);
@@ -541,31 +621,13 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
     kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     if (T >= k) return;
-    std::vector<int> hflags((size_t)nq);
-    check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
-              "hipMemcpyAsync");
-    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-    for (int64_t i = 0; i < nq; ++i)
-      if (hflags[(size_t)i]) redo.push_back((int)i);
+    redo = flagged(s, flags, nq);
     if (redo.empty()) return;
   } else {
     redo.resize((size_t)nq);
     for (int64_t i = 0; i < nq; ++i) redo[(size_t)i] = (int)i;
   }
-  int* qsel = ar.take<int>(redo.size());
-  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
-            "hipMemcpyAsync");
-  const int64_t rcount = (int64_t)redo.size();
-  const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rcount, (int64_t(1) << 28) / n));
-  float* S = ar.take<float>((size_t)per_block * n);
-  for (int64_t r0 = 0; r0 < rcount; r0 += per_block) {
-    const int cnt = (int)std::min<int64_t>(per_block, rcount - r0);
-    kern::HammingScoresArgs hs{bw, qw, qsel + r0, n, cnt, wstride, S};
-    launch(s, "hamming_scores", [&] { return kern::launch_hamming_scores(hs, s); });
-    kern::SelectArgs se{S, n, cnt, k, qsel + r0, kern::kL2, nullptr, 1, ids, dists};
-    launch(s, "select", [&] { return kern::launch_select(se, s); });
-  }
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  hamming_exhaustive(ar, s, bw, qw, wstride, n, redo, k, ids, dists);
 }
 
 // ---- host <-> device helpers ----------------------------------------------------

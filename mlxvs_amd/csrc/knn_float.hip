@@ -382,31 +382,6 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 // holds rows 32 rb + 8 (i / 4) + 4 h + i % 4: tile position bit 2 is h, so
 // the segments are those of fused_kernel (2 split + h).
 
-// Inserts the scores of one 32-row block (rows id0 + 8 (i / 4) + 4 h + i % 4,
-// the first `lim` of the block real) that pass the lane's threshold.  One
-// position at a time, skipped when no lane of the wavefront passes it, so the
-// ids reach the list in increasing order.
-template <int T>
-__device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
-                                             const float (&sc)[16], int h, uint32_t id0,
-                                             int lim) {
-  bool any = false;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    any |= (m < lim) & !(sc[i] < thr);
-  }
-  if (__builtin_amdgcn_ballot_w64(any) == 0) return false;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    const bool p = (m < lim) & !(sc[i] < thr);
-    if (__builtin_amdgcn_ballot_w64(p) != 0) stream_insert<T>(K, I, p ? key_nz(sc[i]) : 0u, id0 + m);
-  }
-  thr = fmaxf(thr, score_of_key(K[T - 1]));
-  return any;
-}
-
 constexpr int kDeepChunk = 32;                 // dims per LDS stage
 constexpr int kDeepStride = kDeepChunk + 4;    // 16-byte pad: 8 rows hit distinct bank quads
 constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront

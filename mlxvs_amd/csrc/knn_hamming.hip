@@ -112,6 +112,257 @@ __global__ void pack_kernel(PackArgs a) {
   a.words[e] = v;
 }
 
+// ---- int8 MFMA route: packed codes unpacked to {0, 1} bytes in LDS ---------------
+//
+// For {0, 1} vectors the squared L2 distance is the Hamming distance and
+// sum b_i^2 is popcount(b), so the k-NN is the L2 one: s = 2 q.b - pop(b)
+// selected largest first, distance pop(q) - s.  The dot products run on
+// v_mfma_i32_32x32x32_i8 (exact int32 sums).  Workgroup and tile as the deep
+// fp32 kernel: 128 queries (wavefront w: queries 32 w ..), 128-row tiles,
+// four 32 x 32 accumulators per wavefront, a K loop over 128-bit chunks of
+// the codes.  The codes travel packed (16 bytes per row and chunk) and each
+// chunk is unpacked into the LDS buffer that the MFMAs read:
+//  * threads 0-127 own a base row each; they hold its NCT packed chunks in
+//    registers and refetch chunk j for the next tile as soon as chunk j of
+//    the current tile is unpacked, so every fetch has a whole tile to land;
+//  * threads 128-255 own a query each and keep its packed code in registers
+//    for the whole kernel.
+// The chunk loop is unrolled over the tile, so every register index is
+// static.  A bound is published with a returning atomic whose result is
+// read a tile later: pending memory events stay reads, and the waits for the
+// refetches keep counting instead of draining.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBitsRows = kDeepRows;
+constexpr int kBitsStride = 36;  // dwords per unpacked LDS row: 128 bytes + 16 pad
+
+// 128 bits -> 128 {0, 1} bytes: dword 8 w + m holds bits 8 j + m of word w
+// in its bytes j.  Rows and queries use the same order, so the dot products
+// are those of the codes.
+__device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t v = x[w];
+    *(u32x4*)(dst + 8 * w) = u32x4{v & 0x01010101u, (v >> 1) & 0x01010101u,
+                                   (v >> 2) & 0x01010101u, (v >> 3) & 0x01010101u};
+    *(u32x4*)(dst + 8 * w + 4) = u32x4{(v >> 4) & 0x01010101u, (v >> 5) & 0x01010101u,
+                                       (v >> 6) & 0x01010101u, (v >> 7) & 0x01010101u};
+  }
+}
+
+template <int NCT, int T>
+__global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
+  __shared__ __align__(16) uint32_t tA[2][kBitsRows * kBitsStride];
+  __shared__ __align__(16) uint32_t tQ[2][kQueriesPerBlock * kBitsStride];
+  __shared__ __align__(16) float tnorm[2][kBitsRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  int split, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_major) {
+      const int slot = id >> 3;
+      split = (id & 7) + 8 * (slot / a.nqb);
+      qb = slot % a.nqb;
+    } else {
+      split = id % a.nsplit;
+      qb = id / a.nsplit;
+    }
+  }
+  const int qb0 = qb * kQueriesPerBlock;
+  const int q = qb0 + wave * 32 + col;
+  const bool wave_on = qb0 + wave * 32 < a.nq;
+  const bool qvalid = q < a.nq;
+  constexpr int ldb = 16 * NCT;  // packed row bytes
+
+  const int64_t r0 = (int64_t)split * a.rows_per_split;
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+  const int ntiles = (nrows + kBitsRows - 1) / kBitsRows;
+
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)a.base + r0 * ldb), (short)0, nrows * ldb, 0x00020000);
+  const int qrows = min(kQueriesPerBlock, a.nq - qb0);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)a.queries + (int64_t)qb0 * ldb), (short)0, qrows * ldb, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.bnorm + r0), (short)0, nrows * 4, 0x00020000);
+
+  const bool row_role = __builtin_amdgcn_readfirstlane(wave) < 2;
+  const int idx = tid & 127;
+  uint32_t* const myA0 = &tA[0][idx * kBitsStride];
+  uint32_t* const myQ0 = &tQ[0][idx * kBitsStride];
+  constexpr int kBuf = kBitsRows * kBitsStride;  // dwords per LDS buffer
+
+  // Packed chunks of the thread's row (of the tile being fetched) or query;
+  // out-of-range rows read zero.  Every thread runs the same fetches (query
+  // threads refetch their own, unchanged chunks and a norm they never use),
+  // so the wait counts are the same on every path.
+  u32x4 pk[NCT];
+  uint32_t pn = 0;
+  const __amdgpu_buffer_rsrc_t rf = row_role ? rb : rq;
+  uint32_t roff = (uint32_t)(idx * ldb);  // the row in the tile being fetched
+  const uint32_t rstep = row_role ? (uint32_t)(kBitsRows * ldb) : 0u;
+  uint32_t noff = (uint32_t)(idx * 4);
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) pk[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * c, 0, 0);
+  pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+  roff += rstep;
+  noff += kBitsRows * 4;
+
+  uint32_t K[T], I[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  float thr = score_of_key(0u);
+  constexpr int S = bound_slots<T>();
+  const bool share = a.mslots > 0;
+  const bool share1 = a.mslots == 1;
+  uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
+  const int myslot = share ? (2 * split + h) % a.mslots : 0;
+  uint32_t pend = 0;  // slot value returned by the last publish (used a tile later)
+
+  // chunk 0 of tile 0, then the refetch of chunk 0 for tile 1
+  unpack_chunk(row_role ? myA0 : myQ0, pk[0]);
+  if (row_role) tnorm[0][idx] = __uint_as_float(pn);
+  pk[0] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff, 0, 0);
+  pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+  __syncthreads();
+
+  i32x16 acc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[r][i] = 0;
+
+  int par = 0;  // LDS buffer of the current chunk
+  for (int t = 0; t < ntiles; ++t) {
+    SharedBound<S> seen;
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      if (c == 0) seen.load(gk);
+      const int buf = (NCT % 2 == 0) ? (c & 1) : par;
+      if (wave_on) {
+        const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 16 * h];
+        const uint32_t* arow = &tA[buf][col * kBitsStride + 16 * h];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const i32x4 bq = *(const i32x4*)(qrow + 4 * v);
+          i32x4 av[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) av[r] = *(const i32x4*)(arow + r * 32 * kBitsStride + 4 * v);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[r], bq, acc[r], 0, 0, 0);
+        }
+      }
+      // the next chunk (j of this tile, or chunk 0 of the next) into the
+      // other buffer, then the row refetch of chunk j one tile further
+      const int j = (c + 1) % NCT;
+      const int nb = buf ^ 1;
+      unpack_chunk((row_role ? myA0 : myQ0) + nb * kBuf, pk[j]);
+      if (c == NCT - 1 && row_role) tnorm[(t + 1) & 1][idx] = __uint_as_float(pn);
+      if (j == 0) {
+        roff += rstep;
+        noff += kBitsRows * 4;
+      }
+      pk[j] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * j, 0, 0);
+      if (j == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+      if (c == NCT - 1) {
+        if (wave_on) {
+          if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
+          if (share1) thr = fmaxf(thr, score_of_key(pend));
+          const int lim0 = nrows - t * kBitsRows;
+          const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kBitsRows);
+          bool inserted = false;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float sc[16];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              const floatx4 nbv = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * jj + 4 * h];
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+                sc[4 * jj + w] = __builtin_fmaf(2.0f, (float)acc[r][4 * jj + w], -nbv[w]);
+            }
+            inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+          }
+          if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
+            pend = __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[r][i] = 0;
+      }
+      par ^= 1;
+      __syncthreads();
+    }
+  }
+
+  if (qvalid) {
+    uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
+#pragma unroll
+    for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
+  }
+}
+
+template <int NCT, int T>
+int bits_occupancy() {
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, bits_kernel<NCT, T>, 256, 0) !=
+      hipSuccess)
+    return 1;
+  return blocks;
+}
+
+template <int NCT>
+int bits_occupancy_t(int T) {
+  switch (T) {
+    case 4: return bits_occupancy<NCT, 4>();
+    case 8: return bits_occupancy<NCT, 8>();
+    case 10: return bits_occupancy<NCT, 10>();
+    case 16: return bits_occupancy<NCT, 16>();
+  }
+  return 1;
+}
+
+template <int NCT>
+hipError_t bits_dispatch_t(const FusedArgs& a, hipStream_t s) {
+  const dim3 grid(a.nsplit * a.nqb);
+  switch (a.T) {
+    case 4: hipLaunchKernelGGL((bits_kernel<NCT, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((bits_kernel<NCT, 8>), grid, dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((bits_kernel<NCT, 10>), grid, dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((bits_kernel<NCT, 16>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Popcounts of 64 rows per workgroup: one thread per (row, word), summed in
+// LDS.
+constexpr int kPopRows = 64;
+__global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* words, int64_t n,
+                                                            int W, float* out) {
+  __shared__ int pop[kPopRows];
+  const int64_t row0 = (int64_t)blockIdx.x * kPopRows;
+  if (threadIdx.x < kPopRows) pop[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t rows = min((int64_t)kPopRows, n - row0);
+  for (int64_t e = threadIdx.x; e < rows * W; e += 256) {
+    const uint32_t x = words[row0 * W + e];
+    if (x) atomicAdd(&pop[e / W], __popc(x));
+  }
+  __syncthreads();
+  if (threadIdx.x < rows) out[row0 + threadIdx.x] = (float)pop[threadIdx.x];
+}
+
 template <int W, int T>
 hipError_t launch_inst(const HammingArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, (a.nq + kHammingQueriesPerBlock - 1) / kHammingQueriesPerBlock);
@@ -200,6 +451,39 @@ hipError_t launch_hamming_scores(const HammingScoresArgs& a, hipStream_t s) {
   if (a.rows <= 0 || a.n <= 0) return hipSuccess;
   dim3 grid((unsigned)((a.n + 255) / 256), a.rows);
   hipLaunchKernelGGL(hamming_scores_kernel, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// Packed row lengths (bytes) with a bits_kernel instance: 16 NCT.
+int bits_row_bytes(int nbytes) {
+  for (int nct = 1; nct <= 16; nct *= 2)
+    if (nbytes <= 16 * nct) return 16 * nct;
+  return 0;
+}
+
+bool deep_bits_supported(int ld, int T) {
+  return bits_row_bytes(ld) == ld && ld >= 16 && (T == 4 || T == 8 || T == 10 || T == 16);
+}
+
+int deep_bits_blocks_per_cu(int T) { return bits_occupancy_t<8>(T); }
+
+hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s) {
+  if (!deep_bits_supported(a.ld, a.T) || a.metric != kL2) return hipErrorInvalidValue;
+  switch (a.ld / 16) {
+    case 1: return bits_dispatch_t<1>(a, s);
+    case 2: return bits_dispatch_t<2>(a, s);
+    case 4: return bits_dispatch_t<4>(a, s);
+    case 8: return bits_dispatch_t<8>(a, s);
+    case 16: return bits_dispatch_t<16>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_popcount_rows(const uint32_t* words, int64_t n, int W, float* pop,
+                                hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(popcount_rows_kernel, dim3((unsigned)((n + kPopRows - 1) / kPopRows)),
+                     dim3(256), 0, s, words, n, W, pop);
   return hipGetLastError();
 }
 

@@ -79,6 +79,17 @@ constexpr int kDeepRows = 128;
 hipError_t launch_deep(const FusedArgs& a, hipStream_t s);
 bool deep_supported(int ld, int T, bool f16);
 int deep_blocks_per_cu(int T);
+// The same arguments, segments and output over bit codes (knn_hamming.hip):
+// base / queries packed little-endian words, ld = packed row length in bytes
+// (bits_row_bytes: 16, 32, 64, 128 or 256, zero padded), bnorm the rows'
+// popcounts as floats, metric kL2.  The kernel unpacks the bits to {0, 1}
+// bytes in LDS; for {0, 1} vectors the squared L2 distance is the Hamming
+// distance, and every product and sum is exact on the int8 MFMA.
+hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s);
+bool deep_bits_supported(int ld, int T);
+int deep_bits_blocks_per_cu(int T);
+// the packed row length with an instance for nbytes-byte codes (0: none)
+int bits_row_bytes(int nbytes);
 
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.
@@ -152,6 +163,10 @@ struct PackArgs {
   int wp;                // words per packed row, >= ceil(nbytes / 4)
 };
 hipError_t launch_pack(const PackArgs& a, hipStream_t s);
+
+// Popcounts of packed rows [n, W] as floats.
+hipError_t launch_popcount_rows(const uint32_t* words, int64_t n, int W, float* pop,
+                                hipStream_t s);
 
 struct HammingArgs {
   const uint32_t* base;    // [n, W]

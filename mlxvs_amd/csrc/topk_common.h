@@ -86,6 +86,48 @@ __device__ __forceinline__ void stream_insert(uint32_t (&K)[T], uint32_t (&I)[T]
   }
 }
 
+// sc[i] for a per-lane i in [0, 16): a select tree on the bits of i.
+__device__ __forceinline__ float pick16(const float (&sc)[16], int i) {
+  const bool b0 = i & 1, b1 = i & 2, b2 = i & 4, b3 = i & 8;
+  const float a0 = b0 ? sc[1] : sc[0], a1 = b0 ? sc[3] : sc[2];
+  const float a2 = b0 ? sc[5] : sc[4], a3 = b0 ? sc[7] : sc[6];
+  const float a4 = b0 ? sc[9] : sc[8], a5 = b0 ? sc[11] : sc[10];
+  const float a6 = b0 ? sc[13] : sc[12], a7 = b0 ? sc[15] : sc[14];
+  const float c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2, c2 = b1 ? a5 : a4, c3 = b1 ? a7 : a6;
+  const float d0 = b2 ? c1 : c0, d1 = b2 ? c3 : c2;
+  return b3 ? d1 : d0;
+}
+
+// Inserts the scores of one 32-row block (rows id0 + 8 (i / 4) + 4 h + i % 4,
+// the first `lim` of the block real) that pass the lane's threshold.  Every
+// lane drains its own bitmask of passing positions, lowest first (so ids
+// reach the list in increasing order); the loop runs as often as the busiest
+// lane needs, and a lane with nothing left inserts the empty key.  A lane's
+// score at its position comes out of a 4-level select tree on the position
+// bits (no dynamic register index).  Returns whether the lane kept any.
+template <int T>
+__device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                             const float (&sc)[16], int h, uint32_t id0,
+                                             int lim) {
+  uint32_t pm = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    pm |= ((m < lim) & !(sc[i] < thr)) ? (1u << i) : 0u;
+  }
+  if (__builtin_amdgcn_ballot_w64(pm != 0) == 0) return false;
+  const bool any = pm != 0;
+  do {
+    const int i = pm ? __builtin_ctz(pm) : 0;
+    const float v = pick16(sc, i);
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    stream_insert<T>(K, I, pm ? key_nz(v) : 0u, id0 + m);
+    pm &= pm - 1u;
+  } while (__builtin_amdgcn_ballot_w64(pm != 0) != 0);
+  thr = fmaxf(thr, score_of_key(K[T - 1]));  // NaN while the list has room
+  return any;
+}
+
 // The rank (see rank_of) of a stream-list slot, 0 for an empty one.
 __device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
   return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
