@@ -12,11 +12,13 @@ MFMA distance + top-k, merge).  W warm-up steps, then exactly K timed steps
 between two device synchronisations; value = queries answered per second.
 
 The same JSON line carries:
-  roofline      the fused kernel's achieved FP32 MFMA rate, from HIP events
+  roofline      the dominant kernel's achieved MFMA rate, from HIP events
                 recorded around each of its launches inside the timed steps
-                (2 nq n d flops per launch over its mean duration), against
-                MI355X's 157.3 TFLOP/s; traffic = HBM bytes per launch from the
-                committed rocprofv3 counter summary when present;
+                (2 nq n d flops per launch over its mean duration; for Hamming
+                2 nq n bits int8 ops), against MI355X's dense peak of that
+                type (FP32 157.3, FP16 2516.6 TFLOP/s, INT8 5033.2 TOP/s);
+                traffic = HBM bytes per launch from the committed rocprofv3
+                counter summary when present;
   cpu_baseline  the CPU restatement of the reference path (oracle/, a port:
                 the reference itself runs only on Apple GPUs) timed on this
                 host's cores over a bounded query sample;
@@ -47,6 +49,7 @@ METRIC = ("queries/s, exact kNN k=10 on 1M×128 fp32 (10k queries); "
           "% of MFMA/HBM roofline")
 PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense FP32 matrix
 PEAK_FP16_MFMA = 2516.6  # TFLOP/s, MI355X dense FP16 matrix
+PEAK_INT8_MFMA = 5033.2  # TOP/s, MI355X dense INT8 matrix
 PEAK_HBM = 8000.0        # GB/s
 VALU_LANE_OPS = 256 * 64 * 2.4e9  # non-packed VALU lane-ops per second
 
@@ -199,7 +202,13 @@ def main() -> int:
     kname = max(stages, key=lambda s_: stages[s_][1])
     cnt, tot = stages[kname]
     per = tot / max(cnt, 1) / 1e3  # seconds per launch
-    if w["kind"] == "hamming":
+    if w["kind"] == "hamming" and kname == "hamming_mfma":
+        # the int8 MFMA route: 2 ops (multiply, add) per code bit and pair
+        ops = 2.0 * nq * n * 8 * d / (cnt / args.steps)  # per launch
+        roof = {"bound": "mfma", "achieved": round(ops / per / 1e12, 2),
+                "peak": PEAK_INT8_MFMA, "unit": "TOP/s"}
+    elif w["kind"] == "hamming":
+        # the popcount route: XOR + popcount-accumulate per 32-bit word
         words = (d + 3) // 4
         work = nq * n * words * 2.0 / (cnt / args.steps)  # per launch
         roof = {"bound": "valu", "achieved": round(work / per / 1e12, 3),
@@ -238,7 +247,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if base.dtype == np.float16 else ("u32" if w["kind"] == "hamming" else "f32"),
+        "dtype": "f16" if base.dtype == np.float16 else ("i8" if w["kind"] == "hamming" else "f32"),
         "data": "synthetic (mlxvs_amd.synth, seeded splitmix64)",
         "config": {"workload": w["desc"], "n": n, "nq": nq, "d": d, "k": k,
                    "metric": w["metric"], "parallelism": "single GPU"},

@@ -156,7 +156,7 @@ class Arena {
       size_t total = 0;
       for (auto& c : chunks_) {
         total += c.size;
-        hipFree(c.ptr);
+        (void)hipFree(c.ptr);
       }
       chunks_.clear();
       char* p = nullptr;
@@ -165,10 +165,28 @@ class Arena {
     }
   }
 
+  // Pinned host memory for small device-to-host reads (the merge's flags),
+  // kept across calls; a copy into pageable memory goes through a staged,
+  // slower path.
+  int* host_ints(size_t count) {
+    if (count > host_count_) {
+      if (host_) (void)hipHostFree(host_);
+      host_ = nullptr;
+      host_count_ = 0;
+      check_hip(hipHostMalloc((void**)&host_, count * sizeof(int), hipHostMallocDefault),
+                "hipHostMalloc");
+      host_count_ = count;
+    }
+    return host_;
+  }
+
   void release() {
-    if (done_) hipEventSynchronize(done_);
-    for (auto& c : chunks_) hipFree(c.ptr);
+    if (done_) (void)hipEventSynchronize(done_);
+    for (auto& c : chunks_) (void)hipFree(c.ptr);
     chunks_.clear();
+    if (host_) (void)hipHostFree(host_);
+    host_ = nullptr;
+    host_count_ = 0;
   }
 
  private:
@@ -179,6 +197,8 @@ class Arena {
   };
   std::vector<Chunk> chunks_;
   hipEvent_t done_ = nullptr;
+  int* host_ = nullptr;
+  size_t host_count_ = 0;
 };
 
 std::mutex g_mutex;
@@ -337,6 +357,18 @@ struct FloatInputs {
 
 // Exhaustive exact k-NN for the queries listed in qsel (device ints), on
 // fp32 rows of stride ld.
+// Queries whose merge flag is set (the flags array has nq entries).
+std::vector<int> flagged(Arena& ar, hipStream_t s, const int* flags, int64_t nq) {
+  int* hflags = ar.host_ints((size_t)nq);
+  std::vector<int> redo;
+  check_hip(hipMemcpyAsync(hflags, flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
+            "hipMemcpyAsync");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  for (int64_t i = 0; i < nq; ++i)
+    if (hflags[i]) redo.push_back((int)i);
+  return redo;
+}
+
 void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
                       const float* queries, int ld, const float* bnorm,
                       const float* qnorm, int64_t n, int d, int metric,
@@ -489,13 +521,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   if (T >= k) return;
 
   // k > T: queries whose lists may have dropped a member go exhaustive.
-  std::vector<int> hflags((size_t)nq);
-  check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
-            "hipMemcpyAsync");
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-  std::vector<int> redo;
-  for (int64_t i = 0; i < nq; ++i)
-    if (hflags[(size_t)i]) redo.push_back((int)i);
+  const std::vector<int> redo = flagged(ar, s, flags, nq);
   if (redo.empty()) return;
   const float *eb, *eq;
   fp32_rows(kbase, n, &eb);
@@ -531,16 +557,6 @@ void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // `redo` is released next
 }
 
-// Queries whose merge flag is set (the flags array has nq entries).
-std::vector<int> flagged(hipStream_t s, const int* flags, int64_t nq) {
-  std::vector<int> hflags((size_t)nq), redo;
-  check_hip(hipMemcpyAsync(hflags.data(), flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
-            "hipMemcpyAsync");
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-  for (int64_t i = 0; i < nq; ++i)
-    if (hflags[(size_t)i]) redo.push_back((int)i);
-  return redo;
-}
 
 // Int8 MFMA route: the deep fused kernel reads packed codes and unpacks them
 // to {0, 1} bytes, whose squared L2 distance is the Hamming distance (bnorm =
@@ -584,7 +600,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   kern::MergeArgs ma{part, nseg, T, k, (int)nq, kern::kL2, qpop, 0, ids, dists, flags};
   launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
   if (T >= k) return true;
-  const std::vector<int> redo = flagged(s, flags, nq);
+  const std::vector<int> redo = flagged(ar, s, flags, nq);
   if (!redo.empty()) hamming_exhaustive(ar, s, bw, qw, ldw, n, redo, k, ids, dists);
   return true;
 }
@@ -621,7 +637,7 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
     kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     if (T >= k) return;
-    redo = flagged(s, flags, nq);
+    redo = flagged(ar, s, flags, nq);
     if (redo.empty()) return;
   } else {
     redo.resize((size_t)nq);
