@@ -96,6 +96,16 @@ MLXVS_API void knn_self_graph_device(const Rows& rows, int k, Metric metric,
                                      int32_t* ids, float* distances,
                                      void* stream = nullptr);
 
+/**
+ * The m nearest centroids of every row of x, nearest first (squared L2,
+ * lowest index among equal distances): int32 labels [n, m], row-major.
+ * 1 <= m <= min(clusters, 256).  The same GEMM + select as brute_force_knn
+ * with the centroids as base rows.  `tile_rows` is accepted and unused.
+ * Replaces reference include/mlxvs/mlxvs.h:89-99 (src/kmeans.cpp:136-169).
+ */
+MLXVS_API std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m = 1,
+                                              int tile_rows = 65536, void* stream = nullptr);
+
 /** Frees the per-device workspace kept between calls. */
 MLXVS_API void release_workspace();
 

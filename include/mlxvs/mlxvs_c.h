@@ -143,6 +143,24 @@ MLXVS_C_API int mlxvs_knn_self_graph(
     float* distances);
 
 /**
+ * The m nearest centroids of every row: labels int32 [n, m], nearest first
+ * (squared L2, lowest index among equal distances).  x [n, d] and
+ * centroids [c, d] are float32 (f16 == 0) or binary16 (f16 != 0) host
+ * arrays; 1 <= m <= min(c, 256).  Extension: exposes mlxvs::kmeans_predict
+ * (reference include/mlxvs/mlxvs.h:89-99, src/kmeans.cpp:136-169), which the
+ * reference binds to C++ and Python only.
+ */
+MLXVS_C_API int mlxvs_kmeans_predict(
+    const void* x,
+    int64_t n,
+    const void* centroids,
+    int64_t c,
+    int32_t d,
+    int32_t f16,
+    int32_t m,
+    int32_t* labels);
+
+/**
  * mlxvs_brute_force_knn on device memory: base [n, d] and queries [nq, d]
  * float32 (f16 == 0) or binary16 (f16 != 0), outputs ids / distances
  * [nq, k] in device memory (distances may be NULL).  Enqueued on stream.

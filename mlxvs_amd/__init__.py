@@ -27,9 +27,11 @@ import numpy as np
 
 __all__ = [
     "Metric",
+    "NearestNeighbors",
     "all_neighbors",
     "brute_force_knn",
     "hamming_knn",
+    "kmeans_predict",
     "library_path",
 ]
 __version__ = "0.16.1"
@@ -59,6 +61,7 @@ def _load():
         "mlxvs_brute_force_knn_f16": [vp, i64, vp, i64, i32, i32, ctypes.c_int, vp, vp],
         "mlxvs_hamming_knn": [vp, i64, vp, i64, i32, i32, vp, vp],
         "mlxvs_knn_self_graph": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp],
+        "mlxvs_kmeans_predict": [vp, i64, vp, i64, i32, i32, i32, vp],
         "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
@@ -221,6 +224,33 @@ def all_neighbors(rows, k, metric=Metric.l2, *, algo="brute_force", n_clusters=1
     return ids, dist
 
 
+def kmeans_predict(x, centroids, m=1, *, tile_rows=65536, stream=None):
+    """The ``m`` nearest centroids of every row, nearest first.
+
+    Mirrors reference python/bindings.cpp:111-139 (src/kmeans.cpp:136-169):
+    ``x`` [n, d] and ``centroids`` [c, d] of any real dtype (float16 when
+    both are, else float32), ``1 <= m <= clusters`` (at most 256 here).
+    Squared L2 with the lowest centroid index first among equal distances
+    (the reference's argmin for m = 1).  Returns int32 ``[n, m]``.
+    """
+    op = "mlxvs::kmeans_predict"
+    xa = _rows(x, "x", op)
+    ca = _rows(centroids, "centroids", op)
+    if xa.shape[1] != ca.shape[1]:
+        raise ValueError(f"[{op}] x and centroids must have the same number of columns.")
+    m = int(m)
+    if xa.dtype == np.float16 and ca.dtype == np.float16:
+        xa, ca, f16 = np.ascontiguousarray(xa), np.ascontiguousarray(ca), 1
+    else:
+        xa = np.ascontiguousarray(xa, dtype=np.float32)
+        ca = np.ascontiguousarray(ca, dtype=np.float32)
+        f16 = 0
+    labels = np.empty((xa.shape[0], max(m, 0)), dtype=np.int32)
+    _check(_L().mlxvs_kmeans_predict(_ptr(xa), xa.shape[0], _ptr(ca), ca.shape[0], xa.shape[1],
+                                     f16, m, _ptr(labels)))
+    return labels
+
+
 def brute_force_knn_device(base_ptr, n, queries_ptr, nq, d, k, metric, ids_ptr,
                            dist_ptr, *, f16=False, stream=None):
     """mlxvs_brute_force_knn_device on device pointers (ints); enqueues only."""
@@ -265,3 +295,6 @@ def release_workspace() -> None:
 
 def version() -> str:
     return _L().mlxvs_version().decode()
+
+
+from mlxvs_amd.neighbors import NearestNeighbors  # noqa: E402  (uses the functions above)

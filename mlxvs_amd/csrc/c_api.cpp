@@ -114,6 +114,18 @@ int mlxvs_knn_self_graph(const void* rows, int64_t n, int32_t d, int32_t f16, in
   });
 }
 
+int mlxvs_kmeans_predict(const void* x, int64_t n, const void* centroids, int64_t c,
+                         int32_t d, int32_t f16, int32_t m, int32_t* labels) {
+  return guarded([&] {
+    require(labels != nullptr, "labels must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto xr = host_rows(x, n, d, t);
+    auto cr = host_rows(centroids, c, d, t);
+    auto r = mlxvs::kmeans_predict(xr, cr, m);
+    if (!r.empty()) std::memcpy(labels, r.data(), r.size() * sizeof(int32_t));
+  });
+}
+
 int mlxvs_brute_force_knn_device(const void* base, int64_t n, const void* queries,
                                  int64_t nq, int32_t d, int32_t f16, int32_t k,
                                  mlxvs_metric metric, int32_t* ids, float* distances,

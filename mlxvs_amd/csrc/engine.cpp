@@ -764,6 +764,36 @@ void brute_force_knn_device(const Rows& base, const Rows& queries, int k, Metric
             k, (int)metric, ids, dists);
 }
 
+std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m,
+                                    int tile_rows, void* stream) {
+  const char* op = "mlxvs::kmeans_predict";
+  (void)tile_rows;
+  check_rows(x, op, "x");
+  check_rows(centroids, op, "centroids");
+  if (x.dtype == Dtype::Uint8 || centroids.dtype == Dtype::Uint8)
+    invalid(op, "rows must be float32 or float16.");
+  // reference src/kmeans.cpp:143-153
+  if (x.d != centroids.d) invalid(op, "x and centroids must have the same number of columns.");
+  if (m < 1 || m > centroids.n) invalid(op, "1 <= m <= clusters");
+  if (m > kern::kMaxK) invalid(op, "m must be at most 256.");
+  if (x.dtype != centroids.dtype) invalid(op, "x and centroids must have the same dtype.");
+  std::vector<int32_t> labels((size_t)(x.n * m));
+  if (x.n == 0) return labels;
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const void* dc = upload(ar, s, centroids);
+  const void* dx = upload(ar, s, x);
+  int32_t* ids = ar.take<int32_t>((size_t)x.n * m);
+  float* dists = ar.take<float>((size_t)x.n * m);
+  float_knn(ss, {dc, dx, centroids.n, x.n, x.d, x.dtype == Dtype::Float16}, m, kern::kL2, ids,
+            dists);
+  check_hip(hipMemcpyAsync(labels.data(), ids, sizeof(int32_t) * x.n * m, hipMemcpyDeviceToHost,
+                           s), "hipMemcpyAsync (labels)");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return labels;
+}
+
 Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k, void* stream) {
   const char* op = "mlxvs::hamming_knn";
   hamming_args(rows, queries, k, op);

@@ -1,0 +1,231 @@
+"""CPU checks of the front ends around the k-NN path: vector files, cuVS index
+files, argument validation of NearestNeighbors / kmeans_predict / the cuVS
+brute-force index.  No GPU call is made here.
+
+The cuVS records are pinned against NumPy's own ``.npy`` format-1.0 reader
+(numpy.lib.format), which parses every record this build writes, and against
+the layout the reference's test checks (python/tests/test_cuvs.py:214-221).
+"""
+
+import io
+
+import numpy as np
+import numpy.lib.format as npf
+import pytest
+
+import mlxvs_amd
+from mlxvs_amd import formats
+from mlxvs_amd.cuvs import _serialize as ser
+from mlxvs_amd.cuvs.neighbors import brute_force
+
+
+# ---- .fvecs / .ivecs / .bvecs ------------------------------------------------------
+
+@pytest.mark.parametrize("kind,dtype", [("fvecs", np.float32), ("ivecs", np.int32),
+                                        ("bvecs", np.uint8)])
+def test_vecs_round_trip_and_layout(tmp_path, kind, dtype):
+    rng = np.random.default_rng(1)
+    a = (rng.standard_normal((7, 5)) * 100).astype(dtype)
+    path = tmp_path / f"x.{kind}"
+    getattr(formats, f"write_{kind}")(path, a)
+    raw = path.read_bytes()
+    item = np.dtype(dtype).itemsize
+    assert len(raw) == 7 * (4 + 5 * item)
+    # every record: int32 little-endian dimension, then the components
+    for r in range(7):
+        rec = raw[r * (4 + 5 * item):(r + 1) * (4 + 5 * item)]
+        assert int.from_bytes(rec[:4], "little") == 5
+        assert rec[4:] == a[r].astype(np.dtype(dtype).newbyteorder("<")).tobytes()
+    b = getattr(formats, f"read_{kind}")(path)
+    assert b.dtype == dtype and np.array_equal(a, b)
+
+
+def test_vecs_rejects_malformed(tmp_path):
+    p = tmp_path / "bad.fvecs"
+    p.write_bytes((3).to_bytes(4, "little") + b"\0" * 10)
+    with pytest.raises(ValueError):
+        formats.read_fvecs(p)
+    p.write_bytes((2).to_bytes(4, "little") + b"\0" * 8 + (3).to_bytes(4, "little") + b"\0" * 8)
+    with pytest.raises(ValueError):
+        formats.read_fvecs(p)
+
+
+def test_reference_ivecs_layout(tmp_path):
+    # reference examples/ground_truth.py:25-30: out[:, 0] = k, out[:, 1:] = ids
+    ids = np.arange(12, dtype=np.int32).reshape(3, 4)
+    p = tmp_path / "gt.ivecs"
+    formats.write_ivecs(p, ids)
+    want = np.empty((3, 5), np.int32)
+    want[:, 0] = 4
+    want[:, 1:] = ids
+    assert p.read_bytes() == want.astype("<i4").tobytes()
+
+
+# ---- cuVS records ------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, np.int8, np.uint8, np.int32,
+                                   np.uint32, np.int64, np.uint64, np.float64])
+@pytest.mark.parametrize("shape", [(), (0,), (5,), (3, 4), (2, 3, 4), (123456, 7)])
+def test_records_parse_with_numpy(dtype, shape):
+    buf = io.BytesIO()
+    if shape == ():
+        ser.write_scalar(buf, 3, dtype)
+    else:
+        ser.write_array(buf, np.zeros(shape, dtype))
+    raw = buf.getvalue()
+    if dtype == np.float16:
+        # RAFT spells binary16 "<e2", which NumPy's reader does not know;
+        # "<f2" has the same length
+        assert b"'descr': '<e2'" in raw
+        raw = raw.replace(b"'<e2'", b"'<f2'")
+    f = io.BytesIO(raw)
+    assert npf.read_magic(f) == (1, 0)
+    got_shape, fortran, got_dtype = npf.read_array_header_1_0(f)
+    assert got_shape == shape and not fortran and got_dtype == np.dtype(dtype)
+    start = f.tell()
+    assert start % 64 == 0  # magic + version + length + header: multiple of 64
+    assert raw[start - 1:start] == b"\n"
+    assert len(raw) - start == int(np.prod(shape)) * np.dtype(dtype).itemsize
+
+
+def test_record_padding_is_1_to_64_spaces():
+    # RAFT pads with 1..64 spaces: when the header would end exactly on a
+    # 64-byte boundary it adds a full 64
+    # (shapes of 1..130 unit dims give header texts of every length mod 64)
+    seen = set()
+    for dims in range(1, 131):
+        h = ser.header_bytes(np.float32, (1,) * dims)
+        body = h[10:]
+        spaces = len(body) - len(body.rstrip(b" \n")) - 1
+        assert 1 <= spaces <= 64 and len(h) % 64 == 0
+        seen.add(spaces)
+    assert seen == set(range(1, 65))
+
+
+def test_record_values_round_trip():
+    buf = io.BytesIO()
+    a = np.random.default_rng(2).standard_normal((4, 3)).astype(np.float16)
+    ser.write_scalar(buf, True, np.bool_)
+    ser.write_scalar(buf, 2 ** 40 + 3, np.uint64)
+    ser.write_scalar(buf, 2.5, np.float32)
+    ser.write_array(buf, a)
+    buf.seek(0)
+    assert ser.read_scalar(buf) == 1
+    assert ser.read_scalar(buf) == 2 ** 40 + 3
+    assert ser.read_scalar(buf) == 2.5
+    assert np.array_equal(ser.read_array(buf), a)
+    # bool has no byte order and is stored as one unsigned byte
+    assert b"'descr': '|u1'" in ser.header_bytes(np.bool_, ())
+
+
+def test_dtype_prefix():
+    assert ser.dtype_prefix(np.float32, 6) == b"<f4\0"
+    assert ser.dtype_prefix(np.float16, 6) == b"<f2\0"
+    assert ser.dtype_prefix(np.float16, 5) == b"<e2\0"
+    assert ser.dtype_prefix(np.uint8, 6) == b"|u1\0"
+    assert ser.read_prefix(io.BytesIO(b"<f2\0")) == np.float16
+
+
+# ---- cuVS brute-force index files ---------------------------------------------------
+
+@pytest.mark.parametrize("metric,code", [("sqeuclidean", 0), ("euclidean", 1), ("cosine", 2),
+                                         ("inner_product", 6)])
+def test_brute_force_file_round_trip(tmp_path, metric, code):
+    x = np.random.default_rng(5).random((10, 3)).astype(np.float32)
+    path = tmp_path / "bf.bin"
+    brute_force.save(str(path), brute_force.build(x, metric))
+    raw = path.read_bytes()
+    # reference python/tests/test_cuvs.py:214-221
+    assert raw[:4] == b"<f4\0"
+    assert raw[4:10] == b"\x93NUMPY"
+    f = io.BytesIO(raw[4:])
+    fields = [ser.read_scalar(f) for _ in range(6)]
+    assert fields == [0, 10, 3, code, pytest.approx(2.0), 1]
+    assert np.array_equal(ser.read_array(f), x)
+    has_norms = ser.read_scalar(f)
+    assert has_norms == (code in (0, 1, 2))
+    if has_norms:
+        norms = ser.read_array(f)
+        want = np.sum(x.astype(np.float32) ** 2, axis=1)
+        if code == 2:
+            want = np.sqrt(want)
+        assert np.array_equal(norms, want.astype(np.float32))
+    assert f.read() == b""
+    idx = brute_force.load(str(path))
+    assert idx.trained and idx._metric == code and np.array_equal(idx.dataset, x)
+    assert len(idx) == 10
+
+
+def test_brute_force_file_float16_and_hamming(tmp_path):
+    x = np.random.default_rng(6).random((4, 8)).astype(np.float16)
+    p = tmp_path / "h.bin"
+    brute_force.save(str(p), brute_force.build(x))
+    assert p.read_bytes()[:4] == b"<f2\0"
+    assert brute_force.load(str(p)).dataset.dtype == np.float16
+    codes = np.random.default_rng(7).integers(0, 256, (5, 16), dtype=np.uint8)
+    brute_force.save(str(p), brute_force.build(codes, metric="bitwise_hamming"))
+    idx = brute_force.load(str(p))
+    assert idx._metric == 20 and np.array_equal(idx.dataset, codes)
+
+
+def test_brute_force_errors(tmp_path):
+    x = np.zeros((4, 3), np.float32)
+    with pytest.raises(ValueError, match="not supported"):
+        brute_force.build(x, "cityblock")
+    with pytest.raises(ValueError, match="matrix"):
+        brute_force.build(np.zeros(3, np.float32))
+    with pytest.raises(ValueError, match="uint8"):
+        brute_force.build(x, "bitwise_hamming")
+    with pytest.raises(ValueError, match="built"):
+        brute_force.search(brute_force.Index(), x, 1)
+
+    class Bitset:
+        type = "bitset"
+
+    with pytest.raises(ValueError, match="prefilter"):
+        brute_force.search(brute_force.build(x), x, 1, prefilter=Bitset())
+    p = tmp_path / "nodata.bin"
+    brute_force.save(str(p), brute_force.build(x), include_dataset=False)
+    with pytest.raises(ValueError, match="no dataset"):
+        brute_force.load(str(p))
+    p.write_bytes(b"<f4\0" + b"garbage")
+    with pytest.raises(ValueError):
+        brute_force.load(str(p))
+
+
+# ---- argument validation ------------------------------------------------------------
+
+def test_nearest_neighbors_arguments():
+    with pytest.raises(ValueError, match="unknown metric"):
+        mlxvs_amd.NearestNeighbors(metric="manhattan")
+    with pytest.raises(ValueError, match="nn_descent"):
+        mlxvs_amd.NearestNeighbors(algorithm="nn_descent")
+    with pytest.raises(ValueError, match="algorithm"):
+        mlxvs_amd.NearestNeighbors(algorithm="kd_tree")
+    nn = mlxvs_amd.NearestNeighbors(3)
+    with pytest.raises(RuntimeError, match="fit"):
+        nn.kneighbors(np.zeros((2, 2)))
+    with pytest.raises(ValueError, match="2-D"):
+        nn.fit(np.zeros(5))
+    nn.fit(np.zeros((4, 2), np.float32))
+    assert nn.n_samples_fit_ == 4 and nn.n_features_in_ == 2
+    # reference python/mlxvs/_neighbors.py:71-74: k in [1, n] (n - 1 without X)
+    with pytest.raises(ValueError, match=r"\[1, 3\]"):
+        nn.kneighbors(n_neighbors=4)
+    with pytest.raises(ValueError, match=r"\[1, 4\]"):
+        nn.kneighbors(np.zeros((1, 2)), n_neighbors=5)
+    with pytest.raises(ValueError):
+        nn.kneighbors(np.zeros((1, 2)), n_neighbors=0)
+
+
+def test_kmeans_predict_arguments():
+    x = np.zeros((10, 4), np.float32)
+    # reference python/tests/test_mlxvs.py:246-247, src/kmeans.cpp:143-153
+    with pytest.raises(ValueError, match="same number of columns"):
+        mlxvs_amd.kmeans_predict(x, np.zeros((2, 5), np.float32))
+    with pytest.raises(ValueError, match="1 <= m <= clusters"):
+        mlxvs_amd.kmeans_predict(x, np.zeros((2, 4), np.float32), 3)
+    with pytest.raises(ValueError, match="1 <= m <= clusters"):
+        mlxvs_amd.kmeans_predict(x, np.zeros((2, 4), np.float32), 0)
+    with pytest.raises(ValueError, match="2-D"):
+        mlxvs_amd.kmeans_predict(np.zeros(4, np.float32), np.zeros((2, 4), np.float32))
