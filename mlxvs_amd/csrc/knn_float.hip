@@ -122,44 +122,6 @@ __global__ __launch_bounds__(256) void rows_transform_kernel(PrepArgs a) {
 // chain), then written to the other LDS buffer; one barrier per tile.  Rows
 // past the split and dims past ld read as zero through the buffer range check.
 
-// Filters one tile's 16 scores of a lane (rows 8 (i / 4) + 4 h + i % 4 of
-// the tile, ids id0 + row) against the lane's float threshold and inserts the
-// survivors into its stream list.  Every lane drains its own bitmask of
-// survivors in a loop that runs as many times as the busiest lane needs
-// (lanes that are done insert the empty key); the scores go through the
-// lane's 16-float LDS slot `stage` so that a lane can pick its own position.
-// FULL: all 32 rows of the tile exist.  Returns whether the lane kept any.
-template <int T, bool FULL>
-__device__ __forceinline__ bool select_tile(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
-                                            const float (&sc)[16], int h, uint32_t id0,
-                                            int lim, float* stage) {
-  bool any = false;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    any |= (FULL || m < lim) & !(sc[i] < thr);
-  }
-  if (__builtin_amdgcn_ballot_w64(any) == 0) return false;
-  uint32_t pm = 0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    pm |= ((FULL || m < lim) & !(sc[i] < thr)) ? (1u << i) : 0u;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    *(floatx4*)(stage + 4 * j) = floatx4{sc[4 * j], sc[4 * j + 1], sc[4 * j + 2], sc[4 * j + 3]};
-  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
-    const int i = pm ? __builtin_ctz(pm) : 0;
-    const float v = stage[i];
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    stream_insert<T>(K, I, pm ? key_nz(v) : 0u, id0 + m);
-    pm &= pm - 1u;
-  }
-  thr = fmaxf(thr, score_of_key(K[T - 1]));  // NaN while the list has room
-  return any;
-}
-
 template <bool F16, int DH>
 constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
@@ -176,9 +138,6 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int QV = DH / EPV;        // query vectors per lane
   __shared__ __align__(16) E tile[2][kTileRows * STRIDE];
   __shared__ __align__(16) float tnorm[2][kTileRows];
-  // each lane's scores for its inserts; a 20-float lane stride keeps the
-  // 16-byte writes of 16 consecutive lanes on distinct bank quads
-  __shared__ __align__(16) float stage[256 * 20];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -346,10 +305,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
       bool inserted;
       if (t + 1 < ntiles || (nrows & (kTileRows - 1)) == 0)
-        inserted = select_tile<T, true>(K, I, thr, sc, h, id0, kTileRows, stage + 20 * tid);
+        inserted = select_block<T, true>(K, I, thr, sc, h, id0, kTileRows);
       else
-        inserted = select_tile<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows,
-                                         stage + 20 * tid);
+        inserted = select_block<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows);
       if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
         __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -553,7 +511,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
             }
           }
-          inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+          inserted |= select_block<T, false>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
         }
         if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
           __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
