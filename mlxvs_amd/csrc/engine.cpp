@@ -462,7 +462,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   const bool use_deep = deep && kern::deep_supported(kld, T, false);
-  const int tile_rows = use_deep ? kern::kDeepRows : kern::kTileRows;
+  // split alignment: whole tiles (deep: 128 rows; fused: 32 or 64)
+  const int tile_rows = use_deep ? kern::kDeepRows : 2 * kern::kTileRows;
   if ((use_deep || kern::fused_supported(kld, T, kf16)) && nq < (int64_t(1) << 31)) {
     const int bpc = use_deep ? kern::deep_blocks_per_cu(T) : kern::fused_blocks_per_cu(kld, T, kf16);
     plan = plan_splits(n, qblocks, k, T, 2, tile_rows, device_slots(bpc), true);

@@ -125,6 +125,16 @@ __global__ __launch_bounds__(256) void rows_transform_kernel(PrepArgs a) {
 template <bool F16, int DH>
 constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
+// 32-row MFMA blocks per streamed tile: two where the registers allow, which
+// halves the barriers and per-tile overhead per row.  One where the query
+// fragments take 64 or more VGPRs and the list is 16 long, or 128 (fp32,
+// 256 dims): the second accumulator and prefetch would spill.
+template <bool F16, int DH, int T>
+constexpr int fused_rb() {
+  constexpr int qregs = DH * (F16 ? 2 : 4) / 4;
+  return (qregs >= 128 || (qregs >= 64 && T >= 16)) ? 1 : 2;
+}
+
 
 template <bool F16, int DH, int T, bool L2>
 __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kernel(FusedArgs a) {
@@ -132,12 +142,14 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int EPV = F16 ? 8 : 4;    // elements per 16-byte vector
   constexpr int D = 2 * DH;           // padded dims of an LDS row
   constexpr int VROW = D / EPV;       // 16-byte vectors per LDS row
-  constexpr int VTILE = kTileRows * VROW;
+  constexpr int RB = fused_rb<F16, DH, T>();
+  constexpr int TR = 32 * RB;         // rows per tile
+  constexpr int VTILE = TR * VROW;
   constexpr int NPF = (VTILE + 255) / 256;
   constexpr int STRIDE = D + EPV;     // 16-byte pad: 8 rows hit distinct bank quads
   constexpr int QV = DH / EPV;        // query vectors per lane
-  __shared__ __align__(16) E tile[2][kTileRows * STRIDE];
-  __shared__ __align__(16) float tnorm[2][kTileRows];
+  __shared__ __align__(16) E tile[2][TR * STRIDE];
+  __shared__ __align__(16) float tnorm[2][TR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -168,7 +180,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const int64_t r0 = (int64_t)split * a.rows_per_split;
   const int64_t r1 = min(a.n, r0 + a.rows_per_split);
   const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
-  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int ntiles = (nrows + TR - 1) / TR;
 
   // buffer resources over this split's rows and norms
   const E* sbase = (const E*)a.base + r0 * ld;
@@ -183,7 +195,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   // accumulators (a VMEM address register overwritten by an MFMA forces a
   // wait for the load).  Vectors past ld start at 2^31, beyond every range
   // (ranges are < 2^31 bytes), and read zero.
-  const uint32_t tile_bytes = kTileRows * ld * (uint32_t)sizeof(E);
+  const uint32_t tile_bytes = TR * ld * (uint32_t)sizeof(E);
   uint32_t voff[NPF];
 #pragma unroll
   for (int j = 0; j < NPF; ++j) {
@@ -192,7 +204,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     voff[j] = (e < VTILE && c < ld) ? (uint32_t)((r * ld + c) * (int)sizeof(E)) : 0x80000000u;
   }
   // norm word of this thread (threads past the tile read beyond the range)
-  uint32_t noff = tid < kTileRows ? tid * 4u : 0x80000000u;
+  uint32_t noff = tid < TR ? tid * 4u : 0x80000000u;
 
   // the lane's query dims [h DH, h DH + DH): 16-byte buffer loads of the
   // query row, zero past ld and for lanes without a query
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       voff[j] += tile_bytes;
     }
     if (l2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
-    noff += kTileRows * 4;
+    noff += TR * 4;
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -231,7 +243,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
         *(u32x4*)&tile[buf][r * STRIDE + c] = pf[j];
       }
     }
-    if (l2 && tid < kTileRows) tnorm[buf][tid] = __uint_as_float(pn);
+    if (l2 && tid < TR) tnorm[buf][tid] = __uint_as_float(pn);
   };
 
   uint32_t K[T], I[T];
@@ -269,45 +281,58 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     issue_loads();
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
-      floatx16 acc;
+      floatx16 acc[RB];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
       const E* arow = &tile[buf][col * STRIDE + h * DH];
 #pragma unroll
       for (int v = 0; v < QV; ++v) {
         if constexpr (F16) {
-          const halfx8 av = *(const halfx8*)(arow + 8 * v);
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[v], acc, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < RB; ++r) {
+            const halfx8 av = *(const halfx8*)(arow + r * 32 * STRIDE + 8 * v);
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[v], acc[r], 0, 0, 0);
+          }
         } else {
-          const floatx4 av = *(const floatx4*)(arow + 4 * v);
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], qf[v][0], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], qf[v][1], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[2], qf[v][2], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], qf[v][3], acc, 0, 0, 0);
+          floatx4 av[RB];
+#pragma unroll
+          for (int r = 0; r < RB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * STRIDE + 4 * v);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], qf[v][u], acc[r], 0, 0, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2;
-      // 2 q.b is exact, so fma(2, q.b, -|b|^2) rounds exactly as that form
-      float sc[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (L2) {
-          const floatx4 nb = *(const floatx4*)&tnorm[buf][8 * j + 4 * h];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) sc[4 * j + u] = __builtin_fmaf(2.0f, acc[4 * j + u], -nb[u]);
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[4 * j + u];
-        }
-      }
       if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
-      const uint32_t id0 = (uint32_t)(r0 + t * kTileRows);
-      bool inserted;
-      if (t + 1 < ntiles || (nrows & (kTileRows - 1)) == 0)
-        inserted = select_block<T, true>(K, I, thr, sc, h, id0, kTileRows);
-      else
-        inserted = select_block<T, false>(K, I, thr, sc, h, id0, nrows - t * kTileRows);
+      const bool full = t + 1 < ntiles || nrows % TR == 0;
+      bool inserted = false;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2;
+        // 2 q.b is exact, so fma(2, q.b, -|b|^2) rounds exactly as that form
+        float sc[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (L2) {
+            const floatx4 nb = *(const floatx4*)&tnorm[buf][32 * r + 8 * j + 4 * h];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              sc[4 * j + u] = __builtin_fmaf(2.0f, acc[r][4 * j + u], -nb[u]);
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
+          }
+        }
+        const uint32_t id0 = (uint32_t)(r0 + t * TR + 32 * r);
+        if (full)
+          inserted |= select_block<T, true>(K, I, thr, sc, h, id0, 32);
+        else
+          inserted |= select_block<T, false>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
+      }
       if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
         __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
