@@ -106,6 +106,40 @@ MLXVS_API void knn_self_graph_device(const Rows& rows, int k, Metric metric,
 MLXVS_API std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m = 1,
                                               int tile_rows = 65536, void* stream = nullptr);
 
+/**
+ * An IVF-Flat index (reference include/mlxvs/mlxvs.h:523-533): the lists'
+ * centers [lists, d], the rows grouped by list [n, d] (unit rows for
+ * Cosine), the id of each row [n] and where each list starts [lists + 1].
+ * float32 / int32 views; host pointers for ivf_flat_search, device pointers
+ * for ivf_flat_search_device.
+ */
+struct IvfFlatIndexView {
+  const float* centers = nullptr;
+  int64_t lists = 0;
+  const float* data = nullptr;
+  int64_t n = 0;
+  const int32_t* indices = nullptr;
+  const int32_t* offsets = nullptr;
+  int d = 0;
+  Metric metric = Metric::L2;
+};
+
+/**
+ * The k nearest indexed rows of every query, scanning the n_probes lists of
+ * nearest center (clamped to [1, lists]): ids and distances as
+ * brute_force_knn, -1 / +-inf where the scanned lists hold fewer than k
+ * rows; among equal scores the candidate of the earlier probe, then the
+ * earlier row of the list, comes first.  1 <= k <= 256.  Replaces reference
+ * include/mlxvs/mlxvs.h:561-571 (src/ivf.cpp:327-416).
+ */
+MLXVS_API Neighbors ivf_flat_search(const IvfFlatIndexView& index, const Rows& queries, int k,
+                                    int n_probes = 20, void* stream = nullptr);
+/** ivf_flat_search on device pointers (queries [nq, index.d] float32); writes
+ * device ids / distances [nq, k] (distances may be null). */
+MLXVS_API void ivf_flat_search_device(const IvfFlatIndexView& index, const float* queries,
+                                      int64_t nq, int k, int n_probes, int32_t* ids,
+                                      float* distances, void* stream = nullptr);
+
 /** Frees the per-device workspace kept between calls. */
 MLXVS_API void release_workspace();
 

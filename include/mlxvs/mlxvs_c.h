@@ -161,6 +161,52 @@ MLXVS_C_API int mlxvs_kmeans_predict(
     int32_t* labels);
 
 /**
+ * IVF-Flat search (extension; exposes mlxvs::ivf_flat_search, reference
+ * include/mlxvs/mlxvs.h:561-571 / src/ivf.cpp:327-416, which the reference
+ * binds to C++ and Python only).  The index: centers [lists, d] float32,
+ * data [n, d] float32 grouped by list (unit rows for MLXVS_COSINE), indices
+ * [n] int32 (the id of each row), offsets [lists + 1] int32.  queries
+ * [nq, d]; n_probes lists scanned per query (clamped to [1, lists]);
+ * 1 <= k <= 256.  ids / distances [nq, k] as mlxvs_brute_force_knn, -1 /
+ * +-inf where the scanned lists hold fewer than k rows.  Host arrays.
+ */
+MLXVS_C_API int mlxvs_ivf_flat_search(
+    const float* centers,
+    int64_t lists,
+    const float* data,
+    int64_t n,
+    const int32_t* indices,
+    const int32_t* offsets,
+    int32_t d,
+    mlxvs_metric metric,
+    const float* queries,
+    int64_t nq,
+    int32_t k,
+    int32_t n_probes,
+    int32_t* ids,
+    float* distances);
+
+/** mlxvs_ivf_flat_search with every array in device memory, enqueued on
+ * stream (a hipStream_t); returns once the results are written (the search
+ * reads the probes back to the host to group them by list). */
+MLXVS_C_API int mlxvs_ivf_flat_search_device(
+    const float* centers,
+    int64_t lists,
+    const float* data,
+    int64_t n,
+    const int32_t* indices,
+    const int32_t* offsets,
+    int32_t d,
+    mlxvs_metric metric,
+    const float* queries,
+    int64_t nq,
+    int32_t k,
+    int32_t n_probes,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/**
  * mlxvs_brute_force_knn on device memory: base [n, d] and queries [nq, d]
  * float32 (f16 == 0) or binary16 (f16 != 0), outputs ids / distances
  * [nq, k] in device memory (distances may be NULL).  Enqueued on stream.

@@ -26,11 +26,15 @@ from pathlib import Path
 import numpy as np
 
 __all__ = [
+    "IvfFlatIndex",
     "Metric",
     "NearestNeighbors",
     "all_neighbors",
     "brute_force_knn",
     "hamming_knn",
+    "ivf_flat_build",
+    "ivf_flat_extend",
+    "ivf_flat_search",
     "kmeans_predict",
     "library_path",
 ]
@@ -62,6 +66,10 @@ def _load():
         "mlxvs_hamming_knn": [vp, i64, vp, i64, i32, i32, vp, vp],
         "mlxvs_knn_self_graph": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp],
         "mlxvs_kmeans_predict": [vp, i64, vp, i64, i32, i32, i32, vp],
+        "mlxvs_ivf_flat_search": [vp, i64, vp, i64, vp, vp, i32, ctypes.c_int, vp, i64, i32, i32,
+                                  vp, vp],
+        "mlxvs_ivf_flat_search_device": [vp, i64, vp, i64, vp, vp, i32, ctypes.c_int, vp, i64,
+                                         i32, i32, vp, vp, vp],
         "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
@@ -298,3 +306,13 @@ def version() -> str:
 
 
 from mlxvs_amd.neighbors import NearestNeighbors  # noqa: E402  (uses the functions above)
+from mlxvs_amd.ivf import (  # noqa: E402
+    IvfFlatIndex, ivf_flat_build, ivf_flat_extend, ivf_flat_search)
+
+
+def ivf_flat_search_device(centers_ptr, lists, data_ptr, n, indices_ptr, offsets_ptr, d, metric,
+                           queries_ptr, nq, k, ids_ptr, dist_ptr, *, n_probes=20, stream=None):
+    """mlxvs_ivf_flat_search_device on device pointers (ints)."""
+    _check(_L().mlxvs_ivf_flat_search_device(
+        centers_ptr, lists, data_ptr, n, indices_ptr, offsets_ptr, d, int(_metric(metric)),
+        queries_ptr, nq, int(k), int(n_probes), ids_ptr, dist_ptr, stream))

@@ -126,6 +126,30 @@ int mlxvs_kmeans_predict(const void* x, int64_t n, const void* centroids, int64_
   });
 }
 
+int mlxvs_ivf_flat_search(const float* centers, int64_t lists, const float* data, int64_t n,
+                          const int32_t* indices, const int32_t* offsets, int32_t d,
+                          mlxvs_metric metric, const float* queries, int64_t nq, int32_t k,
+                          int32_t n_probes, int32_t* ids, float* distances) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    mlxvs::IvfFlatIndexView ix{centers, lists, data, n, indices, offsets, d, to_metric(metric)};
+    auto q = host_rows(queries, nq, d, mlxvs::Dtype::Float32);
+    auto r = mlxvs::ivf_flat_search(ix, q, k, n_probes);
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_ivf_flat_search_device(const float* centers, int64_t lists, const float* data,
+                                 int64_t n, const int32_t* indices, const int32_t* offsets,
+                                 int32_t d, mlxvs_metric metric, const float* queries,
+                                 int64_t nq, int32_t k, int32_t n_probes, int32_t* ids,
+                                 float* distances, void* stream) {
+  return guarded([&] {
+    mlxvs::IvfFlatIndexView ix{centers, lists, data, n, indices, offsets, d, to_metric(metric)};
+    mlxvs::ivf_flat_search_device(ix, queries, nq, k, n_probes, ids, distances, stream);
+  });
+}
+
 int mlxvs_brute_force_knn_device(const void* base, int64_t n, const void* queries,
                                  int64_t nq, int32_t d, int32_t f16, int32_t k,
                                  mlxvs_metric metric, int32_t* ids, float* distances,

@@ -647,6 +647,199 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   hamming_exhaustive(ar, s, bw, qw, wstride, n, redo, k, ids, dists);
 }
 
+// ---- IVF-Flat list scan ------------------------------------------------------------
+//
+// Reference src/ivf.cpp:164-221 (probe, finish) and 327-416 (ivf_flat_search):
+// the n_probes nearest centers of each query (brute force, L2 for L2 and
+// cosine, inner product for inner product); each query's candidates are the
+// rows of its probed lists in probe order, numbered by their column in the
+// query's candidate buffer; the best k by score, then lowest column; ids
+// through the index's id array.
+
+// (query, probe) pairs grouped by list and cut into items of up to 128 pairs
+// (one workgroup each), for the queries [q0, q1).
+struct IvfItems {
+  std::vector<int> items;  // [n][3] list, first pair, pairs
+  std::vector<int> pairs;  // q * P + p, grouped by list
+  int n = 0;
+};
+
+IvfItems ivf_items(const int* probes, int64_t q0, int64_t q1, int P, int64_t lists) {
+  IvfItems r;
+  std::vector<int64_t> count((size_t)lists + 1, 0);
+  for (int64_t q = q0; q < q1; ++q)
+    for (int p = 0; p < P; ++p) ++count[(size_t)probes[q * P + p] + 1];
+  for (int64_t l = 0; l < lists; ++l) count[(size_t)l + 1] += count[(size_t)l];
+  std::vector<int64_t> next(count.begin(), count.end() - 1);
+  r.pairs.resize((size_t)((q1 - q0) * P));
+  for (int64_t q = q0; q < q1; ++q)
+    for (int p = 0; p < P; ++p) {
+      const int l = probes[q * P + p];
+      r.pairs[(size_t)next[(size_t)l]++] = (int)(q * P + p);
+    }
+  for (int64_t l = 0; l < lists; ++l) {
+    for (int64_t f = count[(size_t)l]; f < count[(size_t)l + 1]; f += kQueriesPerBlock) {
+      r.items.push_back((int)l);
+      r.items.push_back((int)f);
+      r.items.push_back((int)std::min<int64_t>(kQueriesPerBlock, count[(size_t)l + 1] - f));
+      ++r.n;
+    }
+  }
+  return r;
+}
+
+template <typename V>
+V* to_device(Arena& ar, hipStream_t s, const std::vector<V>& v) {
+  V* p = ar.take<V>(std::max<size_t>(v.size(), 1));
+  if (!v.empty())
+    check_hip(hipMemcpyAsync(p, v.data(), sizeof(V) * v.size(), hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync");
+  return p;
+}
+
+// One search on device pointers; `off` is the host copy of the offsets.
+void ivf_search(Session& ss, const float* centers, int64_t lists, const float* data, int64_t n,
+                const int32_t* indices, const int32_t* offsets, const std::vector<int32_t>& off,
+                int d, int metric, const float* queries, int64_t nq, int k, int P,
+                int32_t* ids, float* dists) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const bool l2 = metric == kern::kL2;
+  const float pad = l2 ? INFINITY : -INFINITY;
+  // fp32 operands with a row length that is a multiple of 4 floats (zero
+  // padded copies when d is not, or a pointer is not 16-byte aligned)
+  const int ld = round_up(d, 4);
+  const bool aligned = ld == d && (uintptr_t)centers % 16 == 0 && (uintptr_t)data % 16 == 0 &&
+                       (uintptr_t)queries % 16 == 0;
+  auto padded = [&](const float* x, int64_t rows) -> const float* {
+    if (aligned || rows == 0) return x;
+    float* p = ar.take<float>((size_t)rows * ld);
+    kern::PrepArgs t{x, rows, d, d, 0, nullptr, nullptr, p, ld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(t, s); });
+    return p;
+  };
+  const float* kc = padded(centers, lists);
+  const float* kd = padded(data, n);
+  const float* kq = padded(queries, nq);
+  if (metric == kern::kCosine) {  // reference src/ivf.cpp:348-350
+    float* qn = ar.take<float>((size_t)nq);
+    float* uq = ar.take<float>((size_t)nq * ld);
+    kern::PrepArgs pn{kq, nq, ld, ld, 0, qn, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pn, s); });
+    kern::PrepArgs tu{kq, nq, ld, ld, 0, nullptr, qn, uq, ld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(tu, s); });
+    kq = uq;
+  }
+  float* bnorm = nullptr;
+  float* qnorm = nullptr;
+  if (l2) {
+    bnorm = ar.take<float>((size_t)std::max<int64_t>(n, 1));
+    qnorm = ar.take<float>((size_t)nq);
+    kern::PrepArgs pb{kd, n, ld, ld, 0, bnorm, nullptr, nullptr, 0, 0};
+    kern::PrepArgs pq{kq, nq, ld, ld, 0, qnorm, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+    launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
+  }
+
+  // the probes (reference src/ivf.cpp:171-178)
+  int32_t* probes = ar.take<int32_t>((size_t)nq * P);
+  float* pdist = ar.take<float>((size_t)nq * P);
+  float_knn(ss, {kc, kq, lists, nq, ld, false}, P,
+            metric == kern::kInnerProduct ? kern::kInnerProduct : kern::kL2, probes, pdist);
+  std::vector<int32_t> hp((size_t)nq * P);
+  check_hip(hipMemcpyAsync(hp.data(), probes, sizeof(int32_t) * hp.size(), hipMemcpyDeviceToHost,
+                           s), "hipMemcpyAsync (probes)");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+
+  // buffer columns of the probes and the buffer width (src/ivf.cpp:179-183)
+  std::vector<int32_t> slots((size_t)nq * P);
+  int64_t width = 1;
+  for (int64_t q = 0; q < nq; ++q) {
+    int64_t c = 0;
+    for (int p = 0; p < P; ++p) {
+      slots[(size_t)(q * P + p)] = (int32_t)c;
+      const int l = hp[(size_t)(q * P + p)];
+      c += off[(size_t)l + 1] - off[(size_t)l];
+    }
+    width = std::max(width, c);
+  }
+  if (width >= (int64_t(1) << 31)) invalid("mlxvs::ivf_flat_search", "too many candidates per query.");
+  int32_t* dslots = to_device(ar, s, slots);
+  const kern::Metric km = metric == kern::kCosine ? kern::kInnerProduct : (kern::Metric)metric;
+
+  const int T = list_len_float(k);
+  if (k <= T && kern::fused_supported(ld, T, false) &&
+      2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
+    // fused: per-lane lists over every (query, probe) pair, then the merge
+    const IvfItems it = ivf_items(hp.data(), 0, nq, P, lists);
+    int* ditems = to_device(ar, s, it.items);
+    int* dpairs = to_device(ar, s, it.pairs);
+    const int nseg = 2 * P;
+    // every (query, probe) pair is in one item, so every segment is written
+    uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
+    const int slots_n = kern::bound_slots_for(T);
+    uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots_n);
+    launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots_n, 1, s); });
+    kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, 1, 0, 0,
+                       ditems, dpairs, offsets, dslots, P, it.n, nullptr, width, 0};
+    launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
+    kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr};
+    launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+    kern::IvfMapArgs mp{ids, dists, (int)nq, k, nullptr, 0, probes, dslots, offsets, indices, P,
+                        pad};
+    launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
+  } else {
+    // candidate buffers of blocks of queries, exact radix select
+    // (reference src/ivf.cpp:357-409 with the buffers kept near 256 MB)
+    const int64_t block = std::max<int64_t>(1, std::min<int64_t>(nq, (int64_t(1) << 26) / width));
+    float* S = ar.take<float>((size_t)(block * width));
+    std::vector<int> iota((size_t)nq);
+    for (int64_t i = 0; i < nq; ++i) iota[(size_t)i] = (int)i;
+    int* qsel = to_device(ar, s, iota);
+    for (int64_t q0 = 0; q0 < nq; q0 += block) {
+      const int64_t q1 = std::min(nq, q0 + block);
+      const int cnt = (int)(q1 - q0);
+      const IvfItems it = ivf_items(hp.data(), q0, q1, P, lists);
+      int* ditems = to_device(ar, s, it.items);
+      int* dpairs = to_device(ar, s, it.pairs);
+      launch(s, "prep", [&] { return kern::launch_fill_f32(S, cnt * width, -INFINITY, s); });
+      kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, 4, k, nullptr, nullptr, 0, 0,
+                         0, ditems, dpairs, offsets, dslots, P, it.n, S, width, (int)q0};
+      launch(s, "ivf_scan", [&] {
+        return kern::fused_supported(ld, 4, false) ? kern::launch_ivf_scores(fa, s)
+                                                   : kern::launch_ivf_scores_any(fa, s);
+      });
+      kern::SelectArgs se{S, width, cnt, k, qsel + q0, metric, qnorm, 0, ids, dists};
+      launch(s, "select", [&] { return kern::launch_select(se, s); });
+      kern::IvfMapArgs mp{ids, dists, cnt, k, qsel + q0, 0, probes, dslots, offsets, indices, P,
+                          pad};
+      launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
+      // the host item lists are released at the end of the iteration
+      check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    }
+  }
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // host arrays released next
+}
+
+void ivf_args(const IvfFlatIndexView& ix, int64_t nq, int qd, int k, const char* op) {
+  if ((int)ix.metric < 0 || (int)ix.metric > 2) invalid(op, "unknown metric.");
+  if (ix.lists < 1 || ix.lists >= (int64_t(1) << 31)) invalid(op, "the index needs at least one list.");
+  if (ix.n < 0 || ix.n >= (int64_t(1) << 31)) invalid(op, "the number of rows must be in [0, 2^31).");
+  if (ix.d < 1) invalid(op, "the dimension must be at least 1.");
+  if (ix.centers == nullptr || ix.offsets == nullptr || (ix.n > 0 && (!ix.data || !ix.indices)))
+    invalid(op, "index arrays must not be NULL.");
+  if (nq < 0 || nq >= (int64_t(1) << 31)) invalid(op, "the number of queries must be in [0, 2^31).");
+  // reference src/ivf.cpp:337-345
+  if (qd != ix.d) invalid(op, "queries must have the index's columns.");
+  if (k < 1 || k > kern::kMaxK) invalid(op, "k must be in [1, 256].");
+}
+
+void check_offsets(const std::vector<int32_t>& off, int64_t n, const char* op) {
+  if (off.front() != 0 || off.back() != n) invalid(op, "offsets must run from 0 to the row count.");
+  for (size_t i = 1; i < off.size(); ++i)
+    if (off[i] < off[i - 1]) invalid(op, "offsets must not decrease.");
+}
+
 // ---- host <-> device helpers ----------------------------------------------------
 
 size_t elem_size(Dtype t) {
@@ -793,6 +986,56 @@ std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m,
                            s), "hipMemcpyAsync (labels)");
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
   return labels;
+}
+
+Neighbors ivf_flat_search(const IvfFlatIndexView& index, const Rows& queries, int k,
+                          int n_probes, void* stream) {
+  const char* op = "mlxvs::ivf_flat_search";
+  check_rows(queries, op, "queries");
+  if (queries.dtype != Dtype::Float32) invalid(op, "queries must be float32.");
+  ivf_args(index, queries.n, queries.d, k, op);
+  const int64_t nq = queries.n;
+  std::vector<int32_t> off(index.offsets, index.offsets + index.lists + 1);
+  check_offsets(off, index.n, op);
+  Neighbors out;
+  out.nq = nq;
+  out.k = k;
+  if (nq == 0) return out;
+  const int P = (int)std::clamp<int64_t>(n_probes, 1, index.lists);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int d = index.d;
+  const float* dc = (const float*)upload(ar, s, Rows{index.centers, index.lists, d, Dtype::Float32});
+  const float* dd = index.n ? (const float*)upload(ar, s, Rows{index.data, index.n, d, Dtype::Float32})
+                            : nullptr;
+  const float* dq = (const float*)upload(ar, s, queries);
+  int32_t* di = to_device(ar, s, std::vector<int32_t>(index.indices, index.indices + index.n));
+  int32_t* doff = to_device(ar, s, off);
+  int32_t* ids = ar.take<int32_t>((size_t)nq * k);
+  float* dists = ar.take<float>((size_t)nq * k);
+  ivf_search(ss, dc, index.lists, dd, index.n, di, doff, off, d, (int)index.metric, dq, nq, k, P,
+             ids, dists);
+  return download(ar, s, ids, dists, nq, k);
+}
+
+void ivf_flat_search_device(const IvfFlatIndexView& index, const float* queries, int64_t nq,
+                            int k, int n_probes, int32_t* ids, float* distances, void* stream) {
+  const char* op = "mlxvs::ivf_flat_search";
+  ivf_args(index, nq, index.d, k, op);
+  if (nq > 0 && (queries == nullptr || ids == nullptr)) invalid(op, "queries and ids must not be NULL.");
+  if (nq == 0) return;
+  Session ss((hipStream_t)stream);
+  hipStream_t s = ss.stream();
+  std::vector<int32_t> off((size_t)index.lists + 1);
+  check_hip(hipMemcpyAsync(off.data(), index.offsets, sizeof(int32_t) * off.size(),
+                           hipMemcpyDeviceToHost, s), "hipMemcpyAsync (offsets)");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  check_offsets(off, index.n, op);
+  const int P = (int)std::clamp<int64_t>(n_probes, 1, index.lists);
+  float* dists = distances ? distances : ss.arena().take<float>((size_t)nq * k);
+  ivf_search(ss, index.centers, index.lists, index.data, index.n, index.indices, index.offsets,
+             off, index.d, (int)index.metric, queries, nq, k, P, ids, dists);
 }
 
 Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k, void* stream) {

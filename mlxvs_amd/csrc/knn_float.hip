@@ -136,7 +136,10 @@ constexpr int fused_rb() {
 }
 
 
-template <bool F16, int DH, int T, bool L2>
+// MODE 0: dense (split x query block).  MODE 1: IVF-Flat item, per-lane
+// lists (ids = buffer columns).  MODE 2: IVF-Flat item, scores written to
+// the candidate buffers.
+template <bool F16, int DH, int T, bool L2, int MODE = 0>
 __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kernel(FusedArgs a) {
   using E = typename std::conditional<F16, _Float16, float>::type;
   constexpr int EPV = F16 ? 8 : 4;    // elements per 16-byte vector
@@ -154,12 +157,18 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, col = lane & 31;
-  // Workgroup -> (split, query block).  Workgroups are dealt to the 8 XCDs
-  // round-robin by id; with xcd_major, XCD j gets splits j, j + 8, ... for
-  // every query block, split-major, so the workgroups that stream the same
-  // base rows run together on one XCD and share its L2.
-  int split, qb;
-  {
+  // Workgroup -> rows and queries.  Dense: (split, query block); workgroups
+  // are dealt to the 8 XCDs round-robin by id, and with xcd_major XCD j gets
+  // splits j, j + 8, ... for every query block, split-major, so the
+  // workgroups that stream the same base rows run together on one XCD and
+  // share its L2.  IVF: one list and up to 128 (query, probe) pairs.
+  int q, seg;             // the lane's query, its output segment pair (2 x)
+  bool wave_on, qvalid;
+  int64_t r0;
+  int nrows;
+  uint32_t idbase;        // id of the stream's row 0 for this lane
+  if constexpr (MODE == 0) {
+    int split, qb;
     const int id = blockIdx.x;
     if (a.xcd_major) {
       const int slot = id >> 3;
@@ -169,17 +178,30 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       split = id % a.nsplit;
       qb = id / a.nsplit;
     }
+    const int q0w = qb * kQueriesPerBlock + wave * 32;
+    q = q0w + col;
+    wave_on = q0w < a.nq;
+    qvalid = q < a.nq;
+    r0 = (int64_t)split * a.rows_per_split;
+    const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+    nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+    seg = split;
+    idbase = (uint32_t)r0;
+  } else {
+    const int* it = a.items + 3 * blockIdx.x;
+    const int list = it[0], first = it[1], count = it[2];
+    r0 = a.offsets[list];
+    nrows = a.offsets[list + 1] - (int)r0;
+    const int li = wave * 32 + col;
+    wave_on = wave * 32 < count;
+    qvalid = li < count;
+    const int pair = qvalid ? a.pairs[first + li] : 0;
+    q = pair / a.P;
+    seg = pair % a.P;
+    idbase = qvalid ? (uint32_t)a.slots[pair] : 0u;
   }
-  const int q0w = qb * kQueriesPerBlock + wave * 32;
-  const int q = q0w + col;
-  const bool wave_on = q0w < a.nq;
-  const bool qvalid = q < a.nq;
   const int ld = a.ld;
   constexpr bool l2 = L2;
-
-  const int64_t r0 = (int64_t)split * a.rows_per_split;
-  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
-  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
   const int ntiles = (nrows + TR - 1) / TR;
 
   // buffer resources over this split's rows and norms
@@ -258,7 +280,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int S = bound_slots<T>();
   const bool share = a.mslots > 0;
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
-  const int myslot = share ? (2 * split + h) % a.mslots : 0;
+  const int myslot = share ? (2 * seg + h) % a.mslots : 0;
 
   if (ntiles > 0) {
     issue_loads();
@@ -274,8 +296,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     const int buf = t & 1;
     // the shared bound is read before the tile prefetch, so that waiting for
     // it (in the epilogue) does not wait for the prefetch
-    SharedBound<S> seen;
-    seen.load(gk);
+    SharedBound<S> seen{};
+    if constexpr (MODE != 2) seen.load(gk);
     // unconditional (past the last tile the offsets are out of range and
     // read zero), so the wait counts after the shared key stay static
     issue_loads();
@@ -307,7 +329,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
+      if (MODE != 2 && share) thr = fmaxf(thr, score_of_key(seen.bound()));
       const bool full = t + 1 < ntiles || nrows % TR == 0;
       bool inserted = false;
 #pragma unroll
@@ -327,13 +349,26 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
             for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
           }
         }
-        const uint32_t id0 = (uint32_t)(r0 + t * TR + 32 * r);
-        if (full)
+        const uint32_t id0 = idbase + (uint32_t)(t * TR + 32 * r);
+        if constexpr (MODE == 2) {
+          // the lane's 16 scores: rows 8 j + 4 h + u of the block, columns
+          // idbase + row
+          if (qvalid) {
+            float* dst = a.scores + (int64_t)(q - a.q0) * a.width + id0;
+            const int lim = nrows - t * TR - 32 * r;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+              if (m < lim) dst[m] = sc[i];
+            }
+          }
+        } else if (full) {
           inserted |= select_block<T, true>(K, I, thr, sc, h, id0, 32);
-        else
+        } else {
           inserted |= select_block<T, false>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
+        }
       }
-      if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
+      if (MODE != 2 && share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
         __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -341,8 +376,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     __syncthreads();
   }
 
-  if (qvalid) {
-    uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
+  if (MODE != 2 && qvalid) {
+    const int nseg = MODE == 0 ? a.nsplit : a.P;
+    uint64_t* dst = a.part + ((int64_t)q * (2 * nseg) + 2 * seg + h) * T;
 #pragma unroll
     for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
   }
@@ -706,6 +742,61 @@ __global__ void bounds_init_kernel(uint32_t* p, int64_t count, int S, int m) {
   if (i < count) p[i] = (int)(i % S) < m ? 0u : 0xffffffffu;
 }
 
+// IVF-Flat candidate scores for any ld (the VALU route for rows longer
+// than the fused kernel takes): one workgroup per item, one (query, row)
+// pair per thread step.  L2: 2 q.b - |b|^2.
+__global__ __launch_bounds__(256) void ivf_scores_any_kernel(FusedArgs a) {
+  const int* it = a.items + 3 * blockIdx.x;
+  const int list = it[0], first = it[1], count = it[2];
+  const int64_t r0 = a.offsets[list];
+  const int nrows = a.offsets[list + 1] - (int)r0;
+  const float* base = (const float*)a.base;
+  const float* queries = (const float*)a.queries;
+  for (int64_t e = threadIdx.x; e < (int64_t)count * nrows; e += 256) {
+    const int li = (int)(e / nrows), r = (int)(e % nrows);
+    const int pair = a.pairs[first + li];
+    const int q = pair / a.P;
+    const float* qr = queries + (int64_t)q * a.ld;
+    const float* br = base + (r0 + r) * a.ld;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < a.ld; j += 4) {
+      const floatx4 x = *(const floatx4*)(qr + j), y = *(const floatx4*)(br + j);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = __builtin_fmaf(x[u], y[u], acc[u]);
+    }
+    const float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const float sc = a.metric == kL2 ? __builtin_fmaf(2.0f, dot, -a.bnorm[r0 + r]) : dot;
+    a.scores[(int64_t)(q - a.q0) * a.width + a.slots[pair] + r] = sc;
+  }
+}
+
+// Candidate columns -> ids (see IvfMapArgs).
+__global__ void ivf_map_kernel(IvfMapArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)a.rows * a.k) return;
+  const int row = (int)(e / a.k);
+  const int q = a.qsel ? a.qsel[row] : a.q0 + row;
+  const int c = a.ids[e];
+  if (c < 0) return;
+  const int* pr = a.probes + (int64_t)q * a.P;
+  const int* sl = a.slots + (int64_t)q * a.P;
+  for (int p = 0; p < a.P; ++p) {
+    const int list = pr[p];
+    const int len = a.offsets[list + 1] - a.offsets[list];
+    if (c >= sl[p] && c < sl[p] + len) {
+      a.ids[e] = a.indices[a.offsets[list] + (c - sl[p])];
+      return;
+    }
+  }
+  a.ids[e] = -1;  // buffer padding
+  if (a.dists) a.dists[e] = a.pad;
+}
+
+__global__ void fill_f32_kernel(float* p, int64_t count, float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = v;
+}
+
 __global__ void zero_u32_kernel(uint32_t* p, int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < count) p[i] = 0u;
@@ -806,6 +897,46 @@ int dh_for(int ld, bool f16) {
 }
 
 bool t_ok(int T) { return T == 4 || T == 8 || T == 10 || T == 16; }
+
+template <int DH, int T>
+hipError_t ivf_inst(const FusedArgs& a, hipStream_t s, int mode) {
+  if (a.n_items <= 0) return hipSuccess;
+  const dim3 grid(a.n_items);
+  if (mode == 1) {
+    if (a.metric == kL2)
+      hipLaunchKernelGGL((fused_kernel<false, DH, T, true, 1>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((fused_kernel<false, DH, T, false, 1>), grid, dim3(256), 0, s, a);
+  } else {
+    if (a.metric == kL2)
+      hipLaunchKernelGGL((fused_kernel<false, DH, 4, true, 2>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((fused_kernel<false, DH, 4, false, 2>), grid, dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+template <int DH>
+hipError_t ivf_dispatch_t(const FusedArgs& a, hipStream_t s, int mode) {
+  if (mode == 2) return ivf_inst<DH, 4>(a, s, mode);
+  switch (a.T) {
+    case 4: return ivf_inst<DH, 4>(a, s, mode);
+    case 8: return ivf_inst<DH, 8>(a, s, mode);
+    case 10: return ivf_inst<DH, 10>(a, s, mode);
+    case 16: return ivf_inst<DH, 16>(a, s, mode);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t ivf_launch(const FusedArgs& a, hipStream_t s, int mode) {
+  switch (dh_for(a.ld, false)) {
+    case 16: return ivf_dispatch_t<16>(a, s, mode);
+    case 32: return ivf_dispatch_t<32>(a, s, mode);
+    case 64: return ivf_dispatch_t<64>(a, s, mode);
+    case 128: return ivf_dispatch_t<128>(a, s, mode);
+  }
+  return hipErrorInvalidValue;
+}
 
 template <bool F16, int DH>
 hipError_t dispatch_t(const FusedArgs& a, hipStream_t s) {
@@ -910,6 +1041,31 @@ hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s) {
     case 128: return dispatch_t<true, 128>(a, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_ivf_select(const FusedArgs& a, hipStream_t s) { return ivf_launch(a, s, 1); }
+
+hipError_t launch_ivf_scores(const FusedArgs& a, hipStream_t s) { return ivf_launch(a, s, 2); }
+
+hipError_t launch_ivf_scores_any(const FusedArgs& a, hipStream_t s) {
+  if (a.n_items <= 0) return hipSuccess;
+  if (a.ld % 4 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ivf_scores_any_kernel, dim3(a.n_items), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_ivf_map(const IvfMapArgs& a, hipStream_t s) {
+  const int64_t total = (int64_t)a.rows * a.k;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ivf_map_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p,
+                     count, v);
+  return hipGetLastError();
 }
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {

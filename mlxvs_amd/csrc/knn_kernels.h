@@ -64,6 +64,19 @@ struct FusedArgs {
   int mslots;            // ceil(k / T) when <= bound_slots_for(T), else 0 (no sharing)
   int nqb;               // query blocks, ceil(nq / 128)
   int xcd_major;         // nsplit % 8 == 0: XCD-major workgroup order (see kernel)
+  // IVF-Flat list scan (launch_ivf_select / launch_ivf_scores): one workgroup
+  // per item -- a list and up to 128 (query, probe) pairs that probe it --
+  // instead of per (split, query block); a lane's candidates are numbered by
+  // their column in the query's candidate buffer (slot of the probe + row).
+  const int* items;      // [n_items][3]: list, first pair, pairs
+  const int* pairs;      // [*] q * P + p, grouped by list
+  const int* offsets;    // [lists + 1]: rows of each list in base
+  const int* slots;      // [nq * P]: buffer column of the probe's first row
+  int P;                 // probes per query
+  int n_items;
+  float* scores;         // scores mode: [bq][width] buffers of queries q0 ..
+  int64_t width;
+  int q0;
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
@@ -90,6 +103,38 @@ bool deep_bits_supported(int ld, int T);
 int deep_bits_blocks_per_cu(int T);
 // the packed row length with an instance for nbytes-byte codes (0: none)
 int bits_row_bytes(int nbytes);
+
+// IVF-Flat: select mode writes part [nq][2P][T] (segment 2p + h) with
+// candidate columns as ids; scores mode writes the candidate scores (L2:
+// 2 q.b - |b|^2) of queries q0 .. into scores [.][width] (other entries are
+// left as they are).  fp32, ld a multiple of 4 up to 256.
+hipError_t launch_ivf_select(const FusedArgs& a, hipStream_t s);
+hipError_t launch_ivf_scores(const FusedArgs& a, hipStream_t s);
+// The same scores for any ld, on the VALU (rows of deep indexes).
+hipError_t launch_ivf_scores_any(const FusedArgs& a, hipStream_t s);
+
+// Candidate columns -> ids in place (reference src/ivf.cpp:203-213): column
+// c of query q lies in probe p with slots[q P + p] <= c < slots + the list's
+// length; id = indices[offsets[list] + c - slots].  A column past the
+// query's candidates (buffer padding) becomes -1 / pad.
+struct IvfMapArgs {
+  int32_t* ids;          // [rows][k], columns in, ids out
+  float* dists;          // [rows][k] (may be null)
+  int rows;
+  int k;
+  const int* qsel;       // [rows] query of each output row (null: identity from q0)
+  int q0;
+  const int* probes;     // [nq][P]
+  const int* slots;      // [nq][P]
+  const int* offsets;    // [lists + 1]
+  const int32_t* indices;// [n]
+  int P;
+  float pad;             // distance of a missing neighbour
+};
+hipError_t launch_ivf_map(const IvfMapArgs& a, hipStream_t s);
+
+// Fill a float array (candidate buffers start at -inf).
+hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s);
 
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.

@@ -70,19 +70,24 @@ __device__ __forceinline__ uint32_t key_nz(float v) {
 }
 
 // Inserts (kc, ic); kc = 0 is a no-op, so lanes that have nothing to insert
-// pass 0 instead of branching.  The candidate walks down the list and swaps
-// with every entry it beats: one 32-bit compare and four selects per slot.
+// pass 0 instead of branching.  The candidate takes the first slot whose key
+// it beats (an equal key keeps the entry: it has the lower id), and from
+// there on every entry shifts down one slot: the entry carried out of a slot
+// is older, so it has a lower id than any equal-key entry below it and must
+// stay in front of it.  One 32-bit compare, one OR and four selects per slot.
 template <int T>
 __device__ __forceinline__ void stream_insert(uint32_t (&K)[T], uint32_t (&I)[T], uint32_t kc,
                                               uint32_t ic) {
+  bool moved = false;
 #pragma unroll
   for (int j = 0; j < T; ++j) {
-    const bool b = kc > K[j];
+    const bool b = moved || kc > K[j];
     const uint32_t tk = K[j], ti = I[j];
     K[j] = b ? kc : tk;
     I[j] = b ? ic : ti;
     kc = b ? tk : kc;
     ic = b ? ti : ic;
+    moved = b;
   }
 }
 

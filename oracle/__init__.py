@@ -47,6 +47,7 @@ def lib():
         L.oracle_f16_to_f32.argtypes = [vp, i64, vp]
         L.oracle_pack_words.argtypes = [vp, i64, ci, vp]
         L.oracle_key.argtypes = [ctypes.c_float]
+        L.oracle_ivf_flat.argtypes = [vp, ci, vp, vp, vp, ci, ci, vp, i64, ci, ci, ci, vp, vp]
         L.oracle_key.restype = ctypes.c_uint32
         for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_self_graph_rows",
                   "oracle_hamming",
@@ -84,6 +85,27 @@ def knn(base, queries, k, metric="l2", nthreads=None):
                               nthreads or threads(), _p(ids), _p(dist))
     if rc:
         raise ValueError(f"oracle_knn_f32 rejected the arguments ({rc})")
+    return ids, dist
+
+
+def ivf_flat(centers, data, indices, offsets, queries, k, n_probes, metric="l2",
+             nthreads=None):
+    """Restated ivf_flat_search (src/ivf.cpp:164-221, 327-416) over a given
+    index: centers [lists, d], data [n, d] grouped by list (unit rows for
+    cosine), indices [n], offsets [lists + 1]."""
+    c = np.ascontiguousarray(centers, dtype=np.float32)
+    x = np.ascontiguousarray(data, dtype=np.float32)
+    ix = np.ascontiguousarray(indices, dtype=np.int32)
+    off = np.ascontiguousarray(offsets, dtype=np.int32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq = q.shape[0]
+    ids = np.empty((nq, k), np.int32)
+    dist = np.empty((nq, k), np.float32)
+    rc = lib().oracle_ivf_flat(_p(c), c.shape[0], _p(x), _p(ix), _p(off), c.shape[1],
+                               _m(metric), _p(q), nq, k, n_probes, nthreads or threads(),
+                               _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_ivf_flat rejected the arguments ({rc})")
     return ids, dist
 
 

@@ -23,6 +23,15 @@
  *      src/ivf_kernels.h:549-595: popcount of XOR over little-endian uint32
  *      words (zero padded), ascending, lowest id among equal distances;
  *      empty inputs give -1 / +inf.
+ *  - IVF-Flat search            src/ivf.cpp:164-221 (probe, finish),
+ *      327-416 (ivf_flat_search), src/ivf_kernels.h:16-99 (the list scan):
+ *      cosine queries unit-normalised; the n_probes nearest centers by L2
+ *      (L2, cosine) or inner product; every query's candidate buffer holds
+ *      the rows of its probed lists in probe order (column = offset of the
+ *      list in the buffer + row), scored -sum (q - b)^2 (L2) or q.b; the best
+ *      min(k, width) columns by key, then lowest column; a pick whose score is
+ *      infinite or that is buffer padding is missing (-1, +inf for L2, -inf
+ *      otherwise); L2 distance = -score.
  *  - self k-NN graph            src/all_neighbors.cpp:250-263 (k + 1
  *      neighbours) and 56-95 (merge_lists: drop -1 and the row itself, sort by
  *      distance, keep k, pad -1 / +inf for L2 or -inf otherwise).
@@ -450,3 +459,122 @@ int oracle_hamming(const uint8_t* rows, int64_t n, const uint8_t* queries,
 
 /* The order-preserving key, exported so tests can pin it. */
 uint32_t oracle_key(float v) { return key_of(v); }
+
+/* ---- IVF-Flat search ---------------------------------------------------- */
+
+typedef struct {
+  const float* data;
+  const int32_t* indices;
+  const int32_t* offsets;
+  const float* queries; /* unit rows for cosine */
+  const int32_t* probes; /* [nq, P] */
+  int64_t width;
+  int d, k, P, l2;
+  int32_t* ids;
+  float* dists;
+} ivf_ctx;
+
+static void ivf_rows(void* p, int64_t lo, int64_t hi) {
+  ivf_ctx* c = (ivf_ctx*)p;
+  const int kk = (int)(c->k < c->width ? c->k : c->width);
+  uint64_t* hv = (uint64_t*)malloc(sizeof(uint64_t) * (kk > 0 ? kk : 1));
+  float* hs = (float*)malloc(sizeof(float) * (kk > 0 ? kk : 1));
+  int32_t* hid = (int32_t*)malloc(sizeof(int32_t) * (kk > 0 ? kk : 1));
+  pair_t* sel = (pair_t*)malloc(sizeof(pair_t) * (kk > 0 ? kk : 1));
+  for (int64_t q = lo; q < hi; ++q) {
+    const float* qr = c->queries + (size_t)q * c->d;
+    heap_t h = {hv, hs, hid, 0, kk};
+    int64_t col = 0;
+    for (int pi = 0; pi < c->P; ++pi) {
+      const int32_t list = c->probes[(size_t)q * c->P + pi];
+      const int32_t start = c->offsets[list], len = c->offsets[list + 1] - start;
+      for (int32_t r = 0; r < len; ++r, ++col) {
+        const float* b = c->data + (size_t)(start + r) * c->d;
+        float s;
+        if (c->l2) {
+          float acc = 0.0f;
+          for (int j = 0; j < c->d; ++j) {
+            const float u = qr[j] - b[j];
+            acc -= u * u;
+          }
+          s = acc;
+        } else {
+          s = dot8(qr, b, c->d);
+        }
+        heap_push(&h, rank_of(s, (int32_t)col), s, (int32_t)col);
+      }
+    }
+    /* buffer padding up to the width: score -inf, no row */
+    for (int64_t pad = col; pad < c->width && pad < col + kk; ++pad)
+      heap_push(&h, rank_of(-INFINITY, (int32_t)pad), -INFINITY, (int32_t)pad);
+    const int keff = h.size;
+    for (int i = 0; i < keff; ++i) { sel[i].s = h.s[i]; sel[i].id = h.id[i]; }
+    qsort(sel, keff, sizeof(pair_t), before_cmp);
+    for (int i = 0; i < c->k; ++i) {
+      const size_t o = (size_t)q * c->k + i;
+      int32_t id = -1;
+      float dist = c->l2 ? INFINITY : -INFINITY;
+      if (i < keff && !isinf(sel[i].s) && sel[i].id < col) {
+        /* column -> probe, row -> data position -> id */
+        int64_t base = 0;
+        for (int pi = 0; pi < c->P; ++pi) {
+          const int32_t list = c->probes[(size_t)q * c->P + pi];
+          const int32_t len = c->offsets[list + 1] - c->offsets[list];
+          if (sel[i].id < base + len) {
+            id = c->indices[c->offsets[list] + (sel[i].id - base)];
+            break;
+          }
+          base += len;
+        }
+        dist = c->l2 ? -sel[i].s : sel[i].s;
+      }
+      c->ids[o] = id;
+      c->dists[o] = dist;
+    }
+  }
+  free(hv); free(hs); free(hid); free(sel);
+}
+
+/*
+ * IVF-Flat search of queries [nq, d] in an index: centers [lists, d], data
+ * [n, d] grouped by list (unit rows for cosine), indices [n], offsets
+ * [lists + 1].  n_probes is clamped to [1, lists]; 1 <= k <= 256.
+ * ids [nq, k], dists [nq, k].
+ */
+int oracle_ivf_flat(const float* centers, int lists, const float* data,
+                    const int32_t* indices, const int32_t* offsets, int d, int metric,
+                    const float* queries, int64_t nq, int k, int n_probes, int threads,
+                    int32_t* ids, float* dists) {
+  if (d < 1 || lists < 1 || nq < 0 || k < 1 || k > 256 || metric < 0 || metric > 2)
+    return ORACLE_EINVAL;
+  const int P = n_probes < 1 ? 1 : (n_probes > lists ? lists : n_probes);
+  float* uq = NULL;
+  if (metric == M_COS) {
+    uq = (float*)malloc(sizeof(float) * (size_t)(nq ? nq : 1) * d);
+    if (!uq) return ORACLE_ENOMEM;
+    unit_ctx cq = {queries, d, uq};
+    parallel_for(nq, threads, unit_part, &cq);
+  }
+  const float* q = uq ? uq : queries;
+  int32_t* probes = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nq ? nq : 1) * P);
+  float* pd = (float*)malloc(sizeof(float) * (size_t)(nq ? nq : 1) * P);
+  if (!probes || !pd) { free(uq); free(probes); free(pd); return ORACLE_ENOMEM; }
+  /* src/ivf.cpp:171-178: inner product for inner product, else L2 */
+  int rc = oracle_knn_f32(centers, lists, q, nq, d, P, metric == M_IP ? M_IP : M_L2, threads,
+                          probes, pd);
+  if (rc == ORACLE_OK) {
+    int64_t width = 1;
+    for (int64_t i = 0; i < nq; ++i) {
+      int64_t w = 0;
+      for (int pi = 0; pi < P; ++pi) {
+        const int32_t list = probes[(size_t)i * P + pi];
+        w += offsets[list + 1] - offsets[list];
+      }
+      if (w > width) width = w;
+    }
+    ivf_ctx c = {data, indices, offsets, q, probes, width, d, k, P, metric == M_L2, ids, dists};
+    parallel_for(nq, threads, ivf_rows, &c);
+  }
+  free(uq); free(probes); free(pd);
+  return rc;
+}

@@ -176,6 +176,41 @@ def test_ties_keep_lowest_ids(engine):
     assert np.array_equal(first, g["ids"])
 
 
+@pytest.mark.parametrize("d,dtype", [(3, np.float32), (3, np.float16), (300, np.float32)])
+def test_tie_pushed_down_keeps_lower_id(engine, d, dtype):
+    # One lane's stream (rows 0-3, 8-11, ... share a lane): rows 0 and 1 tie at
+    # distance 10, rows 2 and 3 are nearer, then row 8 (distance 1) pushes the
+    # list down one slot.  With k = 4 the tie is at the edge: row 0 (the
+    # lower id) must stay and row 1 go.  (A carried entry once lost an
+    # equal-key comparison against the newer entry below it.)
+    x = np.zeros((64, d), np.float32)
+    x[:, 0] = 10.0                      # distance 100 for the other rows
+    x[0, :3] = (1, 3, 0)                # 10
+    x[1, :3] = (3, 1, 0)                # 10
+    x[2, :3] = (1, 2, 0)                # 5
+    x[3, :3] = (1, 1, 2)                # 6
+    x[8, :3] = (1, 0, 0)                # 1
+    q = np.zeros((1, d), np.float32)
+    ids, dist = engine.brute_force_knn(x.astype(dtype), q.astype(dtype), 4, "l2")
+    assert ids.tolist() == [[8, 2, 3, 0]]
+    assert dist.tolist() == [[1.0, 5.0, 6.0, 10.0]]
+
+
+def test_tie_pushed_down_hamming(engine):
+    # the same pattern on Hamming codes (int8 MFMA route): distances 3, 3, 1,
+    # 2, then 0 for rows 0, 1, 2, 3, 8
+    codes = np.full((64, 16), 0xFF, np.uint8)  # distance 128 for the others
+    q = np.zeros((1, 16), np.uint8)
+    codes[0] = 0; codes[0, 0] = 0b0111
+    codes[1] = 0; codes[1, 1] = 0b0111
+    codes[2] = 0; codes[2, 0] = 0b1
+    codes[3] = 0; codes[3, 0] = 0b11
+    codes[8] = 0
+    ids, dist = engine.hamming_knn(codes, q, 4)
+    assert ids.tolist() == [[8, 2, 3, 0]]
+    assert dist.tolist() == [[0.0, 1.0, 2.0, 3.0]]
+
+
 def test_massive_ties_large_k(engine):
     # every row at the same distance: the k lowest ids, for k above the
     # register list length (the merge's check sends these to the

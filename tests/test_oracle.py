@@ -227,3 +227,86 @@ def test_f16_to_f32_all_patterns(oracle):
     same = (got == want) | (np.isnan(got) & np.isnan(want))
     assert same.all()
     assert np.array_equal(np.signbit(got), np.signbit(want))
+
+
+# ---- IVF-Flat search (src/ivf.cpp:164-221, 327-416; src/ivf_kernels.h:16-99) --------
+
+def ivf_index(x, lists, seed):
+    """A deterministic index: centers = every (n // lists)-th row, each row
+    in the list of its nearest center (float64, lowest index on ties), rows of
+    a list in input order.  Some lists may stay empty."""
+    c = x[:: max(1, x.shape[0] // lists)][:lists].astype(np.float32)
+    d2 = ((x[:, None, :].astype(np.float64) - c[None].astype(np.float64)) ** 2).sum(-1)
+    lab = d2.argmin(1)
+    order = np.argsort(lab, kind="stable")
+    off = np.concatenate([[0], np.cumsum(np.bincount(lab, minlength=lists))]).astype(np.int32)
+    return c, x[order].astype(np.float32), order.astype(np.int32), off
+
+
+def ivf_float64(centers, data, indices, offsets, queries, k, n_probes, metric):
+    """Independent float64 restatement of the reference's IVF-Flat search."""
+    c, x, q = (a.astype(np.float64) for a in (centers, data, queries))
+    lists = c.shape[0]
+    P = min(max(n_probes, 1), lists)
+    if metric == "inner_product":
+        ps = q @ c.T
+    else:
+        ps = -((q[:, None, :] - c[None]) ** 2).sum(-1)
+    probes = np.array([np.lexsort((np.arange(lists), -row))[:P] for row in ps])
+    sizes = np.diff(offsets)
+    width = max(1, int(sizes[probes].sum(1).max()))
+    kk = min(k, width)
+    ids = np.full((q.shape[0], k), -1, np.int32)
+    dist = np.full((q.shape[0], k), np.inf if metric == "l2" else -np.inf, np.float32)
+    for i in range(q.shape[0]):
+        pos = np.concatenate([np.arange(offsets[l], offsets[l + 1]) for l in probes[i]])
+        if metric == "l2":
+            sc = -((x[pos] - q[i]) ** 2).sum(1)
+        else:
+            sc = x[pos] @ q[i]
+        cols = np.arange(pos.size)
+        order = np.lexsort((cols, -sc))[:kk]
+        ids[i, :order.size] = indices[pos[order]]
+        dist[i, :order.size] = -sc[order] if metric == "l2" else sc[order]
+    return ids, dist
+
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("n_probes,k", [(1, 5), (3, 10), (8, 40), (100, 7)])
+def test_ivf_flat_vs_float64(oracle, metric, n_probes, k):
+    # integer data: every score is exact in float32, so the restatement must
+    # equal the float64 one bit for bit, including its tie order (probe
+    # order, then row order) and the -1 padding when the lists run short
+    x = int_rows(3000, 12, 21, hi=6)
+    q = int_rows(70, 12, 22, hi=6)
+    c, data, ind, off = ivf_index(x, 37, 0)
+    ids, dist = oracle.ivf_flat(c, data, ind, off, q, k, n_probes, metric)
+    wi, wd = ivf_float64(c, data, ind, off, q, k, n_probes, metric)
+    assert np.array_equal(ids, wi)
+    assert np.array_equal(dist, wd)
+
+
+def test_ivf_flat_all_lists_is_brute_force(oracle):
+    x = int_rows(2000, 8, 23, hi=8)
+    q = int_rows(50, 8, 24, hi=8)
+    c, data, ind, off = ivf_index(x, 20, 0)
+    ids, dist = oracle.ivf_flat(c, data, ind, off, q, 10, 20, "l2")
+    bid, bdist = oracle.knn(x, q, 10, "l2")
+    assert np.array_equal(dist, bdist)  # same distances; ties may differ in id
+
+
+def test_ivf_flat_short_lists_and_cosine(oracle):
+    x = int_rows(300, 6, 25, hi=8)
+    c, data, ind, off = ivf_index(x, 30, 0)
+    q = int_rows(10, 6, 26, hi=8)
+    ids, dist = oracle.ivf_flat(c, data, ind, off, q, 256, 2, "l2")
+    wi, wd = ivf_float64(c, data, ind, off, q, 256, 2, "l2")
+    assert np.array_equal(ids, wi) and np.array_equal(dist, wd)
+    assert (ids[:, -1] == -1).all() and np.isinf(dist[:, -1]).all()
+    # cosine: queries unit-normalised, data stored as unit rows
+    u = x / np.maximum(np.linalg.norm(x, axis=1, keepdims=True), 1e-30)
+    c, data, ind, off = ivf_index(u.astype(np.float32), 30, 0)
+    ids, dist = oracle.ivf_flat(c, data, ind, off, q, 5, 4, "cosine")
+    qn = q / np.linalg.norm(q, axis=1, keepdims=True)
+    wi, wd = ivf_float64(c, data, ind, off, qn, 5, 4, "cosine")
+    np.testing.assert_allclose(dist, wd, atol=1e-6)
