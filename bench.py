@@ -25,7 +25,7 @@ The same JSON line carries:
   check         the last step's answers for the first 64 queries against the
                 float64 golden fixture (bit-exact, integer-valued data).
 
-Other workloads (c1, c3, c3cos, c4, c5) are for measurement runs; the
+Other workloads (c1, c3, c3cos, c4, c5, ivf) are for measurement runs; the
 driver's line is the default.  --workload copy times a 1 GiB device copy, the
 reference reading for scaling HBM byte counters.
 """
@@ -84,6 +84,16 @@ def workload(name: str):
         q, _ = synth.c4_queries(gen, 1_000_000, 2, 0, 10_000)
         return dict(kind="hamming", base=base, q=q, k=100, metric="hamming",
                     desc="c4: exact Hamming kNN k=100, 1M x 1024-bit codes, 10k queries")
+    if name == "ivf":
+        from mlxvs_amd import ivf_flat_build
+
+        cen = synth.c2_centres()
+        base = synth.chunked(lambda lo, hi: synth.c2_rows(1, lo, hi, centres=cen), 1_000_000)
+        q = synth.chunked(lambda lo, hi: synth.c2_rows(2, lo, hi, centres=cen), 10_000)
+        index = ivf_flat_build(base, "l2", n_lists=1024, kmeans_n_iters=10, seed=42)
+        return dict(kind="ivf", base=base, q=q, k=10, metric="l2", index=index, n_probes=20,
+                    desc="ivf: IVF-Flat L2 k=10, c2 rows (1M x 128 fp32), 1024 lists, "
+                         "20 probes, 10k queries")
     if name == "c5":
         cen = synth.c5_centres()
         x = synth.chunked(lambda lo, hi: synth.c5_rows(1, lo, hi, centres=cen), 200_000)
@@ -123,6 +133,10 @@ def cpu_baseline(w, sample: int):
     elif w["kind"] == "self":
         x = oracle.f16_to_f32(base)
         oracle.knn(x, x[:sample], w["k"] + 1, w["metric"], nthreads=threads)
+    elif w["kind"] == "ivf":
+        c, data, ind, off = w["index"]
+        oracle.ivf_flat(c, data, ind, off, q, w["k"], w["n_probes"], w["metric"],
+                        nthreads=threads)
     else:
         oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
     dt = time.perf_counter() - t0
@@ -156,7 +170,12 @@ def main() -> int:
     base, q, k = w["base"], w["q"], w["k"]
     n, nq = base.shape[0], q.shape[0]
     d = base.shape[1]
-    db = _hip.DeviceBuffer.from_array(base)
+    if w["kind"] == "ivf":
+        c, data, ind, off = w["index"]
+        dix = [_hip.DeviceBuffer.from_array(a) for a in (c, data, ind, off)]
+        db = dix[1]
+    else:
+        db = _hip.DeviceBuffer.from_array(base)
     dq = db if w["kind"] == "self" else _hip.DeviceBuffer.from_array(q)
     di = _hip.DeviceBuffer(nq * k * 4)
     dd = _hip.DeviceBuffer(nq * k * 4)
@@ -168,6 +187,11 @@ def main() -> int:
                                              f16=base.dtype == np.float16)
         elif w["kind"] == "hamming":
             mlxvs_amd.hamming_knn_device(db.value, n, dq.value, nq, d, k, di.value, dd.value)
+        elif w["kind"] == "ivf":
+            mlxvs_amd.ivf_flat_search_device(dix[0].value, c.shape[0], dix[1].value, n,
+                                             dix[2].value, dix[3].value, d, w["metric"],
+                                             dq.value, nq, k, di.value, dd.value,
+                                             n_probes=w["n_probes"])
         else:
             mlxvs_amd.knn_self_graph_device(db.value, n, d, k, w["metric"], di.value,
                                             dd.value, f16=base.dtype == np.float16)
@@ -202,7 +226,15 @@ def main() -> int:
     kname = max(stages, key=lambda s_: stages[s_][1])
     cnt, tot = stages[kname]
     per = tot / max(cnt, 1) / 1e3  # seconds per launch
-    if w["kind"] == "hamming" and kname == "hamming_mfma":
+    if w["kind"] == "ivf" and kname == "ivf_scan":
+        # 2 d flops per (query, candidate row) of the probed lists
+        c, data, ind, off = w["index"]
+        probes = mlxvs_amd.kmeans_predict(q, c, w["n_probes"])
+        cands = float(np.diff(off)[probes].sum())
+        flops = 2.0 * d * cands / (cnt / args.steps)
+        roof = {"bound": "mfma", "achieved": round(flops / per / 1e12, 2),
+                "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s", "candidates_per_query": round(cands / nq, 1)}
+    elif w["kind"] == "hamming" and kname == "hamming_mfma":
         # the int8 MFMA route: 2 ops (multiply, add) per code bit and pair
         ops = 2.0 * nq * n * 8 * d / (cnt / args.steps)  # per launch
         roof = {"bound": "mfma", "achieved": round(ops / per / 1e12, 2),
@@ -233,7 +265,8 @@ def main() -> int:
 
     sample = args.cpu_sample
     if sample is None:
-        sample = {"c1": 100, "c2": 10000, "c3": 16, "c3cos": 16, "c4": 256, "c5": 512}[args.workload]
+        sample = {"c1": 100, "c2": 10000, "c3": 16, "c3cos": 16, "c4": 256, "c5": 512,
+                  "ivf": 10000}[args.workload]
     cpu = cpu_baseline(w, min(sample, nq)) if sample else None
 
     line = {

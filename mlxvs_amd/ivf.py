@@ -24,8 +24,6 @@ python/bindings.cpp:283-361, src/ivf.cpp:236-416):
 
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 
 __all__ = ["IvfFlatIndex", "ivf_flat_build", "ivf_flat_extend", "ivf_flat_search"]
@@ -119,9 +117,12 @@ def ivf_flat_build(rows, metric="l2", *, n_lists=1024, kmeans_n_iters=20,
     for _ in range(int(kmeans_n_iters)):
         lab = kmeans_predict(sample, centers)[:, 0]
         counts = np.bincount(lab, minlength=n_lists)
-        sums = np.zeros_like(centers, dtype=np.float64)
-        np.add.at(sums, lab, sample)
-        empty = counts == 0
+        order = np.argsort(lab, kind="stable")
+        starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+        sums = np.zeros(centers.shape, np.float64)
+        nz = counts > 0
+        sums[nz] = np.add.reduceat(sample[order].astype(np.float64), starts[nz], axis=0)
+        empty = ~nz
         centers = np.where(empty[:, None], centers,
                            sums / np.maximum(counts, 1)[:, None]).astype(np.float32)
         if empty.any():  # an empty list restarts at a random sample row
