@@ -506,9 +506,11 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int mslots = (k + T - 1) / T <= slots ? (k + T - 1) / T : 0;
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
+  // XCD order: the register-resident kernels share only the row tiles
+  // (split-major); the deep kernel streams query chunks too (split-minor)
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, mslots, (int)qblocks,
-                     plan.xcd ? 1 : 0};
+                     plan.xcd ? (use_deep ? 2 : 1) : 0};
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });
   else

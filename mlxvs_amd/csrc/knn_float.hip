@@ -170,14 +170,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   if constexpr (MODE == 0) {
     int split, qb;
     const int id = blockIdx.x;
-    if (a.xcd_major) {
-      const int slot = id >> 3;
-      split = (id & 7) + 8 * (slot / a.nqb);
-      qb = slot % a.nqb;
-    } else {
-      split = id % a.nsplit;
-      qb = id / a.nsplit;
-    }
+    tile_of_workgroup(id, a.nsplit, a.nqb, a.xcd_major, split, qb);
     const int q0w = qb * kQueriesPerBlock + wave * 32;
     q = q0w + col;
     wave_on = q0w < a.nq;
@@ -417,14 +410,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   int split, qb;
   {
     const int id = blockIdx.x;
-    if (a.xcd_major) {
-      const int slot = id >> 3;
-      split = (id & 7) + 8 * (slot / a.nqb);
-      qb = slot % a.nqb;
-    } else {
-      split = id % a.nsplit;
-      qb = id / a.nsplit;
-    }
+    tile_of_workgroup(id, a.nsplit, a.nqb, a.xcd_major, split, qb);
   }
   const int qb0 = qb * kQueriesPerBlock;
   const int q = qb0 + wave * 32 + col;

@@ -63,7 +63,7 @@ struct FusedArgs {
   uint32_t* gkey;        // [nq][bound_slots_for(T)] shared bounds (launch_bounds_init)
   int mslots;            // ceil(k / T) when <= bound_slots_for(T), else 0 (no sharing)
   int nqb;               // query blocks, ceil(nq / 128)
-  int xcd_major;         // nsplit % 8 == 0: XCD-major workgroup order (see kernel)
+  int xcd_major;         // workgroup order, tile_of_workgroup mode (1, 2: nsplit % 8 == 0)
   // IVF-Flat list scan (launch_ivf_select / launch_ivf_scores): one workgroup
   // per item -- a list and up to 128 (query, probe) pairs that probe it --
   // instead of per (split, query block); a lane's candidates are numbered by

@@ -146,6 +146,33 @@ __device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
   return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
 }
 
+// Workgroup id -> (split, query block) of the dense kernels.  The hardware
+// deals workgroups to the 8 XCDs round-robin by id (XCD id % 8, in order
+// id / 8 there), and each XCD has its own L2.
+//  mode 0: split = id % nsplit (no XCD grouping);
+//  mode 1 (nsplit % 8 == 0): XCD j gets splits j, j + 8, ... split-major, so
+//    the workgroups running together on an XCD stream the same base rows
+//    (queries held in registers: only the rows are shared);
+//  mode 2 (nsplit % 8 == 0): the same splits, split-minor, so the resident
+//    workgroups of an XCD cover a few splits x many query blocks and share
+//    both the row tiles and the query chunks in L2 (kernels that stream the
+//    queries too).
+__device__ __forceinline__ void tile_of_workgroup(int id, int nsplit, int nqb, int mode,
+                                                  int& split, int& qb) {
+  if (mode == 1) {
+    const int slot = id >> 3;
+    split = (id & 7) + 8 * (slot / nqb);
+    qb = slot % nqb;
+  } else if (mode == 2) {
+    const int slot = id >> 3, sx = nsplit >> 3;
+    split = (id & 7) + 8 * (slot % sx);
+    qb = slot / sx;
+  } else {
+    split = id % nsplit;
+    qb = id / nsplit;
+  }
+}
+
 // Per-query shared lower bounds on the k-th best score, kept in S slots of
 // gkey[q S .. q S + S).  Segment g publishes its list's T-th best key into
 // slot g % m (m = ceil(k / T) <= S; slots m .. S - 1 hold 0xffffffff and never
