@@ -44,31 +44,62 @@ __device__ __forceinline__ float load_elem(const void* x, int f16, int64_t i) {
 }
 
 // Squared norms of 256 rows per block.  The block stages [256 rows x 32
-// dims] in LDS with coalesced reads (32 lanes per 128-byte row segment), then
-// every thread sums its own row: element j into partial sum j % 8, partial
-// sums added pairwise -- the order of oracle/knn_oracle.c dot8, so the norms
-// are bit-identical to the CPU restatement's.
+// dims] slabs in LDS, then every thread sums its own row: element j into
+// partial sum j % 8, partial sums added pairwise -- the order of
+// oracle/knn_oracle.c dot8, so the norms are bit-identical to the CPU
+// restatement's.  VEC: 16-byte aligned rows whose length is a multiple of 16
+// bytes, fetched with coalesced 16-byte loads (8 threads per 128-byte fp32
+// row slab); otherwise element loads.
+template <bool F16, bool VEC>
 __global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
-  __shared__ float sh[256 * 33];  // odd stride: row r, dim j hits bank (r + j) % 32
+  constexpr int SS = 36;  // LDS row stride (floats): 16-byte rows, 8 rows hit distinct bank quads
+  __shared__ __align__(16) float sh[256 * SS];
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * 256;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int c0 = 0; c0 < a.d; c0 += 32) {
-    for (int e = tid; e < 256 * 32; e += 256) {
-      const int r = e >> 5, j = e & 31;
-      const int64_t row = row0 + r;
-      sh[r * 33 + j] = (row < a.n && c0 + j < a.d) ? load_elem(a.x, a.f16, row * a.ld + c0 + j) : 0.0f;
+    if constexpr (VEC) {
+      constexpr int EPV = F16 ? 8 : 4;         // elements per 16-byte vector
+      constexpr int VPR = 32 / EPV;            // vectors per row slab
+#pragma unroll
+      for (int j = 0; j < VPR; ++j) {
+        const int e = tid + 256 * j;
+        const int r = e / VPR, c = (e % VPR) * EPV;
+        const int64_t row = row0 + r;
+        float v[EPV];
+        if (row < a.n && c0 + c < a.d) {
+          if constexpr (F16) {
+            const halfx8 h = *(const halfx8*)((const _Float16*)a.x + row * a.ld + c0 + c);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = (float)h[u];
+          } else {
+            const floatx4 f = *(const floatx4*)((const float*)a.x + row * a.ld + c0 + c);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = f[u];
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < EPV; ++u) v[u] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < EPV; u += 4)
+          *(floatx4*)&sh[r * SS + c + u] = floatx4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+      }
+    } else {
+      for (int e = tid; e < 256 * 32; e += 256) {
+        const int r = e >> 5, j = e & 31;
+        const int64_t row = row0 + r;
+        sh[r * SS + j] =
+            (row < a.n && c0 + j < a.d) ? load_elem(a.x, F16, row * a.ld + c0 + j) : 0.0f;
+      }
     }
     __syncthreads();
 #pragma unroll
-    for (int j8 = 0; j8 < 32; j8 += 8) {
+    for (int j4 = 0; j4 < 32; j4 += 4) {
+      const floatx4 v = *(const floatx4*)&sh[tid * SS + j4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (c0 + j8 + u < a.d) {
-          const float v = sh[tid * 33 + j8 + u];
-          acc[u] += v * v;
-        }
-      }
+      for (int u = 0; u < 4; ++u)
+        if (c0 + j4 + u < a.d) acc[(j4 + u) & 7] += v[u] * v[u];
     }
     __syncthreads();
   }
@@ -997,8 +1028,16 @@ int fused_blocks_per_cu(int ld, int T, bool f16) {
 
 hipError_t launch_norms(const PrepArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  const int64_t blocks = (a.n + 255) / 256;
-  hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  const dim3 grid((unsigned)((a.n + 255) / 256));
+  const int esize = a.f16 ? 2 : 4;
+  const bool vec = (uintptr_t)a.x % 16 == 0 && ((int64_t)a.ld * esize) % 16 == 0;
+  if (a.f16) {
+    if (vec) hipLaunchKernelGGL((row_norms_kernel<true, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((row_norms_kernel<true, false>), grid, dim3(256), 0, s, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((row_norms_kernel<false, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((row_norms_kernel<false, false>), grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

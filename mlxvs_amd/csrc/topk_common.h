@@ -137,7 +137,11 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
     stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
     pm &= pm - 1u;
   }
-  thr = fmaxf(thr, score_of_key(K[T - 1]));  // NaN while the list has room
+  // Own filter: a later candidate needs a strictly larger key than the
+  // list's last (an equal key has a larger id and would not enter), so the
+  // threshold is the score of the next key up.  NaN while the list has room
+  // (K[T-1] = 0: key 1 is a NaN).  Shared bounds stay inclusive.
+  thr = fmaxf(thr, score_of_key(K[T - 1] + 1u));
   return any;
 }
 
