@@ -272,11 +272,14 @@ struct SplitPlan {
 // (such queries are redone exhaustively).  !ok when the merge cannot hold
 // that many.
 SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
-                      int64_t align, int64_t slots, bool xcd = false) {
+                      int64_t align, int64_t slots, bool xcd = false, int cap_mult = 1) {
   SplitPlan p;
   if (n <= 0) return p;
-  const int64_t cap = std::min<int64_t>(kern::kMaxMergeCandidates / ((int64_t)lanes * T),
-                                        (n + align - 1) / align);
+  // the merge sorts at most kMaxMergeCandidates per query; with k <= T a
+  // first merge level (merge_group) lifts that cap_mult-fold
+  const int64_t cap = std::min<int64_t>(
+      (int64_t)cap_mult * (kern::kMaxMergeCandidates / ((int64_t)lanes * T)),
+      (n + align - 1) / align);
   const int64_t need = k > T ? (4 * (int64_t)k + lanes * T - 1) / (lanes * T) : 1;
   const int64_t lo = std::max<int64_t>(need, (slots + nq_blocks - 1) / nq_blocks);
   const int64_t hi = std::min<int64_t>(cap, 6 * lo);
@@ -387,6 +390,9 @@ void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
+// Split count multiplier allowed by the two-level merge (k <= T).
+constexpr int kMergeGroups = 16;
+
 void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* ids,
                float* dists) {
   Arena& ar = ss.arena();
@@ -466,7 +472,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int tile_rows = use_deep ? kern::kDeepRows : 2 * kern::kTileRows;
   if ((use_deep || kern::fused_supported(kld, T, kf16)) && nq < (int64_t(1) << 31)) {
     const int bpc = use_deep ? kern::deep_blocks_per_cu(T) : kern::fused_blocks_per_cu(kld, T, kf16);
-    plan = plan_splits(n, qblocks, k, T, 2, tile_rows, device_slots(bpc), true);
+    plan = plan_splits(n, qblocks, k, T, 2, tile_rows, device_slots(bpc), true,
+                       k <= T ? kMergeGroups : 1);
     // a split's rows (and one tile past them) must stay inside one 32-bit
     // buffer range
     if (plan.ok && (plan.rows_per_split + tile_rows) * kld * esize >= (int64_t(1) << 31))
@@ -519,7 +526,20 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     });
   int* flags = nullptr;
   if (T < k) flags = ar.take<int>((size_t)nq);
-  kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};
+  const uint64_t* mpart = part;
+  int mseg = nseg;
+  if ((int64_t)nseg * T > kern::kMaxMergeCandidates) {
+    // k <= T: the T best of each group of segment lists first (groups of
+    // about 1,024 candidates: small sorts, many workgroups)
+    const int gs = std::max(1, 1024 / T);
+    const int ngroups = (nseg + gs - 1) / gs;
+    uint64_t* part2 = ar.take<uint64_t>((size_t)nq * ngroups * T);
+    kern::MergeGroupArgs mg{part, nseg, T, (int)nq, gs, ngroups, part2};
+    launch(s, "merge", [&] { return kern::launch_merge_group(mg, s); });
+    mpart = part2;
+    mseg = ngroups;
+  }
+  kern::MergeArgs ma{mpart, mseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};
   launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
   if (T >= k) return;
 

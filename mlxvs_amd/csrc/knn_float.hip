@@ -618,6 +618,20 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
 
 // ---- merge of segment lists ---------------------------------------------------
 
+__global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
+  __shared__ uint64_t buf[kMaxMergeCandidates];
+  const int q = blockIdx.x, g = blockIdx.y;
+  const int s0 = g * a.gs, s1 = min(a.nseg, s0 + a.gs);
+  const int C = (s1 - s0) * a.T;
+  const int P = pow2_at_least(C > 1 ? C : 1);
+  const uint64_t* src = a.part + ((int64_t)q * a.nseg + s0) * a.T;
+  for (int i = threadIdx.x; i < P; i += 256) buf[i] = i < C ? src[i] : 0;
+  __syncthreads();
+  bitonic_desc<256>(buf, P, IdentityOrder{});
+  uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.T;
+  for (int i = threadIdx.x; i < a.T; i += 256) dst[i] = i < P ? buf[i] : 0;
+}
+
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   __shared__ uint64_t buf[kMaxMergeCandidates];
   __shared__ uint64_t work[kMaxK];
@@ -1090,6 +1104,13 @@ hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s) {
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p,
                      count, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.ngroups <= 0) return hipSuccess;
+  if (a.gs * a.T > kMaxMergeCandidates) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(merge_group_kernel, dim3(a.nq, a.ngroups), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

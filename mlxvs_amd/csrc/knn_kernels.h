@@ -153,6 +153,20 @@ struct MergeArgs {
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
+// First merge level when the segments exceed what one workgroup sorts (only
+// for k <= T): the T best ranks of each group of gs consecutive segment
+// lists of a query, written as one list.  grid nq x ngroups.
+struct MergeGroupArgs {
+  const uint64_t* part;  // [nq][nseg][T]
+  int nseg;
+  int T;
+  int nq;
+  int gs;                // segments per group, gs * T <= kMaxMergeCandidates
+  int ngroups;
+  uint64_t* out;         // [nq][ngroups][T]
+};
+hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s);
+
 // Exhaustive path (exact for every input, used when the fused path does not
 // apply and for queries the merge flagged).  Scores of `rows` queries (query
 // i is queries[qsel[i]]) against all n base rows into S [rows][n], then a
