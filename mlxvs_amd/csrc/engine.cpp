@@ -393,6 +393,19 @@ int round_up(int x, int m) { return (x + m - 1) / m * m; }
 // Split count multiplier allowed by the two-level merge (k <= T).
 constexpr int kMergeGroups = 16;
 
+// Bound slots (mslots) a launch shares per query, 0 for none.  Every
+// segment list of a query reads the query's bound words once a tile and
+// raises them as it improves, so the words are one hot address per query:
+// with many segments per query (small batches: hundreds of splits) those
+// accesses cost more than the pruning saves (measured on c2 rows: 1 query,
+// 2,048 segments: 0.25 ms with the bound, 0.13 ms without; 10,000 queries,
+// 16 segments: 5% faster with it).
+constexpr int kMaxSharedSegments = 512;
+int shared_bound_slots(int k, int T, int slots, int nseg) {
+  const int m = (k + T - 1) / T;
+  return m <= slots && nseg <= kMaxSharedSegments ? m : 0;
+}
+
 void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* ids,
                float* dists) {
   Arena& ar = ss.arena();
@@ -443,11 +456,11 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     kq = uq;
   } else {
     if (l2) {
+      // the base norms are launched once the kernel is chosen (the streamed
+      // small-batch scan sums them itself)
       bnorm = ar.take<float>((size_t)n);
       qnorm = ar.take<float>((size_t)nq);
-      kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
       kern::PrepArgs pq{in.queries, nq, d, d, f16, qnorm, nullptr, nullptr, 0, 0};
-      launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
       launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
     }
     const bool aligned = ((uintptr_t)in.base % 16 == 0) && ((uintptr_t)in.queries % 16 == 0);
@@ -468,16 +481,30 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   const bool use_deep = deep && kern::deep_supported(kld, T, false);
-  // split alignment: whole tiles (deep: 128 rows; fused: 32 or 64)
-  const int tile_rows = use_deep ? kern::kDeepRows : 2 * kern::kTileRows;
+  // at most 32 queries (fp32, k <= T): rows streamed straight into registers
+  const bool use_stream = !kf16 && !deep && k <= T && kern::stream_supported(kld, T, nq);
+  // segment lists per split
+  const int lanes = use_stream ? 8 : 2;
+  // split alignment: whole tiles (deep: 128 rows; fused: 32 or 64; stream:
+  // a tile for each of the four wavefronts)
+  const int tile_rows = use_deep ? kern::kDeepRows : use_stream ? 4 * kern::kTileRows
+                                                               : 2 * kern::kTileRows;
   if ((use_deep || kern::fused_supported(kld, T, kf16)) && nq < (int64_t(1) << 31)) {
-    const int bpc = use_deep ? kern::deep_blocks_per_cu(T) : kern::fused_blocks_per_cu(kld, T, kf16);
-    plan = plan_splits(n, qblocks, k, T, 2, tile_rows, device_slots(bpc), true,
+    const int bpc = use_deep     ? kern::deep_blocks_per_cu(T)
+                    : use_stream ? kern::stream_blocks_per_cu(kld)
+                                 : kern::fused_blocks_per_cu(kld, T, kf16);
+    plan = plan_splits(n, qblocks, k, T, lanes, tile_rows, device_slots(bpc), !use_stream,
                        k <= T ? kMergeGroups : 1);
-    // a split's rows (and one tile past them) must stay inside one 32-bit
-    // buffer range
-    if (plan.ok && (plan.rows_per_split + tile_rows) * kld * esize >= (int64_t(1) << 31))
+    // a split's rows and the tiles prefetched past them (stream: two per
+    // wavefront) must stay inside one 32-bit buffer range
+    const int64_t past = use_stream ? 3 * tile_rows : tile_rows;
+    if (plan.ok && (plan.rows_per_split + past) * kld * esize >= (int64_t(1) << 31))
       plan.ok = false;
+  }
+
+  if (l2 && !(use_stream && plan.ok)) {
+    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
   }
 
   // fp32 rows for the exhaustive path (only when it runs)
@@ -507,10 +534,10 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     return;
   }
 
-  const int nseg = 2 * plan.nsplit;
+  const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
-  const int mslots = (k + T - 1) / T <= slots ? (k + T - 1) / T : 0;
+  const int mslots = shared_bound_slots(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
   // XCD order: the register-resident kernels share only the row tiles
@@ -520,6 +547,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
                      plan.xcd ? (use_deep ? 2 : 1) : 0};
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });
+  else if (use_stream)
+    launch(s, "stream_f32", [&] { return kern::launch_stream(fa, s); });
   else
     launch(s, kf16 ? "fused_f16" : "fused_f32", [&] {
       return kf16 ? kern::launch_fused_f16(fa, s) : kern::launch_fused_f32(fa, s);
@@ -613,7 +642,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   const int nseg = 2 * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
-  const int mslots = (k + T - 1) / T <= slots ? (k + T - 1) / T : 0;
+  const int mslots = shared_bound_slots(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
   kern::FusedArgs fa{bw, qw, bpop, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,

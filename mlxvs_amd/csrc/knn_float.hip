@@ -252,18 +252,17 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   // norm word of this thread (threads past the tile read beyond the range)
   uint32_t noff = tid < TR ? tid * 4u : 0x80000000u;
 
-  // the lane's query dims [h DH, h DH + DH): 16-byte buffer loads of the
-  // query row, zero past ld and for lanes without a query
+  // the lane's query dims [h DH, h DH + DH): 16-byte loads of the query
+  // row, zero past ld and for lanes without a query (plain global loads: a
+  // buffer resource per lane would be looped over the wavefront's queries)
   typedef E vecq __attribute__((ext_vector_type(EPV)));
   vecq qf[QV];
   {
     const E* qr = (const E*)a.queries + (int64_t)(qvalid ? q : 0) * ld;
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)qr, (short)0, qvalid ? ld * (int)sizeof(E) : 0, 0x00020000);
 #pragma unroll
     for (int v = 0; v < QV; ++v) {
-      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
-          rq, (h * DH + v * EPV) * (int)sizeof(E), 0, 0);
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (qvalid && h * DH + v * EPV < ld) w = *(const u32x4*)(qr + h * DH + v * EPV);
       qf[v] = __builtin_bit_cast(vecq, w);
     }
   }
@@ -611,6 +610,138 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
 
   if (qvalid) {
     uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
+#pragma unroll
+    for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
+  }
+}
+
+// ---- small batches: streamed rows, register-resident operands --------------------
+//
+// With at most 32 queries every base row is read once and the MFMA units
+// have little to do: HBM bounds the search.  stream_kernel: workgroups of
+// four independent wavefronts, no LDS and no barriers.  Each wavefront holds
+// the queries' fragments as fused_kernel does and walks its own 32-row tiles
+// of the split (tiles w, w + 4, ...), loading each lane's share of a row --
+// the MFMA A operand, lane (h, col) = row col -- straight into registers
+// from HBM, two tiles ahead.  The two lanes of a row take alternate 16-byte
+// vectors (lane h: dims 8v + 4h .. 8v + 4h + 3, the queries permuted
+// alike), so that each load reads 32 contiguous bytes of every row.  L2
+// needs no norm pass: a row's squared norm is summed from the same
+// registers (each lane its vectors, then the pair) and moved to the lanes of
+// the score layout.  Scores, epilogue and per-lane lists as fused_kernel.
+// Segments: eight per workgroup, 8 split + 2 w + h.
+template <int DH, int T, bool L2>
+__global__ __launch_bounds__(256, DH >= 64 ? 1 : 2) void stream_kernel(FusedArgs a) {
+  constexpr int QV = DH / 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x;
+  const int q = col;
+  const bool qvalid = q < a.nq;
+  const int ld = a.ld;
+  const int64_t r0 = (int64_t)split * a.rows_per_split;
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+  const int ntiles = (nrows + 31) / 32;
+  const int mine = ntiles > wave ? (ntiles - wave + 3) / 4 : 0;  // tiles wave, wave + 4, ...
+
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const float*)a.base + r0 * ld), (short)0, nrows * ld * 4, 0x00020000);
+
+  // the lane's query vectors (dims 8 v + 4 h ..), zero past ld and for
+  // lanes without a query
+  floatx4 qf[QV];
+  {
+    const float* qr = (const float*)a.queries + (int64_t)(qvalid ? q : 0) * ld;
+#pragma unroll
+    for (int v = 0; v < QV; ++v) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (qvalid && 8 * v + 4 * h < ld) w = *(const u32x4*)(qr + 8 * v + 4 * h);
+      qf[v] = __builtin_bit_cast(floatx4, w);
+    }
+  }
+
+  // The lane's vectors of tile i (the wavefront's i-th).  Rows past the
+  // split read zero.  Vectors from v = vlim on lie past ld and belong to the
+  // next row: they are zeroed where they are used (not at the load, which
+  // would wait for it), so that no value of another row reaches a score.
+  u32x4 A[2][QV];
+  const int vlim = min(QV, max(0, (ld - 4 * h + 7) / 8));
+  auto issue = [&](int slot, int i) {
+    const int tw = wave + 4 * i;
+    const uint32_t off = (uint32_t)(((tw * 32 + col) * ld + 4 * h) * 4);
+#pragma unroll
+    for (int v = 0; v < QV; ++v) A[slot][v] = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 32 * v, 0, 0);
+  };
+
+  // Each lane list filters with its own T-th best only: the launch has
+  // thousands of segments per query, too many to share a bound (the
+  // query's bound words would be one hot address).
+  uint32_t K[T], I[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  float thr = score_of_key(0u);
+  auto step = [&](int slot, int i) {
+    floatx16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < QV; ++v) {
+      floatx4 av = __builtin_bit_cast(floatx4, A[slot][v]);
+      if (v >= vlim) av = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], qf[v][u], acc, 0, 0, 0);
+        if (L2) ss = __builtin_fmaf(av[u], av[u], ss);
+      }
+    }
+    float sc[16];
+    if (L2) {
+      // row col's squared norm (the pair's sums), then row 8 j + 4 h + u's
+      // at score slot 4 j + u, read from lane 8 j + 4 h + u as a scalar
+      const float nrm = ss + __shfl_xor(ss, 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float n0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nrm), 8 * j + u));
+          const float n1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nrm), 8 * j + 4 + u));
+          sc[4 * j + u] = __builtin_fmaf(2.0f, acc[4 * j + u], -(h ? n1 : n0));
+        }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = acc[e];
+    }
+    // the slot is consumed: refill it with the tile two ahead (out of range
+    // past the end: zeros)
+    issue(slot, i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    const int tw = wave + 4 * i;
+    const int lim = nrows - tw * 32;
+    const uint32_t id0 = (uint32_t)(r0 + tw * 32);
+    if (lim >= 32)
+      select_block<T, true>(K, I, thr, sc, h, id0, 32);
+    else
+      select_block<T, false>(K, I, thr, sc, h, id0, lim);
+  };
+
+  // both steps run in every iteration (with an odd count the last is past
+  // the split: zero rows, nothing real), and the prologue issues slot 0
+  // before slot 1, so that every path into the loop head has the same loads
+  // outstanding and the waits stay partial
+  issue(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int i = 0; i < mine; i += 2) {
+    step(0, i);
+    step(1, i + 1);
+  }
+
+  if (qvalid) {
+    uint64_t* dst = a.part + ((int64_t)q * (8 * a.nsplit) + 8 * split + 2 * wave + h) * T;
 #pragma unroll
     for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
   }
@@ -1061,6 +1192,45 @@ hipError_t launch_transform(const PrepArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(rows_transform_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
                      0, s, a);
   return hipGetLastError();
+}
+
+template <int DH, int T>
+hipError_t stream_inst(const FusedArgs& a, hipStream_t s) {
+  if (a.metric == kL2)
+    hipLaunchKernelGGL((stream_kernel<DH, T, true>), dim3(a.nsplit), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((stream_kernel<DH, T, false>), dim3(a.nsplit), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int DH>
+hipError_t stream_t(const FusedArgs& a, hipStream_t s) {
+  switch (a.T) {
+    case 4: return stream_inst<DH, 4>(a, s);
+    case 8: return stream_inst<DH, 8>(a, s);
+    case 10: return stream_inst<DH, 10>(a, s);
+    case 16: return stream_inst<DH, 16>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+bool stream_supported(int ld, int T, int64_t nq) {
+  const int dh = dh_for(ld, false);
+  return nq <= 32 && t_ok(T) && dh != 0 && dh <= 64;
+}
+
+// one workgroup of four wavefronts per SIMD set: 256 registers a lane
+// (DH <= 32), 512 with the accumulation registers (DH = 64)
+int stream_blocks_per_cu(int ld) { return dh_for(ld, false) >= 64 ? 1 : 2; }
+
+hipError_t launch_stream(const FusedArgs& a, hipStream_t s) {
+  if (!stream_supported(a.ld, a.T, a.nq)) return hipErrorInvalidValue;
+  switch (dh_for(a.ld, false)) {
+    case 16: return stream_t<16>(a, s);
+    case 32: return stream_t<32>(a, s);
+    case 64: return stream_t<64>(a, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s) {

@@ -85,6 +85,15 @@ bool fused_supported(int ld, int T, bool f16);
 // resident workgroups per CU of that instance (HIP occupancy query)
 int fused_blocks_per_cu(int ld, int T, bool f16);
 
+// Small batches (fp32, nq <= 32, ld <= 128): grid nsplit, four independent
+// wavefronts per workgroup streaming their own 32-row tiles of the split
+// (rows_per_split a multiple of 128 keeps every tile whole), eight segments
+// per split (part [nq][8 nsplit][T], segment 8 split + 2 w + h).  L2 sums
+// the row norms itself (bnorm unused); no shared bound (gkey, mslots unused).
+hipError_t launch_stream(const FusedArgs& a, hipStream_t s);
+bool stream_supported(int ld, int T, int64_t nq);
+int stream_blocks_per_cu(int ld);
+
 // Deep rows (fp32, ld > kMaxFusedDimF32, ld a multiple of 32): the same
 // arguments, segments and output as the fused kernels, with kDeepRows rows
 // per tile and a K loop over 32-dim chunks staged in LDS.

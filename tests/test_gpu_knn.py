@@ -380,3 +380,58 @@ def test_c3_subset(engine, oracle):
         assert np.abs(exact - dist).max() < 1e-4
         np.testing.assert_allclose(dist, g["score_" + key], atol=1e-4)
         assert (ids == g["ids_" + key]).mean() > 0.95
+
+
+# ---- small batches (<= 32 queries, fp32, d <= 128, k <= 16: the streamed scan) ---------
+
+@pytest.mark.parametrize("nq", [1, 7, 32])
+@pytest.mark.parametrize("d", [4, 20, 32, 48, 64, 100, 128])
+@pytest.mark.parametrize("k", [1, 4, 10, 16])
+def test_small_batch_integer_bit_exact(engine, oracle, nq, d, k):
+    # n leaves a partial tile in the last split; d below 2 x the half width
+    # exercises the masked dims (values there belong to the next row)
+    rng = np.random.default_rng(nq * 1000 + d * 10 + k)
+    base = rng.integers(0, 6, (70_001, d)).astype(np.float32)
+    q = rng.integers(0, 6, (nq, d)).astype(np.float32)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(base, q, k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
+
+
+@pytest.mark.parametrize("nq", [1, 32])
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_small_batch_float(engine, oracle, nq, metric):
+    base, q = rows(300_000, 128, 31), rows(nq, 128, 32)
+    ids, dist = engine.brute_force_knn(base, q, 10, metric)
+    check_float(oracle, ids, dist, base, q, 10, metric)
+
+
+@pytest.mark.parametrize("n", [1, 31, 127, 128, 129, 5_000])
+def test_small_batch_small_n(engine, oracle, n):
+    rng = np.random.default_rng(n)
+    base = rng.integers(0, 5, (n, 24)).astype(np.float32)
+    q = rng.integers(0, 5, (3, 24)).astype(np.float32)
+    ids, dist = engine.brute_force_knn(base, q, 10, "l2")
+    oid, odist = oracle.knn(base, q, 10, "l2")
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+
+
+def test_small_batch_next_row_values_stay_out():
+    # d = 20 reads 32-dim halves: dims 20-31 of a row's fetch are the next
+    # row's first values (here inf); they must not reach any score
+    x = np.zeros((4096, 20), np.float32)
+    x[:, 0] = np.arange(4096, dtype=np.float32)
+    x[1::2, 0] = np.inf
+    import mlxvs_amd
+    ids, dist = mlxvs_amd.brute_force_knn(x, np.zeros((1, 20), np.float32), 3, "l2")
+    assert ids.tolist() == [[0, 2, 4]]
+    assert dist.tolist() == [[0.0, 4.0, 16.0]]
+
+
+def test_small_batch_ties_keep_lowest_ids(engine):
+    # every row equal: the k lowest ids, from segments of many splits
+    x = np.ones((50_000, 16), np.float32)
+    ids, dist = engine.brute_force_knn(x, np.ones((2, 16), np.float32), 16, "l2")
+    assert (ids == np.arange(16)).all() and (dist == 0).all()
