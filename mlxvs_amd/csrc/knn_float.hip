@@ -353,7 +353,6 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       }
       __builtin_amdgcn_sched_barrier(0);
       if (MODE != 2 && share) thr = fmaxf(thr, score_of_key(seen.bound()));
-      const bool full = t + 1 < ntiles || nrows % TR == 0;
       bool inserted = false;
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
@@ -385,10 +384,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
               if (m < lim) dst[m] = sc[i];
             }
           }
-        } else if (full) {
-          inserted |= select_block<T, true>(K, I, thr, sc, h, id0, 32);
         } else {
-          inserted |= select_block<T, false>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
+          inserted |= select_block<T>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
         }
       }
       if (MODE != 2 && share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
@@ -588,7 +585,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
             }
           }
-          inserted |= select_block<T, false>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+          inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
         }
         if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
           __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
@@ -721,10 +718,7 @@ __global__ __launch_bounds__(256, DH >= 64 ? 1 : 2) void stream_kernel(FusedArgs
     const int tw = wave + 4 * i;
     const int lim = nrows - tw * 32;
     const uint32_t id0 = (uint32_t)(r0 + tw * 32);
-    if (lim >= 32)
-      select_block<T, true>(K, I, thr, sc, h, id0, 32);
-    else
-      select_block<T, false>(K, I, thr, sc, h, id0, lim);
+    select_block<T>(K, I, thr, sc, h, id0, lim);
   };
 
   // both steps run in every iteration (with an odd count the last is past

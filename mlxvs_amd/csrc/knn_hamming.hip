@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
               for (int w = 0; w < 4; ++w)
                 sc[4 * jj + w] = __builtin_fmaf(2.0f, (float)acc[r][4 * jj + w], -nbv[w]);
             }
-            inserted |= select_block<T, false>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+            inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
           }
           if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
             pend = __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,

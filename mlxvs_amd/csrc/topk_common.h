@@ -103,32 +103,42 @@ __device__ __forceinline__ float pick16(const float (&sc)[16], int i) {
   return b3 ? d1 : d0;
 }
 
+// Bit i set when row 8 (i / 4) + 4 h + i % 4 of a 32-row block is one of
+// its first lim rows.
+__device__ __forceinline__ uint32_t real_rows(int h, int lim) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = min(4, max(0, lim - 8 * j - 4 * h));
+    m |= ((1u << c) - 1u) << (4 * j);
+  }
+  return m;
+}
+
 // Inserts the scores of one 32-row block (rows id0 + 8 (i / 4) + 4 h + i % 4,
-// the first `lim` of the block real; FULL: all 32) that pass the lane's
-// threshold.  The common case -- nothing passes -- costs a max tree and one
-// compare.  Otherwise every lane drains its own bitmask of passing
-// positions, lowest first (so ids reach the list in increasing order); the
-// loop runs as often as the busiest lane needs, and a lane with nothing left
-// inserts the empty key.  A lane's score at its position comes out of a
-// select tree on the position bits (no dynamic register index).  Returns
-// whether the lane kept any.
-template <int T, bool FULL>
+// the first `lim` of the block real) that pass the lane's threshold.  The
+// common case -- nothing passes -- costs a max tree and one compare; the
+// rows past `lim` (zero rows of a partial tile: finite scores) take part in
+// the max tree and are masked out only when something passes.  Otherwise
+// every lane drains its own bitmask of passing positions, lowest first (so
+// ids reach the list in increasing order); the loop runs as often as the
+// busiest lane needs, and a lane with nothing left inserts the empty key.  A
+// lane's score at its position comes out of a select tree on the position
+// bits (no dynamic register index).  Returns whether the lane kept any.
+template <int T>
 __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                              const float (&sc)[16], int h, uint32_t id0,
                                              int lim) {
-  auto real = [&](int i) { return FULL || 8 * (i >> 2) + 4 * h + (i & 3) < lim; };
-  float v[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = real(i) ? sc[i] : -INFINITY;
-  const float m0 = fmaxf(fmaxf(v[0], v[1]), v[2]), m1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
-  const float m2 = fmaxf(fmaxf(v[6], v[7]), v[8]), m3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
-  const float m4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
-  const float mx = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), v[15]));
+  const float m0 = fmaxf(fmaxf(sc[0], sc[1]), sc[2]), m1 = fmaxf(fmaxf(sc[3], sc[4]), sc[5]);
+  const float m2 = fmaxf(fmaxf(sc[6], sc[7]), sc[8]), m3 = fmaxf(fmaxf(sc[9], sc[10]), sc[11]);
+  const float m4 = fmaxf(fmaxf(sc[12], sc[13]), sc[14]);
+  const float mx = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), sc[15]));
   // NaN thr (a list with room) passes everything
   if (__builtin_amdgcn_ballot_w64(!(mx < thr)) == 0) return false;
   uint32_t pm = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) pm |= (real(i) && !(sc[i] < thr)) ? (1u << i) : 0u;
+  for (int i = 0; i < 16; ++i) pm |= !(sc[i] < thr) ? (1u << i) : 0u;
+  if (lim < 32) pm &= real_rows(h, lim);
   const bool any = pm != 0;
   while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
     const int i = pm ? __builtin_ctz(pm) : 0;
