@@ -274,7 +274,8 @@ def main() -> int:
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
-        t = json.loads(tfile.read_text()).get(args.workload, {})
+        key = args.workload if args.nq is None else f"{args.workload}_nq{args.nq}"
+        t = json.loads(tfile.read_text()).get(key, {})
         traffic = t.get("hbm_bytes_per_launch")
     roof["traffic"] = traffic
 
