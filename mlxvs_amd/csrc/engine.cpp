@@ -393,17 +393,31 @@ int round_up(int x, int m) { return (x + m - 1) / m * m; }
 // Split count multiplier allowed by the two-level merge (k <= T).
 constexpr int kMergeGroups = 16;
 
-// Bound slots (mslots) a launch shares per query, 0 for none.  Every
-// segment list of a query reads the query's bound words once a tile and
-// raises them as it improves, so the words are one hot address per query:
-// with many segments per query (small batches: hundreds of splits) those
+// Shared bound of a launch (see SharedBound): m slots in use (0: none) and
+// the list entry j - 1 each list publishes, m j >= k.  With lists lists per
+// query: m about k / 3 (so j is 3 to 5: small j bounds tighter, while the
+// minimum over more slots bounds looser), at most the slots there are and
+// one list per slot.  Every list reads the query's bound words once a tile
+// and raises them as it improves, so they are one hot address per query:
+// with many lists per query (small batches: hundreds of splits) those
 // accesses cost more than the pruning saves (measured on c2 rows: 1 query,
-// 2,048 segments: 0.25 ms with the bound, 0.13 ms without; 10,000 queries,
-// 16 segments: 5% faster with it).
+// 2,048 lists: 0.25 ms with the bound, 0.13 ms without; 10,000 queries, 16
+// lists: 5% faster with it).
 constexpr int kMaxSharedSegments = 512;
-int shared_bound_slots(int k, int T, int slots, int nseg) {
-  const int m = (k + T - 1) / T;
-  return m <= slots && nseg <= kMaxSharedSegments ? m : 0;
+struct BoundPlan {
+  int m = 0;
+  int pubj = 0;
+};
+BoundPlan shared_bound(int k, int T, int slots, int lists) {
+  BoundPlan b;
+  if (lists > kMaxSharedSegments) return b;
+  const int cap = std::min(slots, lists);
+  int m = std::min(cap, std::max(1, (k + 2) / 3));
+  if ((k + m - 1) / m > T) m = (k + T - 1) / T;
+  if (m > cap) return b;
+  b.m = m;
+  b.pubj = (k + m - 1) / m - 1;
+  return b;
 }
 
 void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* ids,
@@ -537,14 +551,14 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
-  const int mslots = shared_bound_slots(k, T, slots, nseg);
+  const BoundPlan bp = shared_bound(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
-  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
+  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });
   // XCD order: the register-resident kernels share only the row tiles
   // (split-major); the deep kernel streams query chunks too (split-minor)
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
-                     plan.rows_per_split, plan.nsplit, T, k, part, gkey, mslots, (int)qblocks,
-                     plan.xcd ? (use_deep ? 2 : 1) : 0};
+                     plan.rows_per_split, plan.nsplit, T, k, part, gkey, bp.m, bp.pubj,
+                     (int)qblocks, plan.xcd ? (use_deep ? 2 : 1) : 0};
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });
   else if (use_stream)
@@ -642,11 +656,12 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   const int nseg = 2 * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
-  const int mslots = shared_bound_slots(k, T, slots, nseg);
+  const BoundPlan bp = shared_bound(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
-  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, mslots, s); });
+  launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });
   kern::FusedArgs fa{bw, qw, bpop, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,
-                     plan.nsplit, T, k, part, gkey, mslots, (int)qblocks, plan.xcd ? 1 : 0};
+                     plan.nsplit, T, k, part, gkey, bp.m, bp.pubj, (int)qblocks,
+                     plan.xcd ? 1 : 0};
   launch(s, "hamming_mfma", [&] { return kern::launch_deep_bits(fa, s); });
   int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
   kern::MergeArgs ma{part, nseg, T, k, (int)nq, kern::kL2, qpop, 0, ids, dists, flags};
@@ -829,10 +844,13 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     // every (query, probe) pair is in one item, so every segment is written
     uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
     const int slots_n = kern::bound_slots_for(T);
+    // one slot: the items are short (a list's rows), and a tile's read of
+    // more slots costs more than the tighter bound saves
+    const BoundPlan bp = shared_bound(k, T, 1, nseg);
     uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots_n);
-    launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots_n, 1, s); });
-    kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, 1, 0, 0,
-                       ditems, dpairs, offsets, dslots, P, it.n, nullptr, width, 0};
+    launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots_n, bp.m, s); });
+    kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, bp.m, bp.pubj,
+                       0, 0, ditems, dpairs, offsets, dslots, P, it.n, nullptr, width, 0};
     launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
     kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
@@ -855,7 +873,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
       int* dpairs = to_device(ar, s, it.pairs);
       launch(s, "prep", [&] { return kern::launch_fill_f32(S, cnt * width, -INFINITY, s); });
       kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, 4, k, nullptr, nullptr, 0, 0,
-                         0, ditems, dpairs, offsets, dslots, P, it.n, S, width, (int)q0};
+                         0, 0, ditems, dpairs, offsets, dslots, P, it.n, S, width, (int)q0};
       launch(s, "ivf_scan", [&] {
         return kern::fused_supported(ld, 4, false) ? kern::launch_ivf_scores(fa, s)
                                                    : kern::launch_ivf_scores_any(fa, s);

@@ -315,12 +315,16 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  // the shared bound, read every 4th tile (a stale bound is still a bound,
+  // and the reads of a query's bound words are what sharing costs)
+  SharedBound<S> seen;
+  seen.clear();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    // the shared bound is read before the tile prefetch, so that waiting for
-    // it (in the epilogue) does not wait for the prefetch
-    SharedBound<S> seen{};
-    if constexpr (MODE != 2) seen.load(gk);
+    // read before the tile prefetch, so that waiting for it (in the
+    // epilogue) does not wait for the prefetch
+    if constexpr (MODE != 2)
+      if (share && (t & 3) == 0) seen.load(gk, a.mslots);
     // unconditional (past the last tile the offsets are out of range and
     // read zero), so the wait counts after the shared key stay static
     issue_loads();
@@ -388,8 +392,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
           inserted |= select_block<T>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
         }
       }
-      if (MODE != 2 && share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
-        __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (MODE != 2 && share && qvalid && inserted) {
+        const uint32_t kp = list_key(K, a.pubj);
+        if (kp > seen.slot(myslot))
+          __hip_atomic_fetch_max(gk + myslot, kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     store_tile(buf ^ 1);
@@ -541,8 +548,10 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   int c = 0, t = 0;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
+    // the bound is used at the tile's last chunk: read it in that step only
     SharedBound<S> seen;
-    seen.load(gk);
+    seen.clear();
+    if (share && c + 1 == NC) seen.load(gk, a.mslots);
     // the fetched tile's parity, read before store_chunk advances pc
     const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
     issue_loads();
@@ -587,9 +596,11 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
           }
           inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
         }
-        if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
-          __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (share && qvalid && inserted) {
+          const uint32_t kp = list_key(K, a.pubj);
+          if (kp > seen.slot(myslot))
+            __hip_atomic_fetch_max(gk + myslot, kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
 #pragma unroll
       for (int r = 0; r < kDeepRB; ++r)

@@ -235,9 +235,10 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   int par = 0;  // LDS buffer of the current chunk
   for (int t = 0; t < ntiles; ++t) {
     SharedBound<S> seen;
+    seen.clear();
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-      if (c == 0) seen.load(gk);
+      if (c == 0 && share) seen.load(gk, a.mslots);
       const int buf = (NCT % 2 == 0) ? (c & 1) : par;
       if (wave_on) {
         const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 16 * h];
@@ -284,9 +285,12 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
             }
             inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
           }
-          if (share && qvalid && inserted && K[T - 1] > seen.slot(myslot))
-            pend = __hip_atomic_fetch_max(gk + myslot, K[T - 1], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
+          if (share && qvalid && inserted) {
+            const uint32_t kp = list_key(K, a.pubj);
+            if (kp > seen.slot(myslot))
+              pend = __hip_atomic_fetch_max(gk + myslot, kp, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r)

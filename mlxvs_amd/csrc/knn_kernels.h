@@ -61,7 +61,8 @@ struct FusedArgs {
   int k;                 // neighbours wanted
   uint64_t* part;        // [nq][2*nsplit][T]
   uint32_t* gkey;        // [nq][bound_slots_for(T)] shared bounds (launch_bounds_init)
-  int mslots;            // ceil(k / T) when <= bound_slots_for(T), else 0 (no sharing)
+  int mslots;            // slots in use (m), 0: no sharing
+  int pubj;              // a list publishes its key K[pubj]; m (pubj + 1) >= k
   int nqb;               // query blocks, ceil(nq / 128)
   int xcd_major;         // workgroup order, tile_of_workgroup mode (1, 2: nsplit % 8 == 0)
   // IVF-Flat list scan (launch_ivf_select / launch_ivf_scores): one workgroup

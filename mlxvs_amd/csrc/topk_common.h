@@ -188,53 +188,61 @@ __device__ __forceinline__ void tile_of_workgroup(int id, int nsplit, int nqb, i
 }
 
 // Per-query shared lower bounds on the k-th best score, kept in S slots of
-// gkey[q S .. q S + S).  Segment g publishes its list's T-th best key into
-// slot g % m (m = ceil(k / T) <= S; slots m .. S - 1 hold 0xffffffff and never
-// win a min).  Every slot holds the T-th best key of one segment and the m
-// slots are fed by disjoint classes of segments, which cover disjoint rows,
-// so at least m T >= k candidates score at least the smallest slot: the
-// query's k-th best does too, and a candidate below it is never needed.  Keys
-// only grow, so a stale read is merely a weaker bound.  S = 1 serves k <= T.
+// gkey[q S .. q S + S).  Of the query's segment lists (2 per split, or per
+// probe), list g publishes its j-th best key (j = pubj + 1) into slot g % m,
+// raising it with a relaxed atomic max; slots m .. S - 1 hold 0xffffffff and
+// never win a min.  The m slots are fed by disjoint classes of lists, which
+// cover disjoint rows, and every slot holds the j-th best key of one list, so
+// at least m j >= k candidates score at least the smallest slot: the query's
+// k-th best does too, and a candidate below it is never needed.  Keys only
+// grow, so a stale read is merely a weaker bound.  Several slots with a
+// small j bound tighter than few slots with a large j: in a simulation of
+// the streams, 32 lists of 16 and k = 65 let 66 candidates per list in with
+// 8 slots of 9th-best keys, 84 with 5 slots of 16th-best keys; 16 lists of
+// 10 and k = 10: 31 with 4 slots of 3rd-best keys, 51 with one 10th-best.
+// Reading the slots is the cost (each read is of a word every list of the
+// query shares), so the kernels read only the m slots in use, and only
+// every few tiles.
 template <int T>
-constexpr int bound_slots() { return T == 16 ? 8 : 1; }
+constexpr int bound_slots() { return 8; }
 
 template <int S>
-struct SharedBound;
-
-template <>
-struct SharedBound<1> {
-  uint32_t v;
-  __device__ __forceinline__ void load(const uint32_t* p) {
-    v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __device__ __forceinline__ uint32_t bound() const { return v; }
-  __device__ __forceinline__ uint32_t slot(int) const { return v; }
-};
-
-template <>
-struct SharedBound<8> {
-  uint64_t w[4];
-  __device__ __forceinline__ void load(const uint32_t* p) {
+struct SharedBound {
+  static_assert(S % 2 == 0, "slots are read in pairs");
+  uint64_t w[S / 2];
+  // the words of the first m slots (the rest keep their initial all-ones)
+  __device__ __forceinline__ void load(const uint32_t* p, int m) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = __hip_atomic_load((const uint64_t*)p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < S / 2; ++i)
+      if (2 * i < m)
+        w[i] = __hip_atomic_load((const uint64_t*)p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int i = 0; i < S / 2; ++i) w[i] = ~0ull;
   }
   __device__ __forceinline__ uint32_t bound() const {
     uint32_t m = 0xffffffffu;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m = min(m, (uint32_t)w[i]);
-      m = min(m, (uint32_t)(w[i] >> 32));
-    }
+    for (int i = 0; i < S / 2; ++i) m = min(m, min((uint32_t)w[i], (uint32_t)(w[i] >> 32)));
     return m;
   }
   __device__ __forceinline__ uint32_t slot(int j) const {
     uint32_t r = 0;  // a select chain: a dynamic index would go through scratch
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r = j == i ? (uint32_t)(w[i >> 1] >> (32 * (i & 1))) : r;
+    for (int i = 0; i < S; ++i) r = j == i ? (uint32_t)(w[i >> 1] >> (32 * (i & 1))) : r;
     return r;
   }
 };
+
+// K[j] for a run-time j (a select chain, as above).
+template <int T>
+__device__ __forceinline__ uint32_t list_key(const uint32_t (&K)[T], int j) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < T; ++i) r = j == i ? K[i] : r;
+  return r;
+}
 
 // In-LDS bitonic sort of P (a power of two) values, descending by `ord`.
 // All threads of the workgroup call it; it ends with a barrier.
