@@ -74,20 +74,29 @@ __device__ __forceinline__ uint32_t key_nz(float v) {
 // it beats (an equal key keeps the entry: it has the lower id), and from
 // there on every entry shifts down one slot: the entry carried out of a slot
 // is older, so it has a lower id than any equal-key entry below it and must
-// stay in front of it.  One 32-bit compare, one OR and four selects per slot.
+// stay in front of it.  The keys are sorted descending, so g_j = kc > K[j]
+// is false before that slot and true from it on, and
+//   K'[j] = median(K[j-1], kc, K[j])      (K[-1] = all ones)
+//   I'[j] = g_j ? (g_{j-1} ? I[j-1] : ic) : I[j]
+// One median, one compare and two selects per slot.
+__device__ __forceinline__ uint32_t median3(uint32_t a, uint32_t b, uint32_t c) {
+  return max(min(a, b), min(max(a, b), c));
+}
+
 template <int T>
 __device__ __forceinline__ void stream_insert(uint32_t (&K)[T], uint32_t (&I)[T], uint32_t kc,
                                               uint32_t ic) {
-  bool moved = false;
+  uint32_t kp = 0xffffffffu, ip = 0;
+  bool gp = false;
 #pragma unroll
   for (int j = 0; j < T; ++j) {
-    const bool b = moved || kc > K[j];
-    const uint32_t tk = K[j], ti = I[j];
-    K[j] = b ? kc : tk;
-    I[j] = b ? ic : ti;
-    kc = b ? tk : kc;
-    ic = b ? ti : ic;
-    moved = b;
+    const uint32_t kj = K[j], ij = I[j];
+    const bool g = kc > kj;
+    K[j] = median3(kp, kc, kj);
+    I[j] = g ? (gp ? ip : ic) : ij;
+    kp = kj;
+    ip = ij;
+    gp = g;
   }
 }
 
