@@ -15,8 +15,10 @@ The same JSON line carries:
   roofline      the dominant kernel's achieved MFMA rate, from HIP events
                 recorded around each of its launches inside the timed steps
                 (2 nq n d flops per launch over its mean duration; for Hamming
-                2 nq n bits int8 ops), against MI355X's dense peak of that
-                type (FP32 157.3, FP16 2516.6 TFLOP/s, INT8 5033.2 TOP/s);
+                2 nq n bits ops on the FP4 MFMA), against MI355X's dense peak
+                of that type (FP32 157.3, FP16 2516.6, FP4 10066.4 TFLOP/s),
+                or, below the ridge point (small batches), the rows' bytes per
+                launch against HBM's 8 TB/s;
                 traffic = HBM bytes per launch from the committed rocprofv3
                 counter summary when present;
   cpu_baseline  the CPU restatement of the reference path (oracle/, a port:
@@ -49,7 +51,7 @@ METRIC = ("queries/s, exact kNN k=10 on 1M×128 fp32 (10k queries); "
           "% of MFMA/HBM roofline")
 PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense FP32 matrix
 PEAK_FP16_MFMA = 2516.6  # TFLOP/s, MI355X dense FP16 matrix
-PEAK_INT8_MFMA = 5033.2  # TOP/s, MI355X dense INT8 matrix
+PEAK_FP4_MFMA = 10066.4  # TFLOP/s, MI355X dense FP4 (e2m1) matrix
 PEAK_HBM = 8000.0        # GB/s
 VALU_LANE_OPS = 256 * 64 * 2.4e9  # non-packed VALU lane-ops per second
 
@@ -244,10 +246,15 @@ def main() -> int:
         roof = {"bound": "mfma", "achieved": round(flops / per / 1e12, 2),
                 "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s", "candidates_per_query": round(cands / nq, 1)}
     elif w["kind"] == "hamming" and kname == "hamming_mfma":
-        # the int8 MFMA route: 2 ops (multiply, add) per code bit and pair
+        # the FP4 MFMA route: 2 ops (multiply, add) per code bit and pair
         ops = 2.0 * nq * n * 8 * d / (cnt / args.steps)  # per launch
-        roof = {"bound": "mfma", "achieved": round(ops / per / 1e12, 2),
-                "peak": PEAK_INT8_MFMA, "unit": "TOP/s"}
+        row_bytes = float(n) * d / (cnt / args.steps)
+        if ops / row_bytes < PEAK_FP4_MFMA * 1e12 / (PEAK_HBM * 1e9):
+            roof = {"bound": "hbm", "achieved": round(row_bytes / per / 1e9, 1),
+                    "peak": PEAK_HBM, "unit": "GB/s"}
+        else:
+            roof = {"bound": "mfma", "achieved": round(ops / per / 1e12, 2),
+                    "peak": PEAK_FP4_MFMA, "unit": "TFLOP/s"}
     elif w["kind"] == "hamming":
         # the popcount route: XOR + popcount-accumulate per 32-bit word
         words = (d + 3) // 4

@@ -112,16 +112,22 @@ __global__ void pack_kernel(PackArgs a) {
   a.words[e] = v;
 }
 
-// ---- int8 MFMA route: packed codes unpacked to {0, 1} bytes in LDS ---------------
+// ---- MFMA route: packed codes unpacked to {0, 1} values in LDS ------------------
 //
 // For {0, 1} vectors the squared L2 distance is the Hamming distance and
 // sum b_i^2 is popcount(b), so the k-NN is the L2 one: s = 2 q.b - pop(b)
-// selected largest first, distance pop(q) - s.  The dot products run on
-// v_mfma_i32_32x32x32_i8 (exact int32 sums).  Workgroup and tile as the deep
-// fp32 kernel: 128 queries (wavefront w: queries 32 w ..), 128-row tiles,
-// four 32 x 32 accumulators per wavefront, a K loop over 128-bit chunks of
-// the codes.  The codes travel packed (16 bytes per row and chunk) and each
-// chunk is unpacked into the LDS buffer that the MFMAs read:
+// selected largest first, distance pop(q) - s.  The dot products run on the
+// FP4 MFMA, v_mfma_scale_f32_32x32x64_f8f6f4 with e2m1 operands (a code bit
+// becomes the value 0 or 1.0, scale 1.0; products of 1.0s summed in fp32 are
+// exact up to 2^24): per 128-bit chunk of the codes a row is 128 nibbles,
+// two MFMA steps of 64 (lane half h supplies dwords 8 v + 4 h .. + 3 of step
+// v; any split of K works as long as rows and queries use the same).  An
+// earlier form ran v_mfma_i32_32x32x32_i8 on {0, 1} bytes: twice the
+// unpacking and twice the MFMA passes (C4 12.9 ms there, 9.2 ms here).
+// Workgroup and tile as the deep fp32 kernel: 128 queries (wavefront w:
+// queries 32 w ..), 128-row tiles, four 32 x 32 accumulators per wavefront,
+// a K loop over the chunks.  The codes travel packed (16 bytes per row and
+// chunk) and each chunk is unpacked into the LDS buffer that the MFMAs read:
 //  * threads 0-127 own a base row each; they hold its NCT packed chunks in
 //    registers and refetch chunk j for the next tile as soon as chunk j of
 //    the current tile is unpacked, so every fetch has a whole tile to land;
@@ -133,23 +139,24 @@ __global__ void pack_kernel(PackArgs a) {
 // refetches keep counting instead of draining.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBitsRows = kDeepRows;
-constexpr int kBitsStride = 36;  // dwords per unpacked LDS row: 128 bytes + 16 pad
+// dwords per unpacked LDS row and chunk: 64 bytes of nibbles + 16 pad, which
+// puts the 16 rows a quarter-wavefront reads (16-byte reads) on distinct banks
+constexpr int kBitsStride = 20;
 
-// 128 bits -> 128 {0, 1} bytes: dword 8 w + m holds bits 8 j + m of word w
-// in its bytes j.  Rows and queries use the same order, so the dot products
-// are those of the codes.
+// 128 bits -> 128 e2m1 nibbles of value 0 or 1.0 (code 0x2): dword 4 w + m
+// holds bits 4 j + m of word w in its nibbles j.  Rows and queries use the
+// same order, so the dot products are those of the codes.
 __device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t v = x[w];
-    *(u32x4*)(dst + 8 * w) = u32x4{v & 0x01010101u, (v >> 1) & 0x01010101u,
-                                   (v >> 2) & 0x01010101u, (v >> 3) & 0x01010101u};
-    *(u32x4*)(dst + 8 * w + 4) = u32x4{(v >> 4) & 0x01010101u, (v >> 5) & 0x01010101u,
-                                       (v >> 6) & 0x01010101u, (v >> 7) & 0x01010101u};
+    *(u32x4*)(dst + 4 * w) = u32x4{(v << 1) & 0x22222222u, v & 0x22222222u,
+                                   (v >> 1) & 0x22222222u, (v >> 2) & 0x22222222u};
   }
 }
 
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   __syncthreads();
 
-  i32x16 acc[4];
+  floatx16 acc[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -241,17 +248,21 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       if (c == 0 && share) seen.load(gk, a.mslots);
       const int buf = (NCT % 2 == 0) ? (c & 1) : par;
       if (wave_on) {
-        const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 16 * h];
-        const uint32_t* arow = &tA[buf][col * kBitsStride + 16 * h];
+        const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 4 * h];
+        const uint32_t* arow = &tA[buf][col * kBitsStride + 4 * h];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const i32x4 bq = *(const i32x4*)(qrow + 4 * v);
-          i32x4 av[4];
+        for (int v = 0; v < 2; ++v) {
+          const i32x4 bq4 = *(const i32x4*)(qrow + 8 * v);
+          const i32x8 bq = {bq4[0], bq4[1], bq4[2], bq4[3], 0, 0, 0, 0};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) av[r] = *(const i32x4*)(arow + r * 32 * kBitsStride + 4 * v);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[r], bq, acc[r], 0, 0, 0);
+          for (int r = 0; r < 4; ++r) {
+            const i32x4 a4 = *(const i32x4*)(arow + r * 32 * kBitsStride + 8 * v);
+            const i32x8 av = {a4[0], a4[1], a4[2], a4[3], 0, 0, 0, 0};
+            // formats 4, 4: e2m1 A and B (only the first 4 registers are
+            // read); scales 0x7f: 2^0
+            acc[r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                av, bq, acc[r], 4, 4, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+          }
         }
       }
       // the next chunk (j of this tile, or chunk 0 of the next) into the
@@ -312,8 +323,8 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 template <int NCT, int T>
 int bits_occupancy() {
   int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, bits_kernel<NCT, T>, 256, 0) !=
-      hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, bits_kernel<NCT, T>, 256,
+                                                   0) != hipSuccess)
     return 1;
   return blocks;
 }

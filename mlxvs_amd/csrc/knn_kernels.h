@@ -105,9 +105,10 @@ int deep_blocks_per_cu(int T);
 // The same arguments, segments and output over bit codes (knn_hamming.hip):
 // base / queries packed little-endian words, ld = packed row length in bytes
 // (bits_row_bytes: 16, 32, 64, 128 or 256, zero padded), bnorm the rows'
-// popcounts as floats, metric kL2.  The kernel unpacks the bits to {0, 1}
-// bytes in LDS; for {0, 1} vectors the squared L2 distance is the Hamming
-// distance, and every product and sum is exact on the int8 MFMA.
+// popcounts as floats, metric kL2.  The kernel unpacks the bits to e2m1
+// values 0 / 1.0 in LDS; for {0, 1} vectors the squared L2 distance is the
+// Hamming distance, and every product and sum is exact on the FP4 MFMA
+// (fp32 accumulation of integers below 2^24).
 hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s);
 bool deep_bits_supported(int ld, int T);
 int deep_bits_blocks_per_cu(int T);
