@@ -158,12 +158,12 @@ constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
 // 32-row MFMA blocks per streamed tile: two where the registers allow, which
 // halves the barriers and per-tile overhead per row.  One where the query
-// fragments take 64 or more VGPRs and the list is 16 long, or 128 (fp32,
-// 256 dims): the second accumulator and prefetch would spill.
+// fragments take 128 VGPRs (fp32, 256 dims): the second accumulator and
+// prefetch would spill.
 template <bool F16, int DH, int T>
 constexpr int fused_rb() {
   constexpr int qregs = DH * (F16 ? 2 : 4) / 4;
-  return (qregs >= 128 || (qregs >= 64 && T >= 16)) ? 1 : 2;
+  return qregs >= 128 ? 1 : 2;
 }
 
 
