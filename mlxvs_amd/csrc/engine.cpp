@@ -272,14 +272,13 @@ struct SplitPlan {
 // (such queries are redone exhaustively).  !ok when the merge cannot hold
 // that many.
 SplitPlan plan_splits(int64_t n, int64_t nq_blocks, int k, int T, int lanes,
-                      int64_t align, int64_t slots, bool xcd = false, int cap_mult = 1) {
+                      int64_t align, int64_t slots, bool xcd = false, int max_seg = 0) {
   SplitPlan p;
   if (n <= 0) return p;
-  // the merge sorts at most kMaxMergeCandidates per query; with k <= T a
-  // first merge level (merge_group) lifts that cap_mult-fold
-  const int64_t cap = std::min<int64_t>(
-      (int64_t)cap_mult * (kern::kMaxMergeCandidates / ((int64_t)lanes * T)),
-      (n + align - 1) / align);
+  // the merge sorts at most kMaxMergeCandidates per query (one level), or
+  // max_seg segment lists in two levels (merge_lists)
+  if (max_seg <= 0) max_seg = kern::kMaxMergeCandidates / T;
+  const int64_t cap = std::min<int64_t>(max_seg / lanes, (n + align - 1) / align);
   const int64_t need = k > T ? (4 * (int64_t)k + lanes * T - 1) / (lanes * T) : 1;
   const int64_t lo = std::max<int64_t>(need, (slots + nq_blocks - 1) / nq_blocks);
   const int64_t hi = std::min<int64_t>(cap, 6 * lo);
@@ -390,8 +389,48 @@ void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
-// Split count multiplier allowed by the two-level merge (k <= T).
-constexpr int kMergeGroups = 16;
+// Two-level merge geometry for lists of T and k neighbours: each group of gs
+// lists keeps `keep` ranks (T when k <= T, else k), groups of about 1,024
+// candidates (small sorts, many workgroups) and at least `keep`, and the
+// final merge sorts ngroups * keep <= kMaxMergeCandidates ranks.
+struct MergeGeometry {
+  int keep, gs;
+};
+MergeGeometry merge_geometry(int k, int T) {
+  const int keep = k <= T ? T : k;
+  return {keep, std::max(1024 / T, (keep + T - 1) / T)};
+}
+// Segment lists per query the merge takes in two levels.
+int max_merge_segments(int k, int T) {
+  const MergeGeometry g = merge_geometry(k, T);
+  return kern::kMaxMergeCandidates / g.keep * g.gs;
+}
+
+// Merges the segment lists part [nq][nseg][T] into ids / dists; two levels
+// when one workgroup cannot sort them all.  flags (T < k) as merge_kernel.
+void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T, int k,
+                 int64_t nq, int metric, const float* qnorm, int dist_mode, int32_t* ids,
+                 float* dists, int* flags) {
+  const uint64_t* mpart = part;
+  int mseg = nseg, mT = T;
+  uint64_t* sentinel = nullptr;
+  if ((int64_t)nseg * T > kern::kMaxMergeCandidates) {
+    const MergeGeometry g = merge_geometry(k, T);
+    const int ngroups = (nseg + g.gs - 1) / g.gs;
+    if ((int64_t)ngroups * g.keep > kern::kMaxMergeCandidates)
+      throw std::runtime_error("mlxvs: merge plan exceeds the merge capacity");
+    uint64_t* part2 = ar.take<uint64_t>((size_t)nq * ngroups * g.keep);
+    if (flags) sentinel = ar.take<uint64_t>((size_t)nq * ngroups);
+    kern::MergeGroupArgs mg{part, nseg, T, (int)nq, g.gs, ngroups, g.keep, part2, sentinel};
+    launch(s, "merge", [&] { return kern::launch_merge_group(mg, s); });
+    mpart = part2;
+    mseg = ngroups;
+    mT = g.keep;
+  }
+  kern::MergeArgs ma{mpart, mseg, mT, k, (int)nq, metric, qnorm, dist_mode, ids, dists, flags,
+                     sentinel};
+  launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+}
 
 // Shared bound of a launch (see SharedBound): m slots in use (0: none) and
 // the list entry j - 1 each list publishes, m j >= k.  With lists lists per
@@ -495,8 +534,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   const bool use_deep = deep && kern::deep_supported(kld, T, false);
-  // at most 32 queries (fp32, k <= T): rows streamed straight into registers
-  const bool use_stream = !kf16 && !deep && k <= T && kern::stream_supported(kld, T, nq);
+  // at most 32 queries (fp32): rows streamed straight into registers
+  const bool use_stream = !kf16 && !deep && kern::stream_supported(kld, T, nq);
   // segment lists per split
   const int lanes = use_stream ? 8 : 2;
   // split alignment: whole tiles (deep: 128 rows; fused: 32 or 64; stream:
@@ -508,7 +547,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
                     : use_stream ? kern::stream_blocks_per_cu(kld)
                                  : kern::fused_blocks_per_cu(kld, T, kf16);
     plan = plan_splits(n, qblocks, k, T, lanes, tile_rows, device_slots(bpc), !use_stream,
-                       k <= T ? kMergeGroups : 1);
+                       max_merge_segments(k, T));
     // a split's rows and the tiles prefetched past them (stream: two per
     // wavefront) must stay inside one 32-bit buffer range
     const int64_t past = use_stream ? 3 * tile_rows : tile_rows;
@@ -569,26 +608,18 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     });
   int* flags = nullptr;
   if (T < k) flags = ar.take<int>((size_t)nq);
-  const uint64_t* mpart = part;
-  int mseg = nseg;
-  if ((int64_t)nseg * T > kern::kMaxMergeCandidates) {
-    // k <= T: the T best of each group of segment lists first (groups of
-    // about 1,024 candidates: small sorts, many workgroups)
-    const int gs = std::max(1, 1024 / T);
-    const int ngroups = (nseg + gs - 1) / gs;
-    uint64_t* part2 = ar.take<uint64_t>((size_t)nq * ngroups * T);
-    kern::MergeGroupArgs mg{part, nseg, T, (int)nq, gs, ngroups, part2};
-    launch(s, "merge", [&] { return kern::launch_merge_group(mg, s); });
-    mpart = part2;
-    mseg = ngroups;
-  }
-  kern::MergeArgs ma{mpart, mseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, flags};
-  launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+  merge_lists(ar, s, part, nseg, T, k, nq, metric, qnorm, 0, ids, dists, flags);
   if (T >= k) return;
 
   // k > T: queries whose lists may have dropped a member go exhaustive.
   const std::vector<int> redo = flagged(ar, s, flags, nq);
   if (redo.empty()) return;
+  if (l2 && use_stream) {
+    // the streamed scan summed its row norms itself; the exhaustive path
+    // reads them
+    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+  }
   const float *eb, *eq;
   fp32_rows(kbase, n, &eb);
   fp32_rows(kq, nq, &eq);
@@ -639,15 +670,22 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   const int ldw = ldb / 4;
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan = plan_splits(n, qblocks, k, T, 2, kern::kDeepRows,
-                               device_slots(kern::deep_bits_blocks_per_cu(T)), true);
+                               device_slots(kern::deep_bits_blocks_per_cu(T)), true,
+                               max_merge_segments(k, T));
   // the kernel fetches up to two tiles past a split's rows
   if (!plan.ok || (plan.rows_per_split + 2 * kern::kDeepRows) * ldb >= (int64_t(1) << 31))
     return false;
 
-  uint32_t* bw = ar.take<uint32_t>((size_t)n * ldw);
-  uint32_t* qw = ar.take<uint32_t>((size_t)nq * ldw);
-  launch(s, "pack", [&] { return kern::launch_pack({rows, n, nbytes, bw, ldw}, s); });
-  launch(s, "pack", [&] { return kern::launch_pack({queries, nq, nbytes, qw, ldw}, s); });
+  // rows of whole 16-byte chunks at a 16-byte aligned address are already
+  // the packed little-endian words: used in place
+  auto packed = [&](const uint8_t* x, int64_t rows_) -> const uint32_t* {
+    if (nbytes == ldb && (uintptr_t)x % 16 == 0) return (const uint32_t*)x;
+    uint32_t* w = ar.take<uint32_t>((size_t)rows_ * ldw);
+    launch(s, "pack", [&] { return kern::launch_pack({x, rows_, nbytes, w, ldw}, s); });
+    return w;
+  };
+  const uint32_t* bw = packed(rows, n);
+  const uint32_t* qw = packed(queries, nq);
   float* bpop = ar.take<float>((size_t)n);
   float* qpop = ar.take<float>((size_t)nq);
   launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, s); });
@@ -664,8 +702,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
                      plan.xcd ? 1 : 0};
   launch(s, "hamming_mfma", [&] { return kern::launch_deep_bits(fa, s); });
   int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
-  kern::MergeArgs ma{part, nseg, T, k, (int)nq, kern::kL2, qpop, 0, ids, dists, flags};
-  launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+  merge_lists(ar, s, part, nseg, T, k, nq, kern::kL2, qpop, 0, ids, dists, flags);
   if (T >= k) return true;
   const std::vector<int> redo = flagged(ar, s, flags, nq);
   if (!redo.empty()) hamming_exhaustive(ar, s, bw, qw, ldw, n, redo, k, ids, dists);
@@ -701,7 +738,8 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
     kern::HammingArgs ha{bw, qw, n, (int)nq, Wp, plan.rows_per_split, plan.nsplit, T, part};
     launch(s, "hamming", [&] { return kern::launch_hamming(ha, s); });
     int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
-    kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags};
+    kern::MergeArgs ma{part, plan.nsplit, T, k, (int)nq, kern::kL2, nullptr, 1, ids, dists, flags,
+                       nullptr};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     if (T >= k) return;
     redo = flagged(ar, s, flags, nq);
@@ -852,7 +890,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, bp.m, bp.pubj,
                        0, 0, ditems, dpairs, offsets, dslots, P, it.n, nullptr, width, 0};
     launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
-    kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr};
+    kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr, nullptr};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     kern::IvfMapArgs mp{ids, dists, (int)nq, k, nullptr, 0, probes, dslots, offsets, indices, P,
                         pad};

@@ -763,9 +763,22 @@ __global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
   const uint64_t* src = a.part + ((int64_t)q * a.nseg + s0) * a.T;
   for (int i = threadIdx.x; i < P; i += 256) buf[i] = i < C ? src[i] : 0;
   __syncthreads();
+  if (a.sentinel) {
+    // the largest last entry of the group's full lists, before the sort
+    // reorders buf (lists are read from src)
+    __shared__ unsigned long long s_max;
+    if (threadIdx.x == 0) s_max = 0;
+    __syncthreads();
+    for (int g2 = threadIdx.x; g2 < s1 - s0; g2 += 256) {
+      const uint64_t last = src[(int64_t)g2 * a.T + a.T - 1];
+      if (last != 0) atomicMax(&s_max, (unsigned long long)last);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) a.sentinel[(int64_t)q * a.ngroups + g] = s_max;
+  }
   bitonic_desc<256>(buf, P, IdentityOrder{});
-  uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.T;
-  for (int i = threadIdx.x; i < a.T; i += 256) dst[i] = i < P ? buf[i] : 0;
+  uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.keep;
+  for (int i = threadIdx.x; i < a.keep; i += 256) dst[i] = i < P ? buf[i] : 0;
 }
 
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
@@ -780,12 +793,14 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   if (threadIdx.x == 0) s_flag = 0;
   __syncthreads();
   bitonic_desc<256>(buf, P, IdentityOrder{});
-  if (a.T < a.k) {
+  if (a.flags) {
     // A full segment list whose worst entry made the final k may have had
     // more members than it could keep: send the query to the exhaustive path.
+    // (Ranks are distinct, so last >= kth means the entry is among the k.)
     const uint64_t kth = buf[a.k - 1];
     for (int g = threadIdx.x; g < a.nseg; g += 256) {
-      const uint64_t last = src[(int64_t)g * a.T + a.T - 1];
+      const uint64_t last = a.sentinel ? a.sentinel[(int64_t)q * a.nseg + g]
+                                       : src[(int64_t)g * a.T + a.T - 1];
       if (last != 0 && last >= kth) s_flag = 1;
     }
     __syncthreads();

@@ -371,6 +371,22 @@ __global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* word
   if (threadIdx.x < rows) out[row0 + threadIdx.x] = (float)pop[threadIdx.x];
 }
 
+// Popcounts of rows of L 16-byte vectors (L = 1, 2, 4, 8 or 16): one thread
+// per vector (coalesced loads), the row's L threads summed with lane
+// exchanges; a row never straddles a wavefront (L divides 64).
+__global__ __launch_bounds__(256) void popcount_rows16_kernel(const u32x4* __restrict__ v,
+                                                              int64_t n, int L, float* out) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool ok = e < n * L;
+  uint32_t c = 0;
+  if (ok) {
+    const u32x4 x = v[e];
+    c = __popc(x[0]) + __popc(x[1]) + __popc(x[2]) + __popc(x[3]);
+  }
+  for (int o = L >> 1; o > 0; o >>= 1) c += __shfl_xor(c, o);
+  if (ok && (threadIdx.x & (L - 1)) == 0) out[e / L] = (float)c;
+}
+
 template <int W, int T>
 hipError_t launch_inst(const HammingArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, (a.nq + kHammingQueriesPerBlock - 1) / kHammingQueriesPerBlock);
@@ -490,6 +506,14 @@ hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s) {
 hipError_t launch_popcount_rows(const uint32_t* words, int64_t n, int W, float* pop,
                                 hipStream_t s) {
   if (n <= 0) return hipSuccess;
+  const int L = W / 4;
+  if (W % 4 == 0 && (L == 1 || L == 2 || L == 4 || L == 8 || L == 16) &&
+      (uintptr_t)words % 16 == 0) {
+    const int64_t total = n * L;
+    hipLaunchKernelGGL(popcount_rows16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, s, (const u32x4*)words, n, L, pop);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(popcount_rows_kernel, dim3((unsigned)((n + kPopRows - 1) / kPopRows)),
                      dim3(256), 0, s, words, n, W, pop);
   return hipGetLastError();

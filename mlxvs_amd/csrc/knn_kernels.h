@@ -161,12 +161,20 @@ struct MergeArgs {
   int32_t* ids;          // [nq][k]
   float* dists;          // [nq][k] (may be null)
   int* flags;            // [nq] set to 1 when a segment may have dropped a member
+  // after a first level (merge_group with sentinels): [nq][nseg] the best of
+  // the worst entries of the group's full segment lists (0: none); the
+  // per-list check then uses these instead of the lists' last entries
+  const uint64_t* sentinel;
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
-// First merge level when the segments exceed what one workgroup sorts (only
-// for k <= T): the T best ranks of each group of gs consecutive segment
-// lists of a query, written as one list.  grid nq x ngroups.
+// First merge level when the segments exceed what one workgroup sorts: the
+// `keep` best ranks of each group of gs consecutive segment lists (keep = T
+// when k <= T, else k <= gs T: a group's best k hold all of its members of
+// the query's best k).  With T < k, sentinel [nq][ngroups] receives the
+// largest last entry among the group's full lists (0: none): the final
+// merge flags the query when one of them made the best k, as it does for
+// single-level lists.
 struct MergeGroupArgs {
   const uint64_t* part;  // [nq][nseg][T]
   int nseg;
@@ -174,7 +182,9 @@ struct MergeGroupArgs {
   int nq;
   int gs;                // segments per group, gs * T <= kMaxMergeCandidates
   int ngroups;
-  uint64_t* out;         // [nq][ngroups][T]
+  int keep;              // ranks kept per group
+  uint64_t* out;         // [nq][ngroups][keep]
+  uint64_t* sentinel;    // [nq][ngroups] or null (k <= T)
 };
 hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s);
 

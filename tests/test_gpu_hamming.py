@@ -115,3 +115,37 @@ def test_c4_device_api(engine, c4_data):
     hid, hdist = engine.hamming_knn(base, q, 100)
     assert np.array_equal(di.download(hid.shape, np.int32), hid)
     assert np.array_equal(dd.download(hdist.shape, np.float32), hdist)
+
+
+@pytest.mark.parametrize("nq", [1, 7])
+@pytest.mark.parametrize("k", [10, 100, 256])
+@pytest.mark.parametrize("nbytes", [16, 128])
+def test_small_batches_exact(engine, oracle, nq, k, nbytes):
+    # a handful of queries: hundreds of splits, lists reduced in two levels
+    # (groups keep k; for k > 16 the final merge flags overflowing lists)
+    rng = np.random.default_rng(nq * 100 + k + nbytes)
+    x = rng.integers(0, 256, (150_000, nbytes), dtype=np.uint8)
+    q = rng.integers(0, 256, (nq, nbytes), dtype=np.uint8)
+    ids, dist = engine.hamming_knn(x, q, k)
+    oid, odist = oracle.hamming(x, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+
+
+def test_unaligned_rows_are_packed(engine, oracle):
+    # device rows at an address that is not 16-byte aligned take the packing
+    # copy; aligned whole-chunk rows are used in place: the same answers
+    from mlxvs_amd import _hip
+
+    rng = np.random.default_rng(5)
+    x = rng.integers(0, 256, (20_000, 32), dtype=np.uint8)
+    q = rng.integers(0, 256, (50, 32), dtype=np.uint8)
+    oid, odist = oracle.hamming(x, q, 12)
+    shifted = _hip.DeviceBuffer.from_array(np.concatenate([np.zeros(1, np.uint8), x.ravel()]))
+    aligned = _hip.DeviceBuffer.from_array(x)
+    dq = _hip.DeviceBuffer.from_array(q)
+    for ptr in (shifted.value + 1, aligned.value):
+        di, dd = _hip.DeviceBuffer(50 * 12 * 4), _hip.DeviceBuffer(50 * 12 * 4)
+        engine.hamming_knn_device(ptr, 20_000, dq.value, 50, 32, 12, di.value, dd.value)
+        _hip.synchronize()
+        assert np.array_equal(di.download((50, 12), np.int32), oid)
+        assert np.array_equal(dd.download((50, 12), np.float32), odist)

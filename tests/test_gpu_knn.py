@@ -435,3 +435,31 @@ def test_small_batch_ties_keep_lowest_ids(engine):
     x = np.ones((50_000, 16), np.float32)
     ids, dist = engine.brute_force_knn(x, np.ones((2, 16), np.float32), 16, "l2")
     assert (ids == np.arange(16)).all() and (dist == 0).all()
+
+
+@pytest.mark.parametrize("nq", [1, 5, 32])
+@pytest.mark.parametrize("k", [17, 64, 100, 256])
+def test_small_batch_large_k_bit_exact(engine, oracle, nq, k):
+    # k > T on the streamed scan: thousands of 16-long lists reduced in two
+    # levels (groups keep k, the final merge flags a query when a full list's
+    # last entry made the k; flagged queries go exhaustive)
+    rng = np.random.default_rng(nq * 7 + k)
+    base = rng.integers(0, 6, (120_000, 64)).astype(np.float32)
+    q = rng.integers(0, 6, (nq, 64)).astype(np.float32)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(base, q, k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
+
+
+def test_small_batch_large_k_clustered_ids():
+    # the k best in a contiguous id range: few lists hold all of them, so
+    # the lists overflow and the flagged query is answered exhaustively
+    x = np.full((200_000, 8), 100.0, np.float32)
+    x[5000:5300] = 1.0
+    x[5000:5300, 0] = np.arange(300, dtype=np.float32) / 1000.0
+    import mlxvs_amd
+    ids, dist = mlxvs_amd.brute_force_knn(x, np.ones((1, 8), np.float32), 200, "l2")
+    want = np.argsort(((x.astype(np.float64) - 1.0) ** 2).sum(1), kind="stable")[:200]
+    assert np.array_equal(ids[0], want)
