@@ -669,12 +669,17 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   if (ldb == 0 || nq >= (int64_t(1) << 31) || !kern::deep_bits_supported(ldb, T)) return false;
   const int ldw = ldb / 4;
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  SplitPlan plan = plan_splits(n, qblocks, k, T, 2, kern::kDeepRows,
-                               device_slots(kern::deep_bits_blocks_per_cu(T)), true,
-                               max_merge_segments(k, T));
-  // the kernel fetches up to two tiles past a split's rows
-  if (!plan.ok || (plan.rows_per_split + 2 * kern::kDeepRows) * ldb >= (int64_t(1) << 31))
-    return false;
+  // at most 32 queries: packed rows streamed straight into registers
+  const bool use_stream = kern::stream_bits_supported(ldb, T, nq);
+  const int lanes = use_stream ? 8 : 2;
+  const int bpc = use_stream ? kern::stream_bits_blocks_per_cu(ldb, T)
+                             : kern::deep_bits_blocks_per_cu(T);
+  SplitPlan plan = plan_splits(n, qblocks, k, T, lanes, kern::kDeepRows, device_slots(bpc),
+                               !use_stream, max_merge_segments(k, T));
+  // the kernels fetch up to two tiles (stream: per wavefront) past a split's
+  // rows
+  const int64_t past = use_stream ? 3 * kern::kDeepRows : 2 * kern::kDeepRows;
+  if (!plan.ok || (plan.rows_per_split + past) * ldb >= (int64_t(1) << 31)) return false;
 
   // rows of whole 16-byte chunks at a 16-byte aligned address are already
   // the packed little-endian words: used in place
@@ -686,12 +691,16 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   };
   const uint32_t* bw = packed(rows, n);
   const uint32_t* qw = packed(queries, nq);
-  float* bpop = ar.take<float>((size_t)n);
+  // row popcounts (the streamed scan sums its own)
+  float* bpop = nullptr;
+  if (!use_stream) {
+    bpop = ar.take<float>((size_t)n);
+    launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, s); });
+  }
   float* qpop = ar.take<float>((size_t)nq);
-  launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, s); });
   launch(s, "pack", [&] { return kern::launch_popcount_rows(qw, nq, ldw, qpop, s); });
 
-  const int nseg = 2 * plan.nsplit;
+  const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
   const BoundPlan bp = shared_bound(k, T, slots, nseg);
@@ -700,7 +709,10 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   kern::FusedArgs fa{bw, qw, bpop, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,
                      plan.nsplit, T, k, part, gkey, bp.m, bp.pubj, (int)qblocks,
                      plan.xcd ? 1 : 0};
-  launch(s, "hamming_mfma", [&] { return kern::launch_deep_bits(fa, s); });
+  if (use_stream)
+    launch(s, "stream_bits", [&] { return kern::launch_stream_bits(fa, s); });
+  else
+    launch(s, "hamming_mfma", [&] { return kern::launch_deep_bits(fa, s); });
   int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
   merge_lists(ar, s, part, nseg, T, k, nq, kern::kL2, qpop, 0, ids, dists, flags);
   if (T >= k) return true;

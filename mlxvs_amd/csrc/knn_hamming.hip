@@ -320,6 +320,140 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   }
 }
 
+// ---- small batches: packed rows streamed into registers ----------------------
+//
+// At most 32 queries and codes of up to 128 bytes: the search is HBM-bound
+// (a row's 128 bytes against 32 x 2,048 MFMA ops).  stream_bits_kernel: four
+// independent wavefronts per workgroup, no LDS and no barrier, as the fp32
+// stream kernel.  Lane (h, col) owns words [h NW / 2, (h + 1) NW / 2) of its
+// row and of query col: the query's words are unpacked to e2m1 nibbles once
+// (4 registers per word, one MFMA step per word), the row's packed words
+// arrive straight from HBM two tiles ahead and are unpacked at their step.
+// The row popcounts are summed from the same registers (each lane its
+// words, then the pair) and read as scalars for the score layout, so no
+// popcount pass over the base runs.  Segments: eight per workgroup,
+// 8 split + 2 w + h.
+template <int NW, int T>
+__global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
+  constexpr int HW = NW / 2;       // words per lane (one MFMA step each)
+  constexpr int NV = HW / 4;       // 16-byte loads per lane and tile (HW >= 4)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x;
+  const int q = col;
+  const bool qvalid = q < a.nq;
+  constexpr int ldb = 4 * NW;
+  const int64_t r0 = (int64_t)split * a.rows_per_split;
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  const int nrows = r1 > r0 ? (int)(r1 - r0) : 0;
+  const int ntiles = (nrows + 31) / 32;
+  const int mine = ntiles > wave ? (ntiles - wave + 3) / 4 : 0;  // tiles wave, wave + 4, ...
+
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const char*)a.base + r0 * ldb), (short)0, nrows * ldb, 0x00020000);
+
+  // the lane's query words as nibbles (zero for lanes without a query)
+  i32x4 qn[HW];
+  {
+    const u32x4* qr = (const u32x4*)((const char*)a.queries + (int64_t)(qvalid ? q : 0) * ldb +
+                                     16 * NV * h);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (qvalid) w = qr[v];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t x = w[e];
+        qn[4 * v + e] = i32x4{(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u),
+                              (int)((x >> 1) & 0x22222222u), (int)((x >> 2) & 0x22222222u)};
+      }
+    }
+  }
+
+  u32x4 A[2][NV];
+  auto issue = [&](int slot, int i) {
+    const int tw = wave + 4 * i;
+    const uint32_t off = (uint32_t)((tw * 32 + col) * ldb + 16 * NV * h);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) A[slot][v] = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 16 * v, 0, 0);
+  };
+
+  uint32_t K[T], I[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  float thr = score_of_key(0u);
+  auto step = [&](int slot, int i) {
+    floatx16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    uint32_t pc = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t x = A[slot][v][e];
+        pc += __popc(x);
+        const i32x8 av = {(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u),
+                          (int)((x >> 1) & 0x22222222u), (int)((x >> 2) & 0x22222222u), 0, 0, 0, 0};
+        const i32x4 b4 = qn[4 * v + e];
+        const i32x8 bq = {b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bq, acc, 4, 4, 0, 0x7f7f7f7f,
+                                                              0, 0x7f7f7f7f);
+      }
+    }
+    // row col's popcount (the pair's sums), then row 8 j + 4 h + u's at score
+    // slot 4 j + u, read from lane 8 j + 4 h + u as a scalar
+    const int pop = (int)pc + __shfl_xor((int)pc, 32);
+    float sc[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p0 = __builtin_amdgcn_readlane(pop, 8 * j + u);
+        const int p1 = __builtin_amdgcn_readlane(pop, 8 * j + 4 + u);
+        sc[4 * j + u] = __builtin_fmaf(2.0f, acc[4 * j + u], -(float)(h ? p1 : p0));
+      }
+    // the slot is consumed: refill it with the tile two ahead (out of range
+    // past the end: zeros)
+    issue(slot, i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    const int tw = wave + 4 * i;
+    select_block<T>(K, I, thr, sc, h, (uint32_t)(r0 + tw * 32), nrows - tw * 32);
+  };
+
+  // both steps run in every iteration (an odd count's last is past the
+  // split: zero rows, nothing real), and slot 0 is issued before slot 1, so
+  // every path into the loop head has the same loads outstanding
+  issue(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int i = 0; i < mine; i += 2) {
+    step(0, i);
+    step(1, i + 1);
+  }
+
+  if (qvalid) {
+    uint64_t* dst = a.part + ((int64_t)q * (8 * a.nsplit) + 8 * split + 2 * wave + h) * T;
+#pragma unroll
+    for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
+  }
+}
+
+template <int NW>
+hipError_t stream_bits_t(const FusedArgs& a, hipStream_t s) {
+  const dim3 grid(a.nsplit);
+  switch (a.T) {
+    case 4: hipLaunchKernelGGL((stream_bits_kernel<NW, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((stream_bits_kernel<NW, 8>), grid, dim3(256), 0, s, a); break;
+    case 10: hipLaunchKernelGGL((stream_bits_kernel<NW, 10>), grid, dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((stream_bits_kernel<NW, 16>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int NCT, int T>
 int bits_occupancy() {
   int blocks = 0;
@@ -499,6 +633,36 @@ hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s) {
     case 4: return bits_dispatch_t<4>(a, s);
     case 8: return bits_dispatch_t<8>(a, s);
     case 16: return bits_dispatch_t<16>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+int stream_bits_blocks_per_cu(int ld, int T) {
+  int blocks = 0;
+  hipError_t e = hipErrorInvalidValue;
+  auto occ = [&](auto kernel) { e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, 0); };
+  const int nw = ld / 4;
+  if (nw == 32) {
+    if (T == 16) occ(stream_bits_kernel<32, 16>); else occ(stream_bits_kernel<32, 10>);
+  } else if (nw == 16) {
+    if (T == 16) occ(stream_bits_kernel<16, 16>); else occ(stream_bits_kernel<16, 10>);
+  } else {
+    if (T == 16) occ(stream_bits_kernel<8, 16>); else occ(stream_bits_kernel<8, 10>);
+  }
+  return e == hipSuccess && blocks > 0 ? blocks : 1;
+}
+
+bool stream_bits_supported(int ld, int T, int64_t nq) {
+  return nq <= 32 && (ld == 32 || ld == 64 || ld == 128) &&
+         (T == 4 || T == 8 || T == 10 || T == 16);
+}
+
+hipError_t launch_stream_bits(const FusedArgs& a, hipStream_t s) {
+  if (!stream_bits_supported(a.ld, a.T, a.nq)) return hipErrorInvalidValue;
+  switch (a.ld) {
+    case 32: return stream_bits_t<8>(a, s);
+    case 64: return stream_bits_t<16>(a, s);
+    case 128: return stream_bits_t<32>(a, s);
   }
   return hipErrorInvalidValue;
 }

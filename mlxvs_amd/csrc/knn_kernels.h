@@ -110,6 +110,13 @@ int deep_blocks_per_cu(int T);
 // Hamming distance, and every product and sum is exact on the FP4 MFMA
 // (fp32 accumulation of integers below 2^24).
 hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s);
+// Small batches (nq <= 32, ld = 32, 64 or 128 bytes): grid nsplit, four
+// independent wavefronts per workgroup streaming their own 32-row tiles,
+// eight segments per split (part [nq][8 nsplit][T]); the kernel sums the row
+// popcounts itself (bnorm unused); no shared bound.
+hipError_t launch_stream_bits(const FusedArgs& a, hipStream_t s);
+bool stream_bits_supported(int ld, int T, int64_t nq);
+int stream_bits_blocks_per_cu(int ld, int T);
 bool deep_bits_supported(int ld, int T);
 int deep_bits_blocks_per_cu(int T);
 // the packed row length with an instance for nbytes-byte codes (0: none)
