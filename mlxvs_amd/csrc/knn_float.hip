@@ -296,7 +296,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
   // the filter: the score of K[T-1] or better (NaN -- every candidate
   // passes -- while the list has room and nothing better is known)
-  float thr = score_of_key(0u);
+  // (+inf for a lane without a query: nothing passes, so it never
+  // lengthens the wavefront's drain)
+  float thr = qvalid ? score_of_key(0u) : INFINITY;
   // All lanes of a query -- in every workgroup -- filter with the shared
   // lower bound on its k-th best score (SharedBound), raised with relaxed
   // atomic max operations as the segment lists fill.
@@ -526,7 +528,9 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  float thr = score_of_key(0u);
+  // (+inf for a lane without a query: nothing passes, so it never
+  // lengthens the wavefront's drain)
+  float thr = qvalid ? score_of_key(0u) : INFINITY;
   constexpr int S = bound_slots<T>();
   const bool share = a.mslots > 0;
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
@@ -689,7 +693,9 @@ __global__ __launch_bounds__(256, DH >= 64 ? 1 : 2) void stream_kernel(FusedArgs
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  float thr = score_of_key(0u);
+  // (+inf for a lane without a query: nothing passes, so it never
+  // lengthens the wavefront's drain)
+  float thr = qvalid ? score_of_key(0u) : INFINITY;
   auto step = [&](int slot, int i) {
     floatx16 acc;
 #pragma unroll

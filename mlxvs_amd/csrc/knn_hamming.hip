@@ -218,7 +218,9 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  float thr = score_of_key(0u);
+  // (+inf for a lane without a query: nothing passes, so it never
+  // lengthens the wavefront's drain)
+  float thr = qvalid ? score_of_key(0u) : INFINITY;
   constexpr int S = bound_slots<T>();
   const bool share = a.mslots > 0;
   const bool share1 = a.mslots == 1;
@@ -382,7 +384,9 @@ __global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  float thr = score_of_key(0u);
+  // (+inf for a lane without a query: nothing passes, so it never
+  // lengthens the wavefront's drain)
+  float thr = qvalid ? score_of_key(0u) : INFINITY;
   auto step = [&](int slot, int i) {
     floatx16 acc;
 #pragma unroll
