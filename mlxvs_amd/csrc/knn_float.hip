@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "knn_kernels.h"
@@ -787,6 +788,120 @@ __global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
   for (int i = threadIdx.x; i < a.keep; i += 256) dst[i] = i < P ? buf[i] : 0;
 }
 
+// One wavefront per query (four per workgroup) for up to 1,024 candidates:
+// the P = 64 E ranks sit in registers, element i = lane E + e, and a bitonic
+// network sorts them (descending): pairs closer than E are exchanged within
+// a lane, the others with the partner lane (lane ^ stride / E) through lane
+// shuffles.  No LDS and no barrier, where merge_kernel sorts in LDS with a
+// workgroup barrier per stage.  Then the same steps as merge_kernel: the k
+// best by rank, the overflow flags, the reference's output order (the rank
+// order except that -0 and +0 scores tie and fall back to the id: when a -0
+// key is among the k, the k are sorted again by that order), distances.
+template <int E>
+__device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, bool out_order) {
+  auto ord = [&](uint64_t r) { return out_order ? output_order(r) : r; };
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= E) {
+        const int lm = stride / E;  // partner lane distance
+        const bool lo = (lane & lm) == 0;
+        const bool desc = ((lane * E) & size) == 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint32_t plo = __shfl_xor((uint32_t)x[e], lm);
+          const uint32_t phi = __shfl_xor((uint32_t)(x[e] >> 32), lm);
+          const uint64_t y = ((uint64_t)phi << 32) | plo;
+          const bool keep_big = lo == desc;
+          const bool xb = ord(x[e]) > ord(y);
+          x[e] = (keep_big == xb) ? x[e] : y;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if ((e & stride) == 0) {
+            const int f = e | stride;
+            const bool desc = ((lane * E + e) & size) == 0;
+            const uint64_t u = x[e], v = x[f];
+            const bool sw = desc ? (ord(u) < ord(v)) : (ord(u) > ord(v));
+            x[e] = sw ? v : u;
+            x[f] = sw ? u : v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int E>
+__global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;  // whole wavefronts: no barrier follows
+  const int C = a.nseg * a.T;
+  const int P = 64 * E;
+  const uint64_t* src = a.part + (int64_t)q * C;
+  uint64_t x[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane * E + e;
+    x[e] = i < C ? src[i] : 0;
+  }
+  wave_bitonic<E>(x, lane, P, false);
+  // the k-th best rank (element k - 1), broadcast
+  const int kl = (a.k - 1) / E, ke = (a.k - 1) % E;
+  uint64_t mine = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) mine = e == ke ? x[e] : mine;
+  const uint32_t klo = __shfl((uint32_t)mine, kl), khi = __shfl((uint32_t)(mine >> 32), kl);
+  const uint64_t kth = ((uint64_t)khi << 32) | klo;
+  if (a.flags) {
+    bool f = false;
+    for (int g = lane; g < a.nseg; g += 64) {
+      const uint64_t last = a.sentinel ? a.sentinel[(int64_t)q * a.nseg + g]
+                                       : src[(int64_t)g * a.T + a.T - 1];
+      f |= last != 0 && last >= kth;
+    }
+    const bool any = __builtin_amdgcn_ballot_w64(f) != 0;
+    if (lane == 0) a.flags[q] = any ? 1 : 0;
+  }
+  // keep the k best; when a -0 key is among them, order them as the output
+  bool negz = false;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane * E + e;
+    if (i >= a.k) x[e] = 0;
+    negz |= x[e] != 0 && (uint32_t)(x[e] >> 32) == 0x7fffffffu;
+  }
+  if (__builtin_amdgcn_ballot_w64(negz) != 0) wave_bitonic<E>(x, lane, P, true);
+  const bool l2 = a.metric == kL2;
+  const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane * E + e;
+    if (i < a.k) {
+      const uint64_t r = x[e];
+      const int64_t o = (int64_t)q * a.k + i;
+      if (r == 0) {
+        a.ids[o] = -1;
+        if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
+      } else {
+        a.ids[o] = id_of_rank(r);
+        const float sv = score_of_key((uint32_t)(r >> 32));
+        if (a.dists) {
+          if (a.dist_mode == 1) {
+            a.dists[o] = -sv;
+          } else if (l2) {
+            const float v = qn - sv;  // reference src/knn.cpp:126-129
+            a.dists[o] = v > 0.0f ? v : 0.0f;
+          } else {
+            a.dists[o] = sv;
+          }
+        }
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   __shared__ uint64_t buf[kMaxMergeCandidates];
   __shared__ uint64_t work[kMaxK];
@@ -1312,7 +1427,21 @@ hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s) {
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
   if (a.nq <= 0) return hipSuccess;
-  hipLaunchKernelGGL(merge_kernel, dim3(a.nq), dim3(256), 0, s, a);
+  int P = 1;
+  while (P < std::max(a.nseg * a.T, a.k)) P <<= 1;
+  const dim3 wgrid((unsigned)((a.nq + 3) / 4));
+  if (P <= 64)
+    hipLaunchKernelGGL(merge_wave_kernel<1>, wgrid, dim3(256), 0, s, a);
+  else if (P == 128)
+    hipLaunchKernelGGL(merge_wave_kernel<2>, wgrid, dim3(256), 0, s, a);
+  else if (P == 256)
+    hipLaunchKernelGGL(merge_wave_kernel<4>, wgrid, dim3(256), 0, s, a);
+  else if (P == 512)
+    hipLaunchKernelGGL(merge_wave_kernel<8>, wgrid, dim3(256), 0, s, a);
+  else if (P == 1024)
+    hipLaunchKernelGGL(merge_wave_kernel<16>, wgrid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(merge_kernel, dim3(a.nq), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
