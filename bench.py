@@ -305,7 +305,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if base.dtype == np.float16 else ("i8" if w["kind"] == "hamming" else "f32"),
+        "dtype": "f16" if base.dtype == np.float16 else ("e2m1" if w["kind"] == "hamming" else "f32"),
         "data": "synthetic (mlxvs_amd.synth, seeded splitmix64)",
         "config": {"workload": w["desc"], "n": n, "nq": nq, "d": d, "k": k,
                    "metric": w["metric"], "parallelism": "single GPU"},

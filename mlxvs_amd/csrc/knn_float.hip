@@ -157,6 +157,22 @@ __global__ __launch_bounds__(256) void rows_transform_kernel(PrepArgs a) {
 template <bool F16, int DH>
 constexpr int fused_min_blocks() { return (!F16 && DH >= 128) ? 1 : 2; }
 
+// Buffer loads of 16 / 4 bytes per lane straight into LDS: lane l writes at
+// lds + 16 l (4 l); lds is wavefront-uniform; out-of-range lanes write
+// zeros.  (The builtin exists only for the device target.)
+__device__ __forceinline__ void load16_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voff, 0, 0, 0);
+#endif
+}
+__device__ __forceinline__ void load4_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                           voff, 0, 0, 0);
+#endif
+}
+
 // 32-row MFMA blocks per streamed tile: two where the registers allow, which
 // halves the barriers and per-tile overhead per row.  One where the query
 // fragments take 128 VGPRs (fp32, 256 dims): the second accumulator and
@@ -181,10 +197,21 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr int TR = 32 * RB;         // rows per tile
   constexpr int VTILE = TR * VROW;
   constexpr int NPF = (VTILE + 255) / 256;
-  constexpr int STRIDE = D + EPV;     // 16-byte pad: 8 rows hit distinct bank quads
+  constexpr int ROWE = D;             // elements per LDS row (no pad: swizzled)
   constexpr int QV = DH / EPV;        // query vectors per lane
-  __shared__ __align__(16) E tile[2][TR * STRIDE];
-  __shared__ __align__(16) float tnorm[2][TR];
+  static_assert(VTILE % 256 == 0, "a tile is whole 64-vector chunks for every thread");
+  // Vector c of tile row r is stored at slot c ^ swz(r): the 16 rows that a
+  // quarter-wavefront reads at the same vector index sit in distinct bank
+  // quads without padding (the tile is written by LDS-direct loads, 64
+  // contiguous vectors per instruction).
+  constexpr int SWZ = VROW < 16 ? VROW - 1 : 15;
+  // two separately named buffers (not one array indexed by parity), so the
+  // compiler sees that the loads into one never alias the reads of the
+  // other and does not wait for them before every read
+  __shared__ __align__(16) E tile0[TR * ROWE];
+  __shared__ __align__(16) E tile1[TR * ROWE];
+  __shared__ __align__(16) float tnorm0[64];  // 64: a norm load writes 64 lanes
+  __shared__ __align__(16) float tnorm1[64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -236,22 +263,26 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const float* snorm = l2 ? a.bnorm + r0 : (const float*)a.base;
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
       (void*)snorm, (short)0, l2 ? nrows * 4 : 0, 0x00020000);
-  // Byte offsets of this thread's 16-byte vectors in the next tile to
-  // fetch.  They are carried from tile to tile (+tile_bytes), so they stay
-  // live across the MFMA chain and never share registers with the
-  // accumulators (a VMEM address register overwritten by an MFMA forces a
-  // wait for the load).  Vectors past ld start at 2^31, beyond every range
-  // (ranges are < 2^31 bytes), and read zero.
+  // The tile is fetched straight into LDS (buffer loads with the lds flag:
+  // lane l of an instruction writes 16 bytes at the instruction's LDS base +
+  // 16 l), one tile ahead, so no register staging and no LDS stores.
+  // Instruction j of wavefront w fills LDS vectors [64 g, 64 g + 64), g =
+  // w NPF + j: lane l's vector p = 64 g + l is row p / VROW, slot p % VROW,
+  // so it fetches vector slot ^ swz(row) of that row.  Byte offsets are
+  // carried from tile to tile (+tile_bytes); vectors past ld start at 2^31,
+  // beyond every range (ranges are < 2^31 bytes), and read zero, as do rows
+  // past the split.
   const uint32_t tile_bytes = TR * ld * (uint32_t)sizeof(E);
   uint32_t voff[NPF];
 #pragma unroll
   for (int j = 0; j < NPF; ++j) {
-    const int e = tid + 256 * j;
-    const int r = e / VROW, c = (e % VROW) * EPV;
-    voff[j] = (e < VTILE && c < ld) ? (uint32_t)((r * ld + c) * (int)sizeof(E)) : 0x80000000u;
+    const int p = 64 * (wave * NPF + j) + lane;
+    const int r = p / VROW, c = ((p % VROW) ^ (r & SWZ)) * EPV;
+    voff[j] = c < ld ? (uint32_t)((r * ld + c) * (int)sizeof(E)) : 0x80000000u;
   }
-  // norm word of this thread (threads past the tile read beyond the range)
-  uint32_t noff = tid < TR ? tid * 4u : 0x80000000u;
+  // norm word of this lane (wavefront 0 loads the tile's norms; lanes past
+  // the tile read beyond the range)
+  uint32_t noff = lane < TR ? lane * 4u : 0x80000000u;
 
   // the lane's query dims [h DH, h DH + DH): 16-byte loads of the query
   // row, zero past ld and for lanes without a query (plain global loads: a
@@ -268,28 +299,14 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     }
   }
 
-  // raw bits: the tile and norm words are moved, not converted
-  u32x4 pf[NPF];
-  uint32_t pn = 0;
-  auto issue_loads = [&]() {
+  auto issue_loads = [&](E* dst, float* ndst) {
 #pragma unroll
     for (int j = 0; j < NPF; ++j) {
-      pf[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, voff[j], 0, 0);
+      load16_to_lds(rb, dst + 64 * (wave * NPF + j) * EPV, voff[j]);
       voff[j] += tile_bytes;
     }
-    if (l2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+    if (l2 && wave == 0) load4_to_lds(rn, ndst, noff);
     noff += TR * 4;
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-      const int e = tid + 256 * j;
-      if (e < VTILE) {
-        const int r = e / VROW, c = (e % VROW) * EPV;
-        *(u32x4*)&tile[buf][r * STRIDE + c] = pf[j];
-      }
-    }
-    if (l2 && tid < TR) tnorm[buf][tid] = __uint_as_float(pn);
   };
 
   uint32_t K[T], I[T];
@@ -308,10 +325,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
   const int myslot = share ? (2 * seg + h) % a.mslots : 0;
 
-  if (ntiles > 0) {
-    issue_loads();
-    store_tile(0);
-  }
+  if (ntiles > 0) issue_loads(tile0, tnorm0);
   // nothing may be outstanding at the loop head: the query fragments are
   // read in every iteration, and a pending prologue load would otherwise
   // make each iteration wait for its own tile prefetch as well
@@ -322,15 +336,16 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   // and the reads of a query's bound words are what sharing costs)
   SharedBound<S> seen;
   seen.clear();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+  // tile t from (cur, ncur); tile t + 1 into (nxt, nnxt)
+  auto step = [&](const E* cur, const float* ncur, E* nxt, float* nnxt, int t) {
     // read before the tile prefetch, so that waiting for it (in the
     // epilogue) does not wait for the prefetch
     if constexpr (MODE != 2)
       if (share && (t & 3) == 0) seen.load(gk, a.mslots);
-    // unconditional (past the last tile the offsets are out of range and
-    // read zero), so the wait counts after the shared key stay static
-    issue_loads();
+    // the next tile into the other buffer (read in the previous tile, which
+    // every wavefront has left: the barrier below); unconditional (past the
+    // last tile the offsets are out of range and read zero)
+    issue_loads(nxt, nnxt);
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
       floatx16 acc[RB];
@@ -338,24 +353,36 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
-      const E* arow = &tile[buf][col * STRIDE + h * DH];
+      // row col's vectors h QV + v at their swizzled slots (rows col + 32 r
+      // share the swizzle)
+      const E* arow = cur + col * ROWE;
+      const int sw = col & SWZ;
+      auto frag_at = [&](int r, int v) { return arow + r * 32 * ROWE + EPV * ((h * QV + v) ^ sw); };
+      // A fragments one step ahead: the LDS reads of step v + 1 are issued
+      // before the MFMAs of step v (a scheduling barrier keeps them there),
+      // so the MFMA chain does not wait for LDS at every step
+      typedef typename std::conditional<F16, halfx8, floatx4>::type fragv;
+      fragv av[2][RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) av[0][r] = *(const fragv*)frag_at(r, 0);
 #pragma unroll
       for (int v = 0; v < QV; ++v) {
+        if (v + 1 < QV) {
+#pragma unroll
+          for (int r = 0; r < RB; ++r) av[(v + 1) & 1][r] = *(const fragv*)frag_at(r, v + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (F16) {
 #pragma unroll
-          for (int r = 0; r < RB; ++r) {
-            const halfx8 av = *(const halfx8*)(arow + r * 32 * STRIDE + 8 * v);
-            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[v], acc[r], 0, 0, 0);
-          }
+          for (int r = 0; r < RB; ++r)
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[v & 1][r], qf[v], acc[r], 0, 0, 0);
         } else {
-          floatx4 av[RB];
-#pragma unroll
-          for (int r = 0; r < RB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * STRIDE + 4 * v);
 #pragma unroll
           for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int r = 0; r < RB; ++r)
-              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], qf[v][u], acc[r], 0, 0, 0);
+              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[v & 1][r][u], qf[v][u], acc[r], 0,
+                                                            0, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -369,7 +396,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if constexpr (L2) {
-            const floatx4 nb = *(const floatx4*)&tnorm[buf][32 * r + 8 * j + 4 * h];
+            const floatx4 nb = *(const floatx4*)&ncur[32 * r + 8 * j + 4 * h];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
               sc[4 * j + u] = __builtin_fmaf(2.0f, acc[r][4 * j + u], -nb[u]);
@@ -402,8 +429,13 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    store_tile(buf ^ 1);
+    // this wavefront's LDS-direct loads have landed (the barrier's fence
+    // waits for them), and every wavefront is done with cur
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(tile0, tnorm0, tile1, tnorm1, t);
+    if (t + 1 < ntiles) step(tile1, tnorm1, tile0, tnorm0, t + 1);
   }
 
   if (MODE != 2 && qvalid) {
