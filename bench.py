@@ -27,7 +27,7 @@ The same JSON line carries:
   check         the last step's answers for the first 64 queries against the
                 float64 golden fixture (bit-exact, integer-valued data).
 
-Other workloads (c1, c3, c3cos, c4, c5, ivf) are for measurement runs; the
+Other workloads (c1, c2h, c3, c3cos, c4, c5, ivf) are for measurement runs; the
 driver's line is the default.  --workload copy times a 1 GiB device copy, the
 reference reading for scaling HBM byte counters.
 """
@@ -64,10 +64,17 @@ def workload(name: str):
         q = synth.c1_rows(2, 0, 100)
         return dict(kind="float", base=base, q=q, k=10, metric="l2",
                     desc="c1: exact L2 kNN k=10, 10k x 128 fp32 (int-valued), 100 queries")
-    if name == "c2":
+    if name in ("c2", "c2h"):
         cen = synth.c2_centres()
         base = synth.chunked(lambda lo, hi: synth.c2_rows(1, lo, hi, centres=cen), 1_000_000)
         q = synth.chunked(lambda lo, hi: synth.c2_rows(2, lo, hi, centres=cen), 10_000)
+        if name == "c2h":
+            # the same integers in [0, 255] stored as binary16 (exact), on the
+            # fp16 MFMA path: answers identical to c2's
+            return dict(kind="float", base=base.astype(np.float16), q=q.astype(np.float16),
+                        k=10, metric="l2",
+                        desc="c2h: c2 (1M x 128, int-valued, 10k queries) stored as fp16, "
+                             "L2 k=10")
         return dict(kind="float", base=base, q=q, k=10, metric="l2",
                     desc="c2: exact L2 kNN k=10, 1M x 128 fp32 base (1024-component "
                          "mixture, int-valued in [0,255]), 10k queries")
@@ -139,6 +146,9 @@ def cpu_baseline(w, sample: int):
         c, data, ind, off = w["index"]
         oracle.ivf_flat(c, data, ind, off, q, w["k"], w["n_probes"], w["metric"],
                         nthreads=threads)
+    elif base.dtype == np.float16:
+        oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), w["k"], w["metric"],
+                   nthreads=threads)
     else:
         oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
     dt = time.perf_counter() - t0
@@ -224,8 +234,9 @@ def main() -> int:
     ids = di.download((nq, k), np.int32)
     dist = dd.download((nq, k), np.float32)
     check = None
-    if args.workload in ("c1", "c2", "c4"):
-        fx = {"c1": "c1_full.npz", "c2": "c2_subset.npz", "c4": "c4_subset.npz"}[args.workload]
+    if args.workload in ("c1", "c2", "c2h", "c4"):
+        fx = {"c1": "c1_full.npz", "c2": "c2_subset.npz", "c2h": "c2_subset.npz",
+              "c4": "c4_subset.npz"}[args.workload]
         g = np.load(ROOT / "tests" / "golden" / fx)
         m = min(g["ids"].shape[0], nq)
         ok = np.array_equal(ids[:m], g["ids"][:m]) and np.array_equal(
@@ -290,8 +301,8 @@ def main() -> int:
 
     sample = args.cpu_sample
     if sample is None:
-        sample = {"c1": 100, "c2": 10000, "c3": 16, "c3cos": 16, "c4": 256, "c5": 512,
-                  "ivf": 10000}[args.workload]
+        sample = {"c1": 100, "c2": 10000, "c2h": 2000, "c3": 16, "c3cos": 16, "c4": 256,
+                  "c5": 512, "ivf": 10000}[args.workload]
     cpu = cpu_baseline(w, min(sample, nq)) if sample else None
 
     line = {
