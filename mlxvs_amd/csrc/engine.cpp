@@ -702,7 +702,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
 
   const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
-  const int slots = kern::bound_slots_for(T);
+  const int slots = use_stream ? kern::bound_slots_for(T) : kern::kBitsBoundSlots;
   const BoundPlan bp = shared_bound(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });

@@ -221,7 +221,9 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   // (+inf for a lane without a query: nothing passes, so it never
   // lengthens the wavefront's drain)
   float thr = qvalid ? score_of_key(0u) : INFINITY;
-  constexpr int S = bound_slots<T>();
+  // 16 slots: the bound is read once per 128-row tile of whole codes, so
+  // its reads cost little and the finer slots bound tighter (m ~ k / 3)
+  constexpr int S = kBitsBoundSlots;
   const bool share = a.mslots > 0;
   const bool share1 = a.mslots == 1;
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;

@@ -110,6 +110,8 @@ int deep_blocks_per_cu(int T);
 // Hamming distance, and every product and sum is exact on the FP4 MFMA
 // (fp32 accumulation of integers below 2^24).
 hipError_t launch_deep_bits(const FusedArgs& a, hipStream_t s);
+// bound slots per query of the bits kernel (gkey [nq][kBitsBoundSlots])
+constexpr int kBitsBoundSlots = 16;
 // Small batches (nq <= 32, ld = 32, 64 or 128 bytes): grid nsplit, four
 // independent wavefronts per workgroup streaming their own 32-row tiles,
 // eight segments per split (part [nq][8 nsplit][T]); the kernel sums the row
