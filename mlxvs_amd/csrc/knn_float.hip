@@ -1155,39 +1155,61 @@ __global__ void gather_kernel(const float* in, const int* sel, int rows, int d,
 
 // Self graph: drop the row's own id and -1 entries from its k+1 list, keep
 // k, order by nearness with lowest id first among equal distances
-// (reference src/all_neighbors.cpp:56-95).  One thread per row.  The input
-// is ordered by score and the distance is monotone in the score, so the
+// (reference src/all_neighbors.cpp:56-95).  A workgroup takes R rows
+// (R max(kin, k) <= 4096): their lists are staged through LDS with coalesced loads
+// and stores, and one thread per row does the work there.  The input is
+// ordered by score and the distance is monotone in the score, so the
 // insertion sort only reorders runs of equal distance.  dists is required.
-__global__ void self_drop_kernel(SelfDropArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= a.n) return;
-  const int32_t* iin = a.ids_in + r * a.kin;
-  const float* din = a.dists_in + r * a.kin;
-  int32_t* io = a.ids + r * a.k;
-  float* dout = a.dists + r * a.k;
-  const bool l2 = a.metric == kL2;
-  int m = 0;
-  for (int j = 0; j < a.kin && m < a.k; ++j) {
-    const int32_t id = iin[j];
-    if (id < 0 || id == (int32_t)r) continue;
-    const float v = din[j];
-    const float key = l2 ? v : -v;  // smaller is nearer
-    int p = m;
-    while (p > 0) {
-      const float pk = l2 ? dout[p - 1] : -dout[p - 1];
-      const bool after = pk < key || (pk == key && (uint32_t)io[p - 1] < (uint32_t)id);
-      if (after) break;
-      io[p] = io[p - 1];
-      dout[p] = dout[p - 1];
-      --p;
-    }
-    io[p] = id;
-    dout[p] = v;
-    ++m;
+constexpr int kSelfDropEntries = 4096;
+__global__ __launch_bounds__(256) void self_drop_kernel(SelfDropArgs a, int R) {
+  __shared__ int32_t si[kSelfDropEntries];
+  __shared__ float sd[kSelfDropEntries];
+  __shared__ int32_t oi[kSelfDropEntries];
+  __shared__ float od[kSelfDropEntries];
+  const int64_t r0 = (int64_t)blockIdx.x * R;
+  const int rows = (int)min((int64_t)R, a.n - r0);
+  const int kin = a.kin, k = a.k;
+  for (int e = threadIdx.x; e < rows * kin; e += 256) {
+    si[e] = a.ids_in[r0 * kin + e];
+    sd[e] = a.dists_in[r0 * kin + e];
   }
-  for (int j = m; j < a.k; ++j) {
-    io[j] = -1;
-    dout[j] = l2 ? INFINITY : -INFINITY;
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < rows) {
+    const int64_t r = r0 + t;
+    const int32_t* iin = si + t * kin;
+    const float* din = sd + t * kin;
+    int32_t* io = oi + t * k;
+    float* dout = od + t * k;
+    const bool l2 = a.metric == kL2;
+    int m = 0;
+    for (int j = 0; j < kin && m < k; ++j) {
+      const int32_t id = iin[j];
+      if (id < 0 || id == (int32_t)r) continue;
+      const float v = din[j];
+      const float key = l2 ? v : -v;  // smaller is nearer
+      int p = m;
+      while (p > 0) {
+        const float pk = l2 ? dout[p - 1] : -dout[p - 1];
+        const bool after = pk < key || (pk == key && (uint32_t)io[p - 1] < (uint32_t)id);
+        if (after) break;
+        io[p] = io[p - 1];
+        dout[p] = dout[p - 1];
+        --p;
+      }
+      io[p] = id;
+      dout[p] = v;
+      ++m;
+    }
+    for (int j = m; j < k; ++j) {
+      io[j] = -1;
+      dout[j] = l2 ? INFINITY : -INFINITY;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < rows * k; e += 256) {
+    a.ids[r0 * k + e] = oi[e];
+    a.dists[r0 * k + e] = od[e];
   }
 }
 
@@ -1534,8 +1556,12 @@ hipError_t launch_gather_f32(const float* in, const int* sel, int rows, int d,
 
 hipError_t launch_self_drop(const SelfDropArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(self_drop_kernel, dim3((unsigned)((a.n + 255) / 256)), dim3(256),
-                     0, s, a);
+  // R rows of kin inputs and k outputs each fit the staging arrays
+  const int w = std::max(a.kin, a.k);
+  if (w > kSelfDropEntries) return hipErrorInvalidValue;
+  const int R = std::min(256, kSelfDropEntries / w);
+  hipLaunchKernelGGL(self_drop_kernel, dim3((unsigned)((a.n + R - 1) / R)), dim3(256), 0, s, a,
+                     R);
   return hipGetLastError();
 }
 

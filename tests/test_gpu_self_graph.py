@@ -57,3 +57,14 @@ def test_c5_subset(engine, oracle):
     assert (np.abs(exact - dist[:32]) / np.maximum(1, exact)).max() < 2e-3
     np.testing.assert_allclose(dist[:32], g["dist"], rtol=2e-3)
     assert (ids[:32] == g["ids"]).mean() > 0.95
+
+
+@pytest.mark.parametrize("k", [1, 10, 64, 200, 255])
+def test_integer_rows_bit_exact(engine, oracle, k):
+    # integer rows: many equal distances, so the self-drop's re-ordering of
+    # equal distances by id decides the answer (rows staged 4096 / (k + 1)
+    # per workgroup)
+    x = np.random.default_rng(k).integers(0, 4, (4000, 6)).astype(np.float32)
+    ids, dist = engine.all_neighbors(x, k, "l2")
+    oid, odist = oracle.self_graph(x, k, "l2")
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
