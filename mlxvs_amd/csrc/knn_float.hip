@@ -464,13 +464,18 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 // the segments are those of fused_kernel (2 split + h).
 
 constexpr int kDeepChunk = 32;                 // dims per LDS stage
-constexpr int kDeepStride = kDeepChunk + 4;    // 16-byte pad: 8 rows hit distinct bank quads
 constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
 
 template <int T, bool L2>
 __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
-  __shared__ __align__(16) float tA[2][kDeepRows * kDeepStride];
-  __shared__ __align__(16) float tQ[2][kQueriesPerBlock * kDeepStride];
+  // chunks of the tile's rows and of the block's queries, loaded straight
+  // into LDS (see fused_kernel): rows of 8 vectors without padding, vector c
+  // of row r at slot c ^ (r & 7); separately named buffers, so that loads
+  // into one are not taken to alias reads of the other
+  __shared__ __align__(16) float tA0[kDeepRows * kDeepChunk];
+  __shared__ __align__(16) float tA1[kDeepRows * kDeepChunk];
+  __shared__ __align__(16) float tQ0[kQueriesPerBlock * kDeepChunk];
+  __shared__ __align__(16) float tQ1[kQueriesPerBlock * kDeepChunk];
   __shared__ __align__(16) float tnorm[2][kDeepRows];
 
   const int tid = threadIdx.x;
@@ -507,17 +512,19 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
       (void*)snorm, (short)0, L2 ? nrows * 4 : 0, 0x00020000);
 
-  // Thread's 16-byte vectors of a chunk: e = tid + 256 j -> row e / 8,
-  // vector e % 8, for the base rows and the queries alike.  Offsets of the
-  // next chunk to fetch are carried: +128 bytes per chunk, and at a tile end
-  // the row offsets move on by one tile while the query offsets return to
-  // chunk 0.
+  // Lane l of load instruction j of wavefront w fills LDS vector p = 64 (w
+  // NV + j) + l of a chunk buffer: row p / 8, slot p % 8, so it fetches
+  // vector (p % 8) ^ (row & 7) of that row, for the base rows and the queries
+  // alike.  Offsets of the next chunk to fetch are carried: +128 bytes per
+  // chunk, and at a tile end the row offsets move on by one tile while the
+  // query offsets return to chunk 0.
   constexpr int NV = kDeepRows * (kDeepChunk / 4) / 256;  // 4
   uint32_t aoff[NV], qoff[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int e = tid + 256 * j;
-    const uint32_t o = (uint32_t)(((e >> 3) * ld + 4 * (e & 7)) * 4);
+    const int p = 64 * (wave * NV + j) + lane;
+    const int r = p >> 3, cv = (p & 7) ^ (r & 7);
+    const uint32_t o = (uint32_t)((r * ld + 4 * cv) * 4);
     aoff[j] = o;
     qoff[j] = o;
   }
@@ -525,26 +532,19 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const uint32_t row_wrap = (uint32_t)(kDeepRows * ld * 4) - (uint32_t)(NC * kDeepChunk * 4);
   const uint32_t q_wrap = (uint32_t)(NC * kDeepChunk * 4);
 
-  u32x4 pa[NV], pq[NV];
   uint32_t pn = 0;
   int pc = 0;  // chunk index of the next fetch
-  auto issue_loads = [&]() {
+  auto issue_loads = [&](float* dA, float* dQ) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      pa[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, aoff[j], 0, 0);
-      pq[j] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[j], 0, 0);
+      load16_to_lds(rb, dA + 256 * (wave * NV + j), aoff[j]);
+      load16_to_lds(rq, dQ + 256 * (wave * NV + j), qoff[j]);
     }
     if (L2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   };
-  // stores the fetched chunk (chunk pc of its tile) and advances the offsets
-  auto store_chunk = [&](int buf, int tpar) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int e = tid + 256 * j;
-      const int off = (e >> 3) * kDeepStride + 4 * (e & 7);
-      *(u32x4*)&tA[buf][off] = pa[j];
-      *(u32x4*)&tQ[buf][off] = pq[j];
-    }
+  // stores the fetched chunk's norms (at chunk 0 of a tile) and advances the
+  // offsets
+  auto store_chunk = [&](int tpar) {
     if (L2 && pc == 0 && tid < kDeepRows) tnorm[tpar][tid] = __uint_as_float(pn);
     const bool wrap = ++pc == NC;
 #pragma unroll
@@ -570,8 +570,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const int myslot = share ? (2 * split + h) % a.mslots : 0;
 
   if (nsteps > 0) {
-    issue_loads();
-    store_chunk(0, 0);
+    issue_loads(tA0, tQ0);
+    store_chunk(0);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -583,25 +583,29 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
 
   int c = 0, t = 0;
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
+  // step s: chunk c of tile t from (cA, cQ); the next chunk into (nA, nQ)
+  auto step = [&](const float* cA, const float* cQ, float* nA, float* nQ) {
     // the bound is used at the tile's last chunk: read it in that step only
     SharedBound<S> seen;
     seen.clear();
     if (share && c + 1 == NC) seen.load(gk, a.mslots);
     // the fetched tile's parity, read before store_chunk advances pc
     const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
-    issue_loads();
+    issue_loads(nA, nQ);
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
-      const float* qrow = &tQ[buf][(wave * 32 + col) * kDeepStride + 16 * h];
-      const float* arow = &tA[buf][col * kDeepStride + 16 * h];
+      // lane half h: vectors 4 h .. 4 h + 3 of its rows, at their swizzled
+      // slots (rows col + 32 r share the swizzle of col)
+      const float* qrow = cQ + (wave * 32 + col) * kDeepChunk;
+      const float* arow = cA + col * kDeepChunk;
+      const int sw = col & 7;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const floatx4 bq = *(const floatx4*)(qrow + 4 * v);
+        const int slot = 4 * (((4 * h + v) ^ sw));
+        const floatx4 bq = *(const floatx4*)(qrow + slot);
         floatx4 av[kDeepRB];
 #pragma unroll
-        for (int r = 0; r < kDeepRB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * kDeepStride + 4 * v);
+        for (int r = 0; r < kDeepRB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * kDeepChunk + slot);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -645,12 +649,18 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
-    store_chunk(buf ^ 1, ftpar);
+    store_chunk(ftpar);
+    // this wavefront's loads of the next chunk have landed (the barrier's
+    // fence waits for them), and every wavefront is done with this one
     __syncthreads();
     if (++c == NC) {
       c = 0;
       ++t;
     }
+  };
+  for (int s = 0; s < nsteps; s += 2) {
+    step(tA0, tQ0, tA1, tQ1);
+    if (s + 1 < nsteps) step(tA1, tQ1, tA0, tQ0);
   }
 
   if (qvalid) {
