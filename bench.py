@@ -27,7 +27,7 @@ The same JSON line carries:
   check         the last step's answers for the first 64 queries against the
                 float64 golden fixture (bit-exact, integer-valued data).
 
-Other workloads (c1, c2h, c3, c3cos, c4, c5, ivf) are for measurement runs; the
+Other workloads (c1, c2h, c3, c3cos, c3h, c4, c5, ivf) are for measurement runs; the
 driver's line is the default.  --workload copy times a 1 GiB device copy, the
 reference reading for scaling HBM byte counters.
 """
@@ -78,12 +78,17 @@ def workload(name: str):
         return dict(kind="float", base=base, q=q, k=10, metric="l2",
                     desc="c2: exact L2 kNN k=10, 1M x 128 fp32 base (1024-component "
                          "mixture, int-valued in [0,255]), 10k queries")
-    if name in ("c3", "c3cos"):
+    if name in ("c3", "c3cos", "c3h"):
         cen = synth.c3_centres()
         base = synth.chunked(lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen),
                              1_000_000, chunk=4096)
         q = synth.chunked(lambda lo, hi: synth.c3_rows(2, lo, hi, centres=cen), 10_000,
                           chunk=4096)
+        if name == "c3h":
+            return dict(kind="float", base=base.astype(np.float16), q=q.astype(np.float16),
+                        k=10, metric="inner_product",
+                        desc="c3h: c3's rows stored as fp16 (1M x 1536), inner product k=10, "
+                             "10k queries")
         metric = "cosine" if name == "c3cos" else "inner_product"
         return dict(kind="float", base=base, q=q, k=10, metric=metric,
                     desc=f"c3: exact {metric} kNN k=10, 1M x 1536 unit rows, 10k queries")
@@ -301,8 +306,8 @@ def main() -> int:
 
     sample = args.cpu_sample
     if sample is None:
-        sample = {"c1": 100, "c2": 10000, "c2h": 2000, "c3": 16, "c3cos": 16, "c4": 256,
-                  "c5": 512, "ivf": 10000}[args.workload]
+        sample = {"c1": 100, "c2": 10000, "c2h": 2000, "c3": 16, "c3cos": 16, "c3h": 16,
+                  "c4": 256, "c5": 512, "ivf": 10000}[args.workload]
     cpu = cpu_baseline(w, min(sample, nq)) if sample else None
 
     line = {

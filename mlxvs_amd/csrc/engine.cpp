@@ -481,10 +481,11 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const bool l2 = metric == kern::kL2;
   const bool kf16 = in.f16 && !cosine;
   const int esize = kf16 ? 2 : 4;
-  // fp32 rows longer than the register-resident kernels take go through the
-  // deep kernel, which reads them in 32-dim chunks
-  const bool deep = !kf16 && d > kern::kMaxFusedDimF32;
-  const int vmul = kf16 ? 8 : deep ? 32 : 4;
+  // rows longer than the register-resident kernels take go through the
+  // deep kernel, which reads them in 128-byte chunks (32 fp32 / 64 fp16 dims)
+  const bool deep = d > kern::kMaxFusedDimF32;
+  // row padding: whole 16-byte vectors, or whole 128-byte chunks (deep)
+  const int vmul = deep ? (kf16 ? 64 : 32) : (kf16 ? 8 : 4);
   const void* kbase = in.base;
   const void* kq = in.queries;
   int kld = d;
@@ -533,7 +534,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int T = list_len_float(k);
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
-  const bool use_deep = deep && kern::deep_supported(kld, T, false);
+  const bool use_deep = deep && kern::deep_supported(kld, T, kf16);
   // at most 32 queries (fp32): rows streamed straight into registers
   const bool use_stream = !kf16 && !deep && kern::stream_supported(kld, T, nq);
   // segment lists per split
@@ -543,7 +544,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int tile_rows = use_deep ? kern::kDeepRows : use_stream ? 4 * kern::kTileRows
                                                                : 2 * kern::kTileRows;
   if ((use_deep || kern::fused_supported(kld, T, kf16)) && nq < (int64_t(1) << 31)) {
-    const int bpc = use_deep     ? kern::deep_blocks_per_cu(T)
+    const int bpc = use_deep     ? kern::deep_blocks_per_cu(T, kf16)
                     : use_stream ? kern::stream_blocks_per_cu(kld)
                                  : kern::fused_blocks_per_cu(kld, T, kf16);
     plan = plan_splits(n, qblocks, k, T, lanes, tile_rows, device_slots(bpc), !use_stream,
@@ -599,7 +600,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, bp.m, bp.pubj,
                      (int)qblocks, plan.xcd ? (use_deep ? 2 : 1) : 0};
   if (use_deep)
-    launch(s, "fused_deep", [&] { return kern::launch_deep(fa, s); });
+    launch(s, "fused_deep", [&] { return kern::launch_deep(fa, kf16, s); });
   else if (use_stream)
     launch(s, "stream_f32", [&] { return kern::launch_stream(fa, s); });
   else

@@ -463,19 +463,27 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 // holds rows 32 rb + 8 (i / 4) + 4 h + i % 4: tile position bit 2 is h, so
 // the segments are those of fused_kernel (2 split + h).
 
-constexpr int kDeepChunk = 32;                 // dims per LDS stage
+constexpr int kDeepChunkBytes = 128;           // bytes of a row per LDS stage (8 vectors)
+constexpr int kDeepChunkDwords = kDeepChunkBytes / 4;
 constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
 
-template <int T, bool L2>
+// F16: binary16 rows and queries on v_mfma_f32_32x32x16_f16, 64 dims per
+// stage (the same 128 bytes a row); MFMA step v takes vectors 2 v (lane half
+// 0) and 2 v + 1 (half 1), four steps per stage.  fp32: 32 dims per stage,
+// lane half h takes vectors 4 h .. 4 h + 3, four v_mfma_f32_32x32x2_f32
+// steps per vector.
+template <int T, bool L2, bool F16>
 __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
+  constexpr int esize = F16 ? 2 : 4;
+  constexpr int CH = kDeepChunkBytes / esize;  // dims per stage
   // chunks of the tile's rows and of the block's queries, loaded straight
   // into LDS (see fused_kernel): rows of 8 vectors without padding, vector c
   // of row r at slot c ^ (r & 7); separately named buffers, so that loads
   // into one are not taken to alias reads of the other
-  __shared__ __align__(16) float tA0[kDeepRows * kDeepChunk];
-  __shared__ __align__(16) float tA1[kDeepRows * kDeepChunk];
-  __shared__ __align__(16) float tQ0[kQueriesPerBlock * kDeepChunk];
-  __shared__ __align__(16) float tQ1[kQueriesPerBlock * kDeepChunk];
+  __shared__ __align__(16) uint32_t tA0[kDeepRows * kDeepChunkDwords];
+  __shared__ __align__(16) uint32_t tA1[kDeepRows * kDeepChunkDwords];
+  __shared__ __align__(16) uint32_t tQ0[kQueriesPerBlock * kDeepChunkDwords];
+  __shared__ __align__(16) uint32_t tQ1[kQueriesPerBlock * kDeepChunkDwords];
   __shared__ __align__(16) float tnorm[2][kDeepRows];
 
   const int tid = threadIdx.x;
@@ -491,7 +499,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const bool wave_on = qb0 + wave * 32 < a.nq;
   const bool qvalid = q < a.nq;
   const int ld = a.ld;
-  const int NC = ld / kDeepChunk;
+  const int NC = ld / CH;
 
   const int64_t r0 = (int64_t)split * a.rows_per_split;
   const int64_t r1 = min(a.n, r0 + a.rows_per_split);
@@ -501,13 +509,13 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
 
   // buffer ranges: the split's rows, the block's queries, the split's norms;
   // reads past them return zero
-  const float* sbase = (const float*)a.base + r0 * ld;
+  const char* sbase = (const char*)a.base + r0 * ld * esize;
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)sbase, (short)0, nrows * ld * 4, 0x00020000);
+      (void*)sbase, (short)0, nrows * ld * esize, 0x00020000);
   const int qrows = min(kQueriesPerBlock, a.nq - qb0);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const float*)a.queries + (int64_t)qb0 * ld), (short)0, qrows * ld * 4,
-      0x00020000);
+      (void*)((const char*)a.queries + (int64_t)qb0 * ld * esize), (short)0,
+      qrows * ld * esize, 0x00020000);
   const float* snorm = L2 ? a.bnorm + r0 : (const float*)a.base;
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
       (void*)snorm, (short)0, L2 ? nrows * 4 : 0, 0x00020000);
@@ -518,23 +526,23 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   // alike.  Offsets of the next chunk to fetch are carried: +128 bytes per
   // chunk, and at a tile end the row offsets move on by one tile while the
   // query offsets return to chunk 0.
-  constexpr int NV = kDeepRows * (kDeepChunk / 4) / 256;  // 4
+  constexpr int NV = kDeepRows * (kDeepChunkBytes / 16) / 256;  // 4
   uint32_t aoff[NV], qoff[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int p = 64 * (wave * NV + j) + lane;
     const int r = p >> 3, cv = (p & 7) ^ (r & 7);
-    const uint32_t o = (uint32_t)((r * ld + 4 * cv) * 4);
+    const uint32_t o = (uint32_t)(r * ld * esize + 16 * cv);
     aoff[j] = o;
     qoff[j] = o;
   }
   uint32_t noff = tid < kDeepRows ? tid * 4u : 0x80000000u;
-  const uint32_t row_wrap = (uint32_t)(kDeepRows * ld * 4) - (uint32_t)(NC * kDeepChunk * 4);
-  const uint32_t q_wrap = (uint32_t)(NC * kDeepChunk * 4);
+  const uint32_t row_wrap = (uint32_t)(kDeepRows * ld * esize) - (uint32_t)(NC * kDeepChunkBytes);
+  const uint32_t q_wrap = (uint32_t)(NC * kDeepChunkBytes);
 
   uint32_t pn = 0;
   int pc = 0;  // chunk index of the next fetch
-  auto issue_loads = [&](float* dA, float* dQ) {
+  auto issue_loads = [&](uint32_t* dA, uint32_t* dQ) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       load16_to_lds(rb, dA + 256 * (wave * NV + j), aoff[j]);
@@ -549,8 +557,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     const bool wrap = ++pc == NC;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      aoff[j] += wrap ? row_wrap + kDeepChunk * 4 : kDeepChunk * 4;
-      qoff[j] += wrap ? kDeepChunk * 4 - q_wrap : kDeepChunk * 4;
+      aoff[j] += wrap ? row_wrap + kDeepChunkBytes : kDeepChunkBytes;
+      qoff[j] += wrap ? kDeepChunkBytes - q_wrap : kDeepChunkBytes;
     }
     if (wrap) {
       pc = 0;
@@ -584,7 +592,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
 
   int c = 0, t = 0;
   // step s: chunk c of tile t from (cA, cQ); the next chunk into (nA, nQ)
-  auto step = [&](const float* cA, const float* cQ, float* nA, float* nQ) {
+  auto step = [&](const uint32_t* cA, const uint32_t* cQ, uint32_t* nA, uint32_t* nQ) {
     // the bound is used at the tile's last chunk: read it in that step only
     SharedBound<S> seen;
     seen.clear();
@@ -594,23 +602,34 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     issue_loads(nA, nQ);
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
-      // lane half h: vectors 4 h .. 4 h + 3 of its rows, at their swizzled
-      // slots (rows col + 32 r share the swizzle of col)
-      const float* qrow = cQ + (wave * 32 + col) * kDeepChunk;
-      const float* arow = cA + col * kDeepChunk;
+      // the lane's vectors of its rows at their swizzled slots (rows col +
+      // 32 r share the swizzle of col)
+      const uint32_t* qrow = cQ + (wave * 32 + col) * kDeepChunkDwords;
+      const uint32_t* arow = cA + col * kDeepChunkDwords;
       const int sw = col & 7;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int slot = 4 * (((4 * h + v) ^ sw));
-        const floatx4 bq = *(const floatx4*)(qrow + slot);
-        floatx4 av[kDeepRB];
+        if constexpr (F16) {
+          const int slot = 4 * ((2 * v + h) ^ sw);
+          const halfx8 bq = *(const halfx8*)(qrow + slot);
 #pragma unroll
-        for (int r = 0; r < kDeepRB; ++r) av[r] = *(const floatx4*)(arow + r * 32 * kDeepChunk + slot);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
+          for (int r = 0; r < kDeepRB; ++r) {
+            const halfx8 av = *(const halfx8*)(arow + r * 32 * kDeepChunkDwords + slot);
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq, acc[r], 0, 0, 0);
+          }
+        } else {
+          const int slot = 4 * ((4 * h + v) ^ sw);
+          const floatx4 bq = *(const floatx4*)(qrow + slot);
+          floatx4 av[kDeepRB];
 #pragma unroll
           for (int r = 0; r < kDeepRB; ++r)
-            acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], bq[u], acc[r], 0, 0, 0);
+            av[r] = *(const floatx4*)(arow + r * 32 * kDeepChunkDwords + slot);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < kDeepRB; ++r)
+              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], bq[u], acc[r], 0, 0, 0);
+        }
       }
     }
     if (c + 1 == NC) {
@@ -1317,47 +1336,47 @@ hipError_t dispatch_t(const FusedArgs& a, hipStream_t s) {
 }
 
 template <int T>
-int deep_occupancy() {
+int deep_occupancy(bool f16) {
   int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true>, 256, 0) !=
-      hipSuccess)
-    return 1;
-  return blocks;
+  const hipError_t e =
+      f16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, true>, 256, 0)
+          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, false>, 256, 0);
+  return e == hipSuccess && blocks > 0 ? blocks : 1;
 }
 
-template <int T>
+template <int T, bool F16>
 hipError_t deep_inst(const FusedArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit * a.nqb);
   if (a.metric == kL2)
-    hipLaunchKernelGGL((deep_kernel<T, true>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((deep_kernel<T, true, F16>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((deep_kernel<T, false>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((deep_kernel<T, false, F16>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool deep_supported(int ld, int T, bool f16) {
-  return !f16 && t_ok(T) && ld > kMaxFusedDimF32 && ld % kDeepChunk == 0;
+  return t_ok(T) && ld > kMaxFusedDimF32 && (ld * (f16 ? 2 : 4)) % kDeepChunkBytes == 0;
 }
 
-int deep_blocks_per_cu(int T) {
+int deep_blocks_per_cu(int T, bool f16) {
   switch (T) {
-    case 4: return deep_occupancy<4>();
-    case 8: return deep_occupancy<8>();
-    case 10: return deep_occupancy<10>();
-    case 16: return deep_occupancy<16>();
+    case 4: return deep_occupancy<4>(f16);
+    case 8: return deep_occupancy<8>(f16);
+    case 10: return deep_occupancy<10>(f16);
+    case 16: return deep_occupancy<16>(f16);
   }
   return 1;
 }
 
-hipError_t launch_deep(const FusedArgs& a, hipStream_t s) {
-  if (!deep_supported(a.ld, a.T, false)) return hipErrorInvalidValue;
+hipError_t launch_deep(const FusedArgs& a, bool f16, hipStream_t s) {
+  if (!deep_supported(a.ld, a.T, f16)) return hipErrorInvalidValue;
   switch (a.T) {
-    case 4: return deep_inst<4>(a, s);
-    case 8: return deep_inst<8>(a, s);
-    case 10: return deep_inst<10>(a, s);
-    case 16: return deep_inst<16>(a, s);
+    case 4: return f16 ? deep_inst<4, true>(a, s) : deep_inst<4, false>(a, s);
+    case 8: return f16 ? deep_inst<8, true>(a, s) : deep_inst<8, false>(a, s);
+    case 10: return f16 ? deep_inst<10, true>(a, s) : deep_inst<10, false>(a, s);
+    case 16: return f16 ? deep_inst<16, true>(a, s) : deep_inst<16, false>(a, s);
   }
   return hipErrorInvalidValue;
 }

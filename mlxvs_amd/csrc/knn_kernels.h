@@ -95,13 +95,14 @@ hipError_t launch_stream(const FusedArgs& a, hipStream_t s);
 bool stream_supported(int ld, int T, int64_t nq);
 int stream_blocks_per_cu(int ld);
 
-// Deep rows (fp32, ld > kMaxFusedDimF32, ld a multiple of 32): the same
-// arguments, segments and output as the fused kernels, with kDeepRows rows
-// per tile and a K loop over 32-dim chunks staged in LDS.
+// Deep rows (ld > kMaxFusedDimF32; fp32 with ld a multiple of 32, binary16
+// with ld a multiple of 64): the same arguments, segments and output as the
+// fused kernels, with kDeepRows rows per tile and a K loop over 128-byte
+// chunks of the rows (32 or 64 dims) staged in LDS.
 constexpr int kDeepRows = 128;
-hipError_t launch_deep(const FusedArgs& a, hipStream_t s);
+hipError_t launch_deep(const FusedArgs& a, bool f16, hipStream_t s);
 bool deep_supported(int ld, int T, bool f16);
-int deep_blocks_per_cu(int T);
+int deep_blocks_per_cu(int T, bool f16);
 // The same arguments, segments and output over bit codes (knn_hamming.hip):
 // base / queries packed little-endian words, ld = packed row length in bytes
 // (bits_row_bytes: 16, 32, 64, 128 or 256, zero padded), bnorm the rows'

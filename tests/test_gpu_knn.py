@@ -463,3 +463,29 @@ def test_small_batch_large_k_clustered_ids():
     ids, dist = mlxvs_amd.brute_force_knn(x, np.ones((1, 8), np.float32), 200, "l2")
     want = np.argsort(((x.astype(np.float64) - 1.0) ** 2).sum(1), kind="stable")[:200]
     assert np.array_equal(ids[0], want)
+
+
+# ---- fp16 deep rows (d > 256): the K-looped kernel on the fp16 MFMA ----------------
+
+@pytest.mark.parametrize("d", [288, 300, 512, 768, 1536])
+@pytest.mark.parametrize("k", [10, 16, 64])
+def test_fp16_deep_integer_bit_exact(engine, oracle, d, k):
+    # binary16 integers in [0, 8): exact products and sums, so the answers
+    # equal the restatement's bit for bit (d = 300: zero-padded to 320)
+    rng = np.random.default_rng(d + k)
+    base = rng.integers(0, 8, (20_000, d)).astype(np.float16)
+    q = rng.integers(0, 8, (150, d)).astype(np.float16)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
+
+
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_fp16_deep_float(engine, oracle, metric):
+    b = rows(30_000, 768, 11).astype(np.float16)
+    q = rows(100, 768, 12).astype(np.float16)
+    ids, dist = engine.brute_force_knn(b, q, 10, metric)
+    check_float(oracle, ids, dist, oracle.f16_to_f32(b), oracle.f16_to_f32(q), 10, metric,
+                tol=2e-3)
