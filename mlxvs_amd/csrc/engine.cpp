@@ -557,7 +557,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   }
 
   if (l2 && !(use_stream && plan.ok)) {
-    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
+    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0, 1};
     launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
   }
 
@@ -618,7 +618,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   if (l2 && use_stream) {
     // the streamed scan summed its row norms itself; the exhaustive path
     // reads them
-    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0};
+    kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0, 1};
     launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
   }
   const float *eb, *eq;
@@ -656,10 +656,11 @@ void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint
 }
 
 
-// Int8 MFMA route: the deep fused kernel reads packed codes and unpacks them
-// to {0, 1} bytes, whose squared L2 distance is the Hamming distance (bnorm =
-// popcounts), then the float merge finishes (L2 finalise: qpop - s = the
-// distance, exact).  Returns false when the route does not apply.
+// FP4 MFMA route: the bits kernel reads packed codes and unpacks them to
+// {0, 1} e2m1 values, whose squared L2 distance is the Hamming distance
+// (bnorm = -popcounts / 2), then the float merge finishes (L2 finalise:
+// qpop - s = the distance, exact).  Returns false when the route does not
+// apply.
 bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
                   int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
   Arena& ar = ss.arena();
@@ -696,10 +697,10 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   float* bpop = nullptr;
   if (!use_stream) {
     bpop = ar.take<float>((size_t)n);
-    launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, s); });
+    launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, -0.5f, s); });
   }
   float* qpop = ar.take<float>((size_t)nq);
-  launch(s, "pack", [&] { return kern::launch_popcount_rows(qw, nq, ldw, qpop, s); });
+  launch(s, "pack", [&] { return kern::launch_popcount_rows(qw, nq, ldw, qpop, 1.0f, s); });
 
   const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
@@ -852,7 +853,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   if (l2) {
     bnorm = ar.take<float>((size_t)std::max<int64_t>(n, 1));
     qnorm = ar.take<float>((size_t)nq);
-    kern::PrepArgs pb{kd, n, ld, ld, 0, bnorm, nullptr, nullptr, 0, 0};
+    kern::PrepArgs pb{kd, n, ld, ld, 0, bnorm, nullptr, nullptr, 0, 0, 1};
     kern::PrepArgs pq{kq, nq, ld, ld, 0, qnorm, nullptr, nullptr, 0, 0};
     launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
     launch(s, "prep", [&] { return kern::launch_norms(pq, s); });

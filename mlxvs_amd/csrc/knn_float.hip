@@ -8,6 +8,9 @@
 //
 //  * row_norms / rows_transform: |x|^2 in the summation order of the CPU
 //    restatement (L2, cosine), unit rows (cosine), padded or fp32 copies.
+//    Base rows' norms are stored as -|b|^2 / 2: the L2 kernels select on
+//    half scores q.b - |b|^2 / 2 (twice one is the score 2 q.b - |b|^2),
+//    and the fused kernels start their accumulators there.
 //  * fused_*: one kernel streams 32-row base tiles through LDS and multiplies
 //    them against register-resident query fragments on the MFMA units; the
 //    L2 epilogue and a per-lane top-T list live in registers, so the score
@@ -107,7 +110,8 @@ __global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
   if (row0 + tid < a.n) {
     float s01 = acc[0] + acc[1], s23 = acc[2] + acc[3];
     float s45 = acc[4] + acc[5], s67 = acc[6] + acc[7];
-    a.norm[row0 + tid] = (s01 + s23) + (s45 + s67);
+    const float nn = (s01 + s23) + (s45 + s67);
+    a.norm[row0 + tid] = a.half_neg ? -0.5f * nn : nn;
   }
 }
 
@@ -312,8 +316,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  // the filter: the score of K[T-1] or better (NaN -- every candidate
-  // passes -- while the list has room and nothing better is known)
+  // the filter: the score of K[T-1] or better, for L2 on half scores
+  // (filter_of) (NaN -- every candidate passes -- while the list has room
+  // and nothing better is known)
   // (+inf for a lane without a query: nothing passes, so it never
   // lengthens the wavefront's drain)
   float thr = qvalid ? score_of_key(0u) : INFINITY;
@@ -348,11 +353,18 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     issue_loads(nxt, nnxt);
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
+      // L2: the accumulators start at the rows' -|b|^2 / 2 (the norms array
+      // holds them), so they end at the half score q.b - |b|^2 / 2 with no
+      // epilogue arithmetic: acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
       floatx16 acc[RB];
 #pragma unroll
       for (int r = 0; r < RB; ++r)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          const floatx4 nb = l2 ? *(const floatx4*)&ncur[32 * r + 8 * j + 4 * h] : floatx4{};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[r][4 * j + u] = nb[u];
+        }
       // row col's vectors h QV + v at their swizzled slots (rows col + 32 r
       // share the swizzle)
       const E* arow = cur + col * ROWE;
@@ -386,25 +398,16 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (MODE != 2 && share) thr = fmaxf(thr, score_of_key(seen.bound()));
+      if (MODE != 2 && share) thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
       bool inserted = false;
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        // epilogue: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2;
-        // 2 q.b is exact, so fma(2, q.b, -|b|^2) rounds exactly as that form
+        // scores: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2,
+        // here s / 2 (selected as such: the keys are made from 2 (s / 2),
+        // exact), q.b for inner product
         float sc[16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (L2) {
-            const floatx4 nb = *(const floatx4*)&ncur[32 * r + 8 * j + 4 * h];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-              sc[4 * j + u] = __builtin_fmaf(2.0f, acc[r][4 * j + u], -nb[u]);
-          } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
-          }
-        }
+        for (int i = 0; i < 16; ++i) sc[i] = acc[r][i];
         const uint32_t id0 = idbase + (uint32_t)(t * TR + 32 * r);
         if constexpr (MODE == 2) {
           // the lane's 16 scores: rows 8 j + 4 h + u of the block, columns
@@ -415,11 +418,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-              if (m < lim) dst[m] = sc[i];
+              if (m < lim) dst[m] = l2 ? 2.0f * sc[i] : sc[i];
             }
           }
         } else {
-          inserted |= select_block<T>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
+          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
         }
       }
       if (MODE != 2 && share && qvalid && inserted) {
@@ -635,26 +638,27 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     if (c + 1 == NC) {
       __builtin_amdgcn_sched_barrier(0);
       if (wave_on) {
-        if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
+        if (share) thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
         const int lim0 = nrows - t * kDeepRows;
         const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kDeepRows);
         bool inserted = false;
 #pragma unroll
         for (int r = 0; r < kDeepRB; ++r) {
+          // L2 half scores q.b + (-|b|^2 / 2): twice this rounded sum is
+          // 2 q.b - |b|^2 rounded once (doubling is exact)
           float sc[16];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             if constexpr (L2) {
-              const floatx4 nb = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * j + 4 * h];
+              const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * j + 4 * h];
 #pragma unroll
-              for (int u = 0; u < 4; ++u)
-                sc[4 * j + u] = __builtin_fmaf(2.0f, acc[r][4 * j + u], -nb[u]);
+              for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u] + hn[u];
             } else {
 #pragma unroll
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
             }
           }
-          inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
         }
         if (share && qvalid && inserted) {
           const uint32_t kp = list_key(K, a.pubj);
@@ -1036,7 +1040,7 @@ __global__ __launch_bounds__(256) void scores_kernel(ScoresArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int64_t j = j0 + tx * 4 + v;
       if (j >= a.n) continue;
-      a.S[(int64_t)i * a.n + j] = l2 ? 2.0f * acc[u][v] - a.bnorm[j] : acc[u][v];
+      a.S[(int64_t)i * a.n + j] = l2 ? 2.0f * (acc[u][v] + a.bnorm[j]) : acc[u][v];
     }
   }
 }
@@ -1129,7 +1133,7 @@ __global__ __launch_bounds__(256) void ivf_scores_any_kernel(FusedArgs a) {
       for (int u = 0; u < 4; ++u) acc[u] = __builtin_fmaf(x[u], y[u], acc[u]);
     }
     const float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    const float sc = a.metric == kL2 ? __builtin_fmaf(2.0f, dot, -a.bnorm[r0 + r]) : dot;
+    const float sc = a.metric == kL2 ? 2.0f * (dot + a.bnorm[r0 + r]) : dot;
     a.scores[(int64_t)(q - a.q0) * a.width + a.slots[pair] + r] = sc;
   }
 }

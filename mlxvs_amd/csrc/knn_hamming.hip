@@ -238,10 +238,6 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   __syncthreads();
 
   floatx16 acc[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[r][i] = 0;
 
   int par = 0;  // LDS buffer of the current chunk
   for (int t = 0; t < ntiles; ++t) {
@@ -251,6 +247,19 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
     for (int c = 0; c < NCT; ++c) {
       if (c == 0 && share) seen.load(gk, a.mslots);
       const int buf = (NCT % 2 == 0) ? (c & 1) : par;
+      if (c == 0 && wave_on) {
+        // the accumulators start at the tile's -popcount / 2 (the norms
+        // array holds them) and end at the half score q.b - |b|^2 / 2 of
+        // the {0, 1} vectors: acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * jj + 4 * h];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) acc[r][4 * jj + w] = hn[w];
+          }
+      }
       if (wave_on) {
         const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 4 * h];
         const uint32_t* arow = &tA[buf][col * kBitsStride + 4 * h];
@@ -283,22 +292,18 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       if (j == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
       if (c == NCT - 1) {
         if (wave_on) {
-          if (share) thr = fmaxf(thr, score_of_key(seen.bound()));
-          if (share1) thr = fmaxf(thr, score_of_key(pend));
+          if (share) thr = fmaxf(thr, filter_of<true>(score_of_key(seen.bound())));
+          if (share1) thr = fmaxf(thr, filter_of<true>(score_of_key(pend)));
           const int lim0 = nrows - t * kBitsRows;
           const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kBitsRows);
           bool inserted = false;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
+            // half scores (all integers / 2 below 2^23: exact)
             float sc[16];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              const floatx4 nbv = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * jj + 4 * h];
-#pragma unroll
-              for (int w = 0; w < 4; ++w)
-                sc[4 * jj + w] = __builtin_fmaf(2.0f, (float)acc[r][4 * jj + w], -nbv[w]);
-            }
-            inserted |= select_block<T>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+            for (int i = 0; i < 16; ++i) sc[i] = acc[r][i];
+            inserted |= select_block<T, true>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
           }
           if (share && qvalid && inserted) {
             const uint32_t kp = list_key(K, a.pubj);
@@ -307,10 +312,6 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
                                             __HIP_MEMORY_SCOPE_AGENT);
           }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[r][i] = 0;
       }
       par ^= 1;
       __syncthreads();
@@ -494,10 +495,10 @@ hipError_t bits_dispatch_t(const FusedArgs& a, hipStream_t s) {
 }
 
 // Popcounts of 64 rows per workgroup: one thread per (row, word), summed in
-// LDS.
+// LDS; written times `scale` (1 or -1/2: exact for these integers).
 constexpr int kPopRows = 64;
 __global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* words, int64_t n,
-                                                            int W, float* out) {
+                                                            int W, float* out, float scale) {
   __shared__ int pop[kPopRows];
   const int64_t row0 = (int64_t)blockIdx.x * kPopRows;
   if (threadIdx.x < kPopRows) pop[threadIdx.x] = 0;
@@ -508,14 +509,16 @@ __global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* word
     if (x) atomicAdd(&pop[e / W], __popc(x));
   }
   __syncthreads();
-  if (threadIdx.x < rows) out[row0 + threadIdx.x] = (float)pop[threadIdx.x];
+  if (threadIdx.x < rows) out[row0 + threadIdx.x] = scale * (float)pop[threadIdx.x];
 }
 
 // Popcounts of rows of L 16-byte vectors (L = 1, 2, 4, 8 or 16): one thread
 // per vector (coalesced loads), the row's L threads summed with lane
-// exchanges; a row never straddles a wavefront (L divides 64).
+// exchanges; a row never straddles a wavefront (L divides 64).  Times
+// `scale` as above.
 __global__ __launch_bounds__(256) void popcount_rows16_kernel(const u32x4* __restrict__ v,
-                                                              int64_t n, int L, float* out) {
+                                                              int64_t n, int L, float* out,
+                                                              float scale) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const bool ok = e < n * L;
   uint32_t c = 0;
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(256) void popcount_rows16_kernel(const u32x4* __res
     c = __popc(x[0]) + __popc(x[1]) + __popc(x[2]) + __popc(x[3]);
   }
   for (int o = L >> 1; o > 0; o >>= 1) c += __shfl_xor(c, o);
-  if (ok && (threadIdx.x & (L - 1)) == 0) out[e / L] = (float)c;
+  if (ok && (threadIdx.x & (L - 1)) == 0) out[e / L] = scale * (float)c;
 }
 
 template <int W, int T>
@@ -674,18 +677,18 @@ hipError_t launch_stream_bits(const FusedArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_popcount_rows(const uint32_t* words, int64_t n, int W, float* pop,
-                                hipStream_t s) {
+                                float scale, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const int L = W / 4;
   if (W % 4 == 0 && (L == 1 || L == 2 || L == 4 || L == 8 || L == 16) &&
       (uintptr_t)words % 16 == 0) {
     const int64_t total = n * L;
     hipLaunchKernelGGL(popcount_rows16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
-                       0, s, (const u32x4*)words, n, L, pop);
+                       0, s, (const u32x4*)words, n, L, pop, scale);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(popcount_rows_kernel, dim3((unsigned)((n + kPopRows - 1) / kPopRows)),
-                     dim3(256), 0, s, words, n, W, pop);
+                     dim3(256), 0, s, words, n, W, pop, scale);
   return hipGetLastError();
 }
 

@@ -36,6 +36,8 @@ struct PrepArgs {
   void* out;                // launch_transform: out rows [n, out_ld], zero past d
   int out_ld;
   int out_f16;              // out is binary16 (else fp32)
+  int half_neg;             // launch_norms: write -|x|^2 / 2 (the base-row form the
+                            // scoring kernels read), else |x|^2
 };
 hipError_t launch_norms(const PrepArgs& a, hipStream_t s);
 hipError_t launch_transform(const PrepArgs& a, hipStream_t s);
@@ -50,7 +52,7 @@ struct FusedArgs {
   const void* base;      // [n, ld] fp32 or binary16, 16-byte aligned, ld a multiple
                          // of 4 (fp32) / 8 (fp16); zero past the real dims
   const void* queries;   // [nq, ld]
-  const float* bnorm;    // [n] squared norms (L2), else null
+  const float* bnorm;    // [n] -|b|^2 / 2 of the rows (L2), else null
   int64_t n;
   int nq;
   int ld;
@@ -106,7 +108,7 @@ int deep_blocks_per_cu(int T, bool f16);
 // The same arguments, segments and output over bit codes (knn_hamming.hip):
 // base / queries packed little-endian words, ld = packed row length in bytes
 // (bits_row_bytes: 16, 32, 64, 128 or 256, zero padded), bnorm the rows'
-// popcounts as floats, metric kL2.  The kernel unpacks the bits to e2m1
+// popcounts times -1/2 as floats, metric kL2.  The kernel unpacks the bits to e2m1
 // values 0 / 1.0 in LDS; for {0, 1} vectors the squared L2 distance is the
 // Hamming distance, and every product and sum is exact on the FP4 MFMA
 // (fp32 accumulation of integers below 2^24).
@@ -206,7 +208,7 @@ struct ScoresArgs {
   const float* base;     // [n, d] fp32 (prepared)
   const float* queries;  // [*, d] fp32 (prepared)
   const int* qsel;       // [rows] query index of each scored row
-  const float* bnorm;    // [n] (L2) else null
+  const float* bnorm;    // [n] -|b|^2 / 2 of the rows (L2) else null
   int64_t n;
   int rows;
   int d;
@@ -254,9 +256,10 @@ struct PackArgs {
 };
 hipError_t launch_pack(const PackArgs& a, hipStream_t s);
 
-// Popcounts of packed rows [n, W] as floats.
+// Popcounts of packed rows [n, W] as floats, times scale (1, or -1/2 for
+// the base rows of the bits kernel: -|b|^2 / 2 of the {0, 1} vector).
 hipError_t launch_popcount_rows(const uint32_t* words, int64_t n, int W, float* pop,
-                                hipStream_t s);
+                                float scale, hipStream_t s);
 
 struct HammingArgs {
   const uint32_t* base;    // [n, W]

@@ -112,6 +112,16 @@ __device__ __forceinline__ float pick16(const float (&sc)[16], int i) {
   return b3 ? d1 : d0;
 }
 
+// The filter on half scores (HALF) for a score bound s: a value f <= s / 2
+// (so x >= f for every x with 2 x >= s; filtering is allowed to let more
+// through), s / 2 itself, which is exact, unless |s| < 2^-120, where halving
+// could round; NaN (no bound) stays NaN.  Without HALF, s.
+template <bool HALF>
+__device__ __forceinline__ float filter_of(float s) {
+  if constexpr (HALF) return fabsf(s) < 0x1p-120f ? -0x1p-120f : 0.5f * s;
+  return s;
+}
+
 // Bit i set when row 8 (i / 4) + 4 h + i % 4 of a 32-row block is one of
 // its first lim rows.
 __device__ __forceinline__ uint32_t real_rows(int h, int lim) {
@@ -134,7 +144,11 @@ __device__ __forceinline__ uint32_t real_rows(int h, int lim) {
 // busiest lane needs, and a lane with nothing left inserts the empty key.  A
 // lane's score at its position comes out of a select tree on the position
 // bits (no dynamic register index).  Returns whether the lane kept any.
-template <int T>
+//
+// HALF: sc holds half scores (s / 2; the score 2 q.b - |b|^2 of L2 as q.b -
+// |b|^2 / 2) and thr a filter on them (filter_of): the keys are made from
+// 2 sc, which is exact, so the lists are those of the full scores.
+template <int T, bool HALF = false>
 __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                              const float (&sc)[16], int h, uint32_t id0,
                                              int lim) {
@@ -151,7 +165,7 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
   const bool any = pm != 0;
   while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
     const int i = pm ? __builtin_ctz(pm) : 0;
-    const float x = pick16(sc, i);
+    const float x = HALF ? 2.0f * pick16(sc, i) : pick16(sc, i);
     const int m = 8 * (i >> 2) + 4 * h + (i & 3);
     stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
     pm &= pm - 1u;
@@ -160,7 +174,7 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
   // list's last (an equal key has a larger id and would not enter), so the
   // threshold is the score of the next key up.  NaN while the list has room
   // (K[T-1] = 0: key 1 is a NaN).  Shared bounds stay inclusive.
-  thr = fmaxf(thr, score_of_key(K[T - 1] + 1u));
+  thr = fmaxf(thr, filter_of<HALF>(score_of_key(K[T - 1] + 1u)));
   return any;
 }
 
