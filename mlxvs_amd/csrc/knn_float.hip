@@ -260,23 +260,24 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   constexpr bool l2 = L2;
   const int ntiles = (nrows + TR - 1) / TR;
 
-  // buffer resources over this split's rows and norms
-  const E* sbase = (const E*)a.base + r0 * ld;
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)sbase, (short)0, nrows * ld * (int)sizeof(E), 0x00020000);
+  // this split's rows and norms
+  const char* sbase = (const char*)((const E*)a.base + r0 * ld);
   const float* snorm = l2 ? a.bnorm + r0 : (const float*)a.base;
-  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)snorm, (short)0, l2 ? nrows * 4 : 0, 0x00020000);
   // The tile is fetched straight into LDS (buffer loads with the lds flag:
   // lane l of an instruction writes 16 bytes at the instruction's LDS base +
   // 16 l), one tile ahead, so no register staging and no LDS stores.
   // Instruction j of wavefront w fills LDS vectors [64 g, 64 g + 64), g =
   // w NPF + j: lane l's vector p = 64 g + l is row p / VROW, slot p % VROW,
-  // so it fetches vector slot ^ swz(row) of that row.  Byte offsets are
-  // carried from tile to tile (+tile_bytes); vectors past ld start at 2^31,
-  // beyond every range (ranges are < 2^31 bytes), and read zero, as do rows
-  // past the split.
+  // so it fetches vector slot ^ swz(row) of that row.  The byte offsets are
+  // relative to the tile and fixed; each tile's loads go through buffer
+  // resources built for it (base at the tile, range = the split's bytes
+  // left), scalar work only.  Vectors past ld start at 2^31, beyond every
+  // range (ranges are < 2^31 bytes), and read zero, as do rows past the
+  // split and tiles past the last.
   const uint32_t tile_bytes = TR * ld * (uint32_t)sizeof(E);
+  const uint32_t split_bytes = (uint32_t)nrows * ld * (uint32_t)sizeof(E);
+  // the wavefront index as a scalar (the LDS destinations are per wavefront)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   uint32_t voff[NPF];
 #pragma unroll
   for (int j = 0; j < NPF; ++j) {
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   }
   // norm word of this lane (wavefront 0 loads the tile's norms; lanes past
   // the tile read beyond the range)
-  uint32_t noff = lane < TR ? lane * 4u : 0x80000000u;
+  const uint32_t noff = lane < TR ? lane * 4u : 0x80000000u;
 
   // the lane's query dims [h DH, h DH + DH): 16-byte loads of the query
   // row, zero past ld and for lanes without a query (plain global loads: a
@@ -303,14 +304,23 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     }
   }
 
-  auto issue_loads = [&](E* dst, float* ndst) {
+  // tile t into (dst, ndst)
+  auto issue_loads = [&](E* dst, float* ndst, int t) {
+    // (the saturating difference is a vector operation: readfirstlane keeps
+    // the resource scalar, else the loads would be looped per lane value)
+    const uint32_t done = (uint32_t)t * tile_bytes;
+    const uint32_t left = __builtin_amdgcn_readfirstlane(done < split_bytes ? split_bytes - done : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + done), (short)0, left, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < NPF; ++j) {
-      load16_to_lds(rb, dst + 64 * (wave * NPF + j) * EPV, voff[j]);
-      voff[j] += tile_bytes;
+    for (int j = 0; j < NPF; ++j) load16_to_lds(rb, dst + 64 * (wv * NPF + j) * EPV, voff[j]);
+    if (l2 && wv == 0) {
+      const int r = t * TR;
+      const uint32_t nleft = __builtin_amdgcn_readfirstlane(r < nrows ? (uint32_t)(nrows - r) * 4u : 0u);
+      const __amdgpu_buffer_rsrc_t rn =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(snorm + r), (short)0, nleft, 0x00020000);
+      load4_to_lds(rn, ndst, noff);
     }
-    if (l2 && wave == 0) load4_to_lds(rn, ndst, noff);
-    noff += TR * 4;
   };
 
   uint32_t K[T], I[T];
@@ -330,7 +340,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
   const int myslot = share ? (2 * seg + h) % a.mslots : 0;
 
-  if (ntiles > 0) issue_loads(tile0, tnorm0);
+  if (ntiles > 0) issue_loads(tile0, tnorm0, 0);
   // nothing may be outstanding at the loop head: the query fragments are
   // read in every iteration, and a pending prologue load would otherwise
   // make each iteration wait for its own tile prefetch as well
@@ -349,8 +359,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       if (share && (t & 3) == 0) seen.load(gk, a.mslots);
     // the next tile into the other buffer (read in the previous tile, which
     // every wavefront has left: the barrier below); unconditional (past the
-    // last tile the offsets are out of range and read zero)
-    issue_loads(nxt, nnxt);
+    // last tile the range is empty and the loads write zeros)
+    issue_loads(nxt, nnxt, t + 1);
     __builtin_amdgcn_sched_barrier(0);
     if (wave_on) {
       // L2: the accumulators start at the rows' -|b|^2 / 2 (the norms array
@@ -398,7 +408,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (MODE != 2 && share) thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
+      // the bound changes only where it was read
+      if (MODE != 2 && share && (t & 3) == 0)
+        thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
       bool inserted = false;
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
