@@ -412,6 +412,19 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       if (MODE != 2 && share && (t & 3) == 0)
         thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
       bool inserted = false;
+      // lists of 16 (k > 10, often k > 16: many lanes pass): the two blocks
+      // drain together; for shorter lists the pair's registers cost more
+      // than it saves
+      if constexpr (MODE != 2 && RB == 2 && T == 16) {
+        float sc0[16], sc1[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sc0[i] = acc[0][i];
+          sc1[i] = acc[1][i];
+        }
+        inserted = select_pair<T, L2>(K, I, thr, sc0, sc1, h, idbase + (uint32_t)(t * TR),
+                                      nrows - t * TR);
+      } else
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         // scores: reference src/knn.cpp:114-115, s = 2 q.b - |b|^2 for L2,

@@ -178,6 +178,49 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
   return any;
 }
 
+// select_block over two 32-row blocks at once (rows id0 + 32 b + 8 (i / 4) +
+// 4 h + i % 4 of block b, the first `lim` of the 64 real): one vote for both
+// and one drain over the lane's 32 positions, so a wavefront whose passing
+// candidates sit in different lanes of the two blocks drains them in the
+// same iterations.  Both blocks are filtered against the threshold from
+// before the pair (a candidate it lets through that the list no longer
+// takes falls off the end of the list).
+template <int T, bool HALF = false>
+__device__ __forceinline__ bool select_pair(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                            const float (&sc0)[16], const float (&sc1)[16],
+                                            int h, uint32_t id0, int lim) {
+  float mx0 = fmaxf(fmaxf(sc0[0], sc0[1]), sc0[2]), mx1 = fmaxf(fmaxf(sc1[0], sc1[1]), sc1[2]);
+#pragma unroll
+  for (int i = 3; i < 15; i += 2) {
+    mx0 = fmaxf(fmaxf(mx0, sc0[i]), sc0[i + 1]);
+    mx1 = fmaxf(fmaxf(mx1, sc1[i]), sc1[i + 1]);
+  }
+  const float mx = fmaxf(fmaxf(mx0, sc0[15]), fmaxf(mx1, sc1[15]));
+  if (__builtin_amdgcn_ballot_w64(!(mx < thr)) == 0) return false;
+  uint32_t pm = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pm |= !(sc0[i] < thr) ? (1u << i) : 0u;
+    pm |= !(sc1[i] < thr) ? (1u << (16 + i)) : 0u;
+  }
+  if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
+  const bool any = pm != 0;
+  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+    const int i = pm ? __builtin_ctz(pm) : 0;
+    const bool b = i & 16;
+    float s[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = b ? sc1[e] : sc0[e];
+    const int j = i & 15;
+    const float x = HALF ? 2.0f * pick16(s, j) : pick16(s, j);
+    const int m = (b ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
+    stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
+    pm &= pm - 1u;
+  }
+  thr = fmaxf(thr, filter_of<HALF>(score_of_key(K[T - 1] + 1u)));
+  return any;
+}
+
 // The rank (see rank_of) of a stream-list slot, 0 for an empty one.
 __device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
   return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
