@@ -537,8 +537,11 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const bool use_deep = deep && kern::deep_supported(kld, T, kf16);
   // at most 32 queries (fp32): rows streamed straight into registers
   const bool use_stream = !kf16 && !deep && kern::stream_supported(kld, T, nq);
+  // deep rows, at most 32 queries: the deep kernel's wavefronts split the
+  // row blocks of a tile instead of the queries
+  const bool deep_rs = use_deep && nq <= 32;
   // segment lists per split
-  const int lanes = use_stream ? 8 : 2;
+  const int lanes = (use_stream || deep_rs) ? 8 : 2;
   // split alignment: whole tiles (deep: 128 rows; fused: 32 or 64; stream:
   // a tile for each of the four wavefronts)
   const int tile_rows = use_deep ? kern::kDeepRows : use_stream ? 4 * kern::kTileRows
@@ -591,7 +594,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int nseg = lanes * plan.nsplit;
   uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
   const int slots = kern::bound_slots_for(T);
-  const BoundPlan bp = shared_bound(k, T, slots, nseg);
+  const BoundPlan bp = deep_rs ? BoundPlan{} : shared_bound(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });
   // XCD order: the register-resident kernels share only the row tiles
@@ -600,7 +603,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, bp.m, bp.pubj,
                      (int)qblocks, plan.xcd ? (use_deep ? 2 : 1) : 0};
   if (use_deep)
-    launch(s, "fused_deep", [&] { return kern::launch_deep(fa, kf16, s); });
+    launch(s, "fused_deep", [&] { return kern::launch_deep(fa, kf16, deep_rs, s); });
   else if (use_stream)
     launch(s, "stream_f32", [&] { return kern::launch_stream(fa, s); });
   else

@@ -490,6 +490,13 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 // ld >= 512 it is a few percent of the tile.  Lane (h, col) of row block rb
 // holds rows 32 rb + 8 (i / 4) + 4 h + i % 4: tile position bit 2 is h, so
 // the segments are those of fused_kernel (2 split + h).
+//
+// RS (row split, at most 32 queries): the four wavefronts take the four row
+// blocks of each tile against the same 32 queries, instead of all four
+// blocks against their own 32, so a small batch does a quarter of the MFMA
+// work per row and streams the rows at HBM speed.  Wavefront w's lanes then
+// hold rows 32 w + 8 (i / 4) + 4 h + i % 4: segments 8 split + 2 w + h
+// (part [nq][8 nsplit][T]), no shared bound.
 
 constexpr int kDeepChunkBytes = 128;           // bytes of a row per LDS stage (8 vectors)
 constexpr int kDeepChunkDwords = kDeepChunkBytes / 4;
@@ -500,7 +507,7 @@ constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
 // 0) and 2 v + 1 (half 1), four steps per stage.  fp32: 32 dims per stage,
 // lane half h takes vectors 4 h .. 4 h + 3, four v_mfma_f32_32x32x2_f32
 // steps per vector.
-template <int T, bool L2, bool F16>
+template <int T, bool L2, bool F16, bool RS>
 __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   constexpr int esize = F16 ? 2 : 4;
   constexpr int CH = kDeepChunkBytes / esize;  // dims per stage
@@ -523,9 +530,14 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     tile_of_workgroup(id, a.nsplit, a.nqb, a.xcd_major, split, qb);
   }
   const int qb0 = qb * kQueriesPerBlock;
-  const int q = qb0 + wave * 32 + col;
-  const bool wave_on = qb0 + wave * 32 < a.nq;
+  // the wavefront's queries (its block of 32, or the block's first 32)
+  const int qw = RS ? 0 : wave * 32;
+  const int q = qb0 + qw + col;
+  const bool wave_on = qb0 + qw < a.nq;
   const bool qvalid = q < a.nq;
+  // row blocks of a tile per wavefront, and the first
+  constexpr int NB = RS ? 1 : kDeepRB;
+  const int rb0 = RS ? wave : 0;
   const int ld = a.ld;
   const int NC = ld / CH;
 
@@ -603,7 +615,9 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   constexpr int S = bound_slots<T>();
   const bool share = a.mslots > 0;
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
-  const int myslot = share ? (2 * split + h) % a.mslots : 0;
+  // the lane's segment
+  const int seg = RS ? 8 * split + 2 * wave + h : 2 * split + h;
+  const int myslot = share ? seg % a.mslots : 0;
 
   if (nsteps > 0) {
     issue_loads(tA0, tQ0);
@@ -612,9 +626,9 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  floatx16 acc[kDeepRB];
+  floatx16 acc[NB];
 #pragma unroll
-  for (int r = 0; r < kDeepRB; ++r)
+  for (int r = 0; r < NB; ++r)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
 
@@ -632,8 +646,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     if (wave_on) {
       // the lane's vectors of its rows at their swizzled slots (rows col +
       // 32 r share the swizzle of col)
-      const uint32_t* qrow = cQ + (wave * 32 + col) * kDeepChunkDwords;
-      const uint32_t* arow = cA + col * kDeepChunkDwords;
+      const uint32_t* qrow = cQ + (qw + col) * kDeepChunkDwords;
+      const uint32_t* arow = cA + (32 * rb0 + col) * kDeepChunkDwords;
       const int sw = col & 7;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -641,21 +655,21 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
           const int slot = 4 * ((2 * v + h) ^ sw);
           const halfx8 bq = *(const halfx8*)(qrow + slot);
 #pragma unroll
-          for (int r = 0; r < kDeepRB; ++r) {
+          for (int r = 0; r < NB; ++r) {
             const halfx8 av = *(const halfx8*)(arow + r * 32 * kDeepChunkDwords + slot);
             acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq, acc[r], 0, 0, 0);
           }
         } else {
           const int slot = 4 * ((4 * h + v) ^ sw);
           const floatx4 bq = *(const floatx4*)(qrow + slot);
-          floatx4 av[kDeepRB];
+          floatx4 av[NB];
 #pragma unroll
-          for (int r = 0; r < kDeepRB; ++r)
+          for (int r = 0; r < NB; ++r)
             av[r] = *(const floatx4*)(arow + r * 32 * kDeepChunkDwords + slot);
 #pragma unroll
           for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int r = 0; r < kDeepRB; ++r)
+            for (int r = 0; r < NB; ++r)
               acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], bq[u], acc[r], 0, 0, 0);
         }
       }
@@ -668,14 +682,14 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
         const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kDeepRows);
         bool inserted = false;
 #pragma unroll
-        for (int r = 0; r < kDeepRB; ++r) {
+        for (int r = 0; r < NB; ++r) {
           // L2 half scores q.b + (-|b|^2 / 2): twice this rounded sum is
           // 2 q.b - |b|^2 rounded once (doubling is exact)
           float sc[16];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             if constexpr (L2) {
-              const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * j + 4 * h];
+              const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * (rb0 + r) + 8 * j + 4 * h];
 #pragma unroll
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u] + hn[u];
             } else {
@@ -683,7 +697,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u];
             }
           }
-          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0 + 32 * (rb0 + r),
+                                          lim0 - 32 * (rb0 + r));
         }
         if (share && qvalid && inserted) {
           const uint32_t kp = list_key(K, a.pubj);
@@ -692,7 +707,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
         }
       }
 #pragma unroll
-      for (int r = 0; r < kDeepRB; ++r)
+      for (int r = 0; r < NB; ++r)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.0f;
     }
@@ -712,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   }
 
   if (qvalid) {
-    uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
+    uint64_t* dst = a.part + ((int64_t)q * ((RS ? 8 : 2) * a.nsplit) + seg) * T;
 #pragma unroll
     for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
   }
@@ -1368,19 +1383,27 @@ template <int T>
 int deep_occupancy(bool f16) {
   int blocks = 0;
   const hipError_t e =
-      f16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, true>, 256, 0)
-          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, false>, 256, 0);
+      f16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, true, false>,
+                                                         256, 0)
+          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, deep_kernel<T, true, false, false>,
+                                                         256, 0);
   return e == hipSuccess && blocks > 0 ? blocks : 1;
 }
 
-template <int T, bool F16>
+template <int T, bool F16, bool RS>
 hipError_t deep_inst(const FusedArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit * a.nqb);
   if (a.metric == kL2)
-    hipLaunchKernelGGL((deep_kernel<T, true, F16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((deep_kernel<T, true, F16, RS>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((deep_kernel<T, false, F16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((deep_kernel<T, false, F16, RS>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
+}
+
+template <int T>
+hipError_t deep_t(const FusedArgs& a, bool f16, bool rs, hipStream_t s) {
+  if (f16) return rs ? deep_inst<T, true, true>(a, s) : deep_inst<T, true, false>(a, s);
+  return rs ? deep_inst<T, false, true>(a, s) : deep_inst<T, false, false>(a, s);
 }
 
 }  // namespace
@@ -1399,13 +1422,15 @@ int deep_blocks_per_cu(int T, bool f16) {
   return 1;
 }
 
-hipError_t launch_deep(const FusedArgs& a, bool f16, hipStream_t s) {
+hipError_t launch_deep(const FusedArgs& a, bool f16, bool row_split, hipStream_t s) {
   if (!deep_supported(a.ld, a.T, f16)) return hipErrorInvalidValue;
+  // row split: one block of at most 32 queries, no shared bound
+  if (row_split && (a.nq > 32 || a.nqb != 1 || a.mslots != 0)) return hipErrorInvalidValue;
   switch (a.T) {
-    case 4: return f16 ? deep_inst<4, true>(a, s) : deep_inst<4, false>(a, s);
-    case 8: return f16 ? deep_inst<8, true>(a, s) : deep_inst<8, false>(a, s);
-    case 10: return f16 ? deep_inst<10, true>(a, s) : deep_inst<10, false>(a, s);
-    case 16: return f16 ? deep_inst<16, true>(a, s) : deep_inst<16, false>(a, s);
+    case 4: return deep_t<4>(a, f16, row_split, s);
+    case 8: return deep_t<8>(a, f16, row_split, s);
+    case 10: return deep_t<10>(a, f16, row_split, s);
+    case 16: return deep_t<16>(a, f16, row_split, s);
   }
   return hipErrorInvalidValue;
 }

@@ -102,7 +102,10 @@ int stream_blocks_per_cu(int ld);
 // fused kernels, with kDeepRows rows per tile and a K loop over 128-byte
 // chunks of the rows (32 or 64 dims) staged in LDS.
 constexpr int kDeepRows = 128;
-hipError_t launch_deep(const FusedArgs& a, bool f16, hipStream_t s);
+// row_split: at most 32 queries (nqb 1, mslots 0); the four wavefronts take
+// the four row blocks of each tile, segments 8 split + 2 w + h (part
+// [nq][8 nsplit][T]).
+hipError_t launch_deep(const FusedArgs& a, bool f16, bool row_split, hipStream_t s);
 bool deep_supported(int ld, int T, bool f16);
 int deep_blocks_per_cu(int T, bool f16);
 // The same arguments, segments and output over bit codes (knn_hamming.hip):

@@ -489,3 +489,58 @@ def test_fp16_deep_float(engine, oracle, metric):
     ids, dist = engine.brute_force_knn(b, q, 10, metric)
     check_float(oracle, ids, dist, oracle.f16_to_f32(b), oracle.f16_to_f32(q), 10, metric,
                 tol=2e-3)
+
+
+# ---- deep rows, small batches (<= 32 queries): the row-split deep kernel ------------
+
+@pytest.mark.parametrize("nq", [1, 7, 32])
+@pytest.mark.parametrize("d", [288, 512, 1536])
+@pytest.mark.parametrize("k", [1, 10, 16, 64, 256])
+def test_deep_small_batch_integer_bit_exact(engine, oracle, nq, d, k):
+    # the four wavefronts take a tile's four row blocks against the same
+    # queries (eight lists per split); n leaves a partial last tile
+    rng = np.random.default_rng(nq * 100 + d + k)
+    base = rng.integers(0, 16, (50_001, d)).astype(np.float32)
+    q = rng.integers(0, 16, (nq, d)).astype(np.float32)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(base, q, k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
+
+
+@pytest.mark.parametrize("nq", [1, 32])
+@pytest.mark.parametrize("d", [320, 1536])
+def test_deep_small_batch_fp16_integer_bit_exact(engine, oracle, nq, d):
+    rng = np.random.default_rng(nq + d)
+    base = rng.integers(0, 8, (40_000, d)).astype(np.float16)
+    q = rng.integers(0, 8, (nq, d)).astype(np.float16)
+    for k in (10, 64):
+        ids, dist = engine.brute_force_knn(base, q, k, "l2")
+        oid, odist = oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), k, "l2")
+        assert np.array_equal(ids, oid)
+        assert np.array_equal(dist, odist)
+
+
+@pytest.mark.parametrize("nq", [1, 32])
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_deep_small_batch_float(engine, oracle, nq, metric):
+    base, q = rows(60_000, 768, 41), rows(nq, 768, 42)
+    ids, dist = engine.brute_force_knn(base, q, 10, metric)
+    check_float(oracle, ids, dist, base, q, 10, metric)
+
+
+@pytest.mark.parametrize("n", [1, 31, 127, 128, 129, 1_000])
+def test_deep_small_batch_small_n(engine, oracle, n):
+    base, q = rows(n, 384, 43), rows(3, 384, 44)
+    for k in (1, 10, 64):
+        ids, dist = engine.brute_force_knn(base, q, k, "l2")
+        check_float(oracle, ids, dist, base, q, k, "l2")
+
+
+def test_deep_small_batch_ties_keep_lowest_ids(engine):
+    # every row equal: the k lowest ids, spread over the four row blocks of
+    # the first tile
+    x = np.ones((20_000, 512), np.float32)
+    ids, dist = engine.brute_force_knn(x, np.ones((2, 512), np.float32), 100, "l2")
+    assert (ids == np.arange(100)).all() and (dist == 0).all()
