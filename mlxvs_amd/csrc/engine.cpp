@@ -406,26 +406,35 @@ int max_merge_segments(int k, int T) {
   return kern::kMaxMergeCandidates / g.keep * g.gs;
 }
 
-// Merges the segment lists part [nq][nseg][T] into ids / dists; two levels
-// when one workgroup cannot sort them all.  flags (T < k) as merge_kernel.
+// Merges the segment lists part [nq][nseg][T] into ids / dists.  Up to
+// 1,024 candidates per query: one wavefront per query (merge_wave_kernel).
+// More: levels of group merges, one wavefront per (query, group) of about
+// 1,024 candidates keeping `keep` (the first level groups gs lists of T,
+// later ones 1,024 / keep groups), until a query's groups fit one
+// wavefront; a small batch's thousands of lists thus merge on many CUs in a
+// few short steps instead of one workgroup's sort.  flags (T < k) as
+// merge_kernel, from the sentinels the levels pass on.
 void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T, int k,
                  int64_t nq, int metric, const float* qnorm, int dist_mode, int32_t* ids,
                  float* dists, int* flags) {
   const uint64_t* mpart = part;
   int mseg = nseg, mT = T;
   uint64_t* sentinel = nullptr;
-  if ((int64_t)nseg * T > kern::kMaxMergeCandidates) {
-    const MergeGeometry g = merge_geometry(k, T);
-    const int ngroups = (nseg + g.gs - 1) / g.gs;
-    if ((int64_t)ngroups * g.keep > kern::kMaxMergeCandidates)
-      throw std::runtime_error("mlxvs: merge plan exceeds the merge capacity");
-    uint64_t* part2 = ar.take<uint64_t>((size_t)nq * ngroups * g.keep);
-    if (flags) sentinel = ar.take<uint64_t>((size_t)nq * ngroups);
-    kern::MergeGroupArgs mg{part, nseg, T, (int)nq, g.gs, ngroups, g.keep, part2, sentinel};
+  const MergeGeometry g = merge_geometry(k, T);
+  bool first = true;
+  while ((int64_t)mseg * mT > 1024) {
+    const int gs = first ? g.gs : std::max(2, 1024 / g.keep);
+    const int ngroups = (mseg + gs - 1) / gs;
+    uint64_t* out = ar.take<uint64_t>((size_t)nq * ngroups * g.keep);
+    uint64_t* sent = flags ? ar.take<uint64_t>((size_t)nq * ngroups) : nullptr;
+    kern::MergeGroupArgs mg{mpart, mseg, mT, (int)nq, gs, ngroups, g.keep, out, sent,
+                            first ? nullptr : sentinel};
     launch(s, "merge", [&] { return kern::launch_merge_group(mg, s); });
-    mpart = part2;
+    mpart = out;
     mseg = ngroups;
     mT = g.keep;
+    sentinel = sent;
+    first = false;
   }
   kern::MergeArgs ma{mpart, mseg, mT, k, (int)nq, metric, qnorm, dist_mode, ids, dists, flags,
                      sentinel};

@@ -882,7 +882,8 @@ __global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
     if (threadIdx.x == 0) s_max = 0;
     __syncthreads();
     for (int g2 = threadIdx.x; g2 < s1 - s0; g2 += 256) {
-      const uint64_t last = src[(int64_t)g2 * a.T + a.T - 1];
+      const uint64_t last = a.in_sentinel ? a.in_sentinel[(int64_t)q * a.nseg + s0 + g2]
+                                          : src[(int64_t)g2 * a.T + a.T - 1];
       if (last != 0) atomicMax(&s_max, (unsigned long long)last);
     }
     __syncthreads();
@@ -1004,6 +1005,55 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
         }
       }
     }
+  }
+}
+
+// The largest of the wavefront's values.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)m, o), hi = __shfl_xor((uint32_t)(m >> 32), o);
+    const uint64_t y = ((uint64_t)hi << 32) | lo;
+    m = y > m ? y : m;
+  }
+  return m;
+}
+
+// merge_group_kernel for groups of at most 64 E candidates: one wavefront per
+// (query, group), the ranks sorted in registers (wave_bitonic), no LDS and
+// no barrier; several levels of it reduce the lists of a small batch (many
+// splits) to one wavefront's worth for merge_wave_kernel.
+template <int E>
+__global__ __launch_bounds__(256) void merge_group_wave_kernel(MergeGroupArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)a.nq * a.ngroups) return;  // whole wavefronts: no barrier follows
+  const int q = (int)(w / a.ngroups), g = (int)(w % a.ngroups);
+  const int s0 = g * a.gs, s1 = min(a.nseg, s0 + a.gs);
+  const int C = (s1 - s0) * a.T;
+  const uint64_t* src = a.part + ((int64_t)q * a.nseg + s0) * a.T;
+  uint64_t x[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane * E + e;
+    x[e] = i < C ? src[i] : 0;
+  }
+  if (a.sentinel) {
+    uint64_t m = 0;
+    for (int g2 = lane; g2 < s1 - s0; g2 += 64) {
+      const uint64_t v = a.in_sentinel ? a.in_sentinel[(int64_t)q * a.nseg + s0 + g2]
+                                       : src[(int64_t)g2 * a.T + a.T - 1];
+      m = v > m ? v : m;
+    }
+    m = wave_max_u64(m);
+    if (lane == 0) a.sentinel[(int64_t)q * a.ngroups + g] = m;
+  }
+  wave_bitonic<E>(x, lane, 64 * E, false);
+  uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.keep;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = lane * E + e;
+    if (i < a.keep) dst[i] = x[e];
   }
 }
 
@@ -1557,7 +1607,25 @@ hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s) {
 
 hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.ngroups <= 0) return hipSuccess;
-  if (a.gs * a.T > kMaxMergeCandidates) return hipErrorInvalidValue;
+  const int C = a.gs * a.T;
+  if (C > kMaxMergeCandidates || a.keep > C) return hipErrorInvalidValue;
+  // a wavefront per group when there are enough groups to fill the GPU;
+  // fewer (a small batch) sort faster on a workgroup each
+  const int64_t waves = (int64_t)a.nq * a.ngroups;
+  if (C <= 1024 && waves >= 2048) {
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (C <= 64)
+      hipLaunchKernelGGL(merge_group_wave_kernel<1>, grid, dim3(256), 0, s, a);
+    else if (C <= 128)
+      hipLaunchKernelGGL(merge_group_wave_kernel<2>, grid, dim3(256), 0, s, a);
+    else if (C <= 256)
+      hipLaunchKernelGGL(merge_group_wave_kernel<4>, grid, dim3(256), 0, s, a);
+    else if (C <= 512)
+      hipLaunchKernelGGL(merge_group_wave_kernel<8>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(merge_group_wave_kernel<16>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(merge_group_kernel, dim3(a.nq, a.ngroups), dim3(256), 0, s, a);
   return hipGetLastError();
 }

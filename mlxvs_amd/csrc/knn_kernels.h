@@ -200,6 +200,10 @@ struct MergeGroupArgs {
   int keep;              // ranks kept per group
   uint64_t* out;         // [nq][ngroups][keep]
   uint64_t* sentinel;    // [nq][ngroups] or null (k <= T)
+  // [nq][nseg]: the input lists are a lower level's groups, whose sentinels
+  // pass on (the largest of the group's); null: lists of T from the kernels,
+  // sentinel = the largest last entry of the group's full lists
+  const uint64_t* in_sentinel;
 };
 hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s);
 
