@@ -787,14 +787,17 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
 // through the index's id array.
 
 // (query, probe) pairs grouped by list and cut into items of up to 128 pairs
-// (one workgroup each), for the queries [q0, q1).
+// (one workgroup each), for the queries [q0, q1); items of longer lists
+// first (a workgroup streams its whole list, and the longest ones started
+// last would leave the GPU to them at the end).
 struct IvfItems {
   std::vector<int> items;  // [n][3] list, first pair, pairs
   std::vector<int> pairs;  // q * P + p, grouped by list
   int n = 0;
 };
 
-IvfItems ivf_items(const int* probes, int64_t q0, int64_t q1, int P, int64_t lists) {
+IvfItems ivf_items(const int* probes, int64_t q0, int64_t q1, int P, int64_t lists,
+                   const std::vector<int32_t>& off) {
   IvfItems r;
   std::vector<int64_t> count((size_t)lists + 1, 0);
   for (int64_t q = q0; q < q1; ++q)
@@ -807,9 +810,14 @@ IvfItems ivf_items(const int* probes, int64_t q0, int64_t q1, int P, int64_t lis
       const int l = probes[q * P + p];
       r.pairs[(size_t)next[(size_t)l]++] = (int)(q * P + p);
     }
-  for (int64_t l = 0; l < lists; ++l) {
+  std::vector<int> order((size_t)lists);
+  for (int64_t l = 0; l < lists; ++l) order[(size_t)l] = (int)l;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    return off[(size_t)a + 1] - off[(size_t)a] > off[(size_t)b + 1] - off[(size_t)b];
+  });
+  for (const int l : order) {
     for (int64_t f = count[(size_t)l]; f < count[(size_t)l + 1]; f += kQueriesPerBlock) {
-      r.items.push_back((int)l);
+      r.items.push_back(l);
       r.items.push_back((int)f);
       r.items.push_back((int)std::min<int64_t>(kQueriesPerBlock, count[(size_t)l + 1] - f));
       ++r.n;
@@ -901,7 +909,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   if (k <= T && kern::fused_supported(ld, T, false) &&
       2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
     // fused: per-lane lists over every (query, probe) pair, then the merge
-    const IvfItems it = ivf_items(hp.data(), 0, nq, P, lists);
+    const IvfItems it = ivf_items(hp.data(), 0, nq, P, lists, off);
     int* ditems = to_device(ar, s, it.items);
     int* dpairs = to_device(ar, s, it.pairs);
     const int nseg = 2 * P;
@@ -932,7 +940,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     for (int64_t q0 = 0; q0 < nq; q0 += block) {
       const int64_t q1 = std::min(nq, q0 + block);
       const int cnt = (int)(q1 - q0);
-      const IvfItems it = ivf_items(hp.data(), q0, q1, P, lists);
+      const IvfItems it = ivf_items(hp.data(), q0, q1, P, lists, off);
       int* ditems = to_device(ar, s, it.items);
       int* dpairs = to_device(ar, s, it.pairs);
       launch(s, "prep", [&] { return kern::launch_fill_f32(S, cnt * width, -INFINITY, s); });
