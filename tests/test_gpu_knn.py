@@ -544,3 +544,22 @@ def test_deep_small_batch_ties_keep_lowest_ids(engine):
     x = np.ones((20_000, 512), np.float32)
     ids, dist = engine.brute_force_knn(x, np.ones((2, 512), np.float32), 100, "l2")
     assert (ids == np.arange(100)).all() and (dist == 0).all()
+
+
+# ---- many queries, k > T, heavy ties ---------------------------------------------
+
+@pytest.mark.parametrize("k", [17, 64, 100])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_many_queries_large_k_integer_bit_exact(engine, oracle, k, dtype):
+    # 40,000 queries (313 query blocks) and lists of 16 < k over few rows of
+    # small integers: the shared bounds, the list overflow checks and the
+    # lowest-id tie-break all see many equal scores
+    rng = np.random.default_rng(k + (dtype == np.float16))
+    base = rng.integers(0, 8, (6000, 24)).astype(dtype)
+    q = rng.integers(0, 8, (40_000, 24)).astype(dtype)
+    b32, q32 = base.astype(np.float32), q.astype(np.float32)
+    for metric in ("l2", "inner_product"):
+        ids, dist = engine.brute_force_knn(base, q, k, metric)
+        oid, odist = oracle.knn(b32, q32, k, metric)
+        assert np.array_equal(ids, oid), metric
+        assert np.array_equal(dist, odist), metric
