@@ -138,6 +138,7 @@ __global__ void pack_kernel(PackArgs a) {
 // read a tile later: pending memory events stay reads, and the waits for the
 // refetches keep counting instead of draining.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -148,22 +149,38 @@ constexpr int kBitsRows = kDeepRows;
 // puts the 16 rows a quarter-wavefront reads (16-byte reads) on distinct banks
 constexpr int kBitsStride = 20;
 
-// 128 bits -> 128 e2m1 nibbles of value 0 or 1.0 (code 0x2): dword 4 w + m
-// holds bits 4 j + m of word w in its nibbles j.  Rows and queries use the
+// One code word -> 32 e2m1 nibbles of value 0 or 1.0 (code 0x2): dword m
+// holds bits 4 j + m of the word in its nibbles j.  Rows and queries use the
 // same order, so the dot products are those of the codes.
-__device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t v = x[w];
-    *(u32x4*)(dst + 4 * w) = u32x4{(v << 1) & 0x22222222u, v & 0x22222222u,
-                                   (v >> 1) & 0x22222222u, (v >> 2) & 0x22222222u};
-  }
+__device__ __forceinline__ u32x4 unpack_word(uint32_t v) {
+  return u32x4{(v << 1) & 0x22222222u, v & 0x22222222u, (v >> 1) & 0x22222222u,
+               (v >> 2) & 0x22222222u};
 }
 
+// Two code words at dwords 0 .. 7 of dst.
+__device__ __forceinline__ void unpack_pair(uint32_t* dst, u32x2 x) {
+  *(u32x4*)dst = unpack_word(x[0]);
+  *(u32x4*)(dst + 4) = unpack_word(x[1]);
+}
+
+// A 128-bit chunk (four words) at dwords 0 .. 15 of dst: word w at 4 w.
+__device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) *(u32x4*)(dst + 4 * w) = unpack_word(x[w]);
+}
+
+// QREG (codes of up to 128 bytes): each lane holds its query's B fragments
+// for the whole code, unpacked once (4 registers per word, 64 for 128-byte
+// codes), and all four wavefronts fetch and unpack the tile's rows (thread t:
+// words 2 p, 2 p + 1 of every chunk of row t % 128, p = t / 128).  Longer
+// codes (256 bytes: 128 registers of fragments would spill) keep the
+// queries in LDS too: wavefronts 0-1 fetch and unpack the rows' chunks,
+// 2-3 the queries' (the same chunks again every tile).
 template <int NCT, int T>
 __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
+  constexpr bool QREG = NCT <= 8;
   __shared__ __align__(16) uint32_t tA[2][kBitsRows * kBitsStride];
-  __shared__ __align__(16) uint32_t tQ[2][kQueriesPerBlock * kBitsStride];
+  __shared__ __align__(16) uint32_t tQ[2][QREG ? 4 : kQueriesPerBlock * kBitsStride];
   __shared__ __align__(16) float tnorm[2][kBitsRows];
 
   const int tid = threadIdx.x;
@@ -193,24 +210,50 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.bnorm + r0), (short)0, nrows * 4, 0x00020000);
 
-  const bool row_role = __builtin_amdgcn_readfirstlane(wave) < 2;
-  const int idx = tid & 127;
-  uint32_t* const myA0 = &tA[0][idx * kBitsStride];
-  uint32_t* const myQ0 = &tQ[0][idx * kBitsStride];
-  constexpr int kBuf = kBitsRows * kBitsStride;  // dwords per LDS buffer
+  // QREG: MFMA step v of chunk c takes, in lane half h, code word 4 c + 2 v + h
+  u32x4 qf[QREG ? NCT : 1][2];
+  if constexpr (QREG) {
+    const uint32_t* qr = (const uint32_t*)((const char*)a.queries + (int64_t)(qvalid ? q : 0) * ldb);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) qf[c][v] = unpack_word(qvalid ? qr[4 * c + 2 * v + h] : 0u);
+  }
 
-  // Packed chunks of the thread's row (of the tile being fetched) or query;
-  // out-of-range rows read zero.  Every thread runs the same fetches (query
-  // threads refetch their own, unchanged chunks and a norm they never use),
-  // so the wait counts are the same on every path.
-  u32x4 pk[NCT];
+  // The thread's fetch: QREG, words 2 p .. 2 p + 1 of each chunk of row
+  // idx; otherwise the whole row idx (wavefronts 0-1) or query idx (2-3).
+  // Out-of-range rows read zero.  Every thread also fetches the norm of row
+  // idx (only row threads store it), so the wait counts are the same on
+  // every path.
+  const int idx = tid & 127;
+  const bool row_role = QREG || __builtin_amdgcn_readfirstlane(wave) < 2;
+  const bool stores_norm = QREG ? tid < 128 : row_role;
+  const int part = QREG ? tid >> 7 : 0;
+  uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 8 * part]
+                             : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
+  constexpr int kBuf = kBitsRows * kBitsStride;  // dwords per LDS buffer
+  typedef typename std::conditional<QREG, u32x2, u32x4>::type frag_t;
+  frag_t pk[NCT];
   uint32_t pn = 0;
   const __amdgpu_buffer_rsrc_t rf = row_role ? rb : rq;
-  uint32_t roff = (uint32_t)(idx * ldb);  // the row in the tile being fetched
+  // offset of the thread's fetch in the tile being fetched
+  uint32_t roff = (uint32_t)(idx * ldb + 8 * part);
   const uint32_t rstep = row_role ? (uint32_t)(kBitsRows * ldb) : 0u;
   uint32_t noff = (uint32_t)(idx * 4);
+  auto fetch = [&](int c) {
+    if constexpr (QREG)
+      pk[c] = __builtin_amdgcn_raw_buffer_load_b64(rf, roff + 16 * c, 0, 0);
+    else
+      pk[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * c, 0, 0);
+  };
+  auto unpack = [&](uint32_t* dst, frag_t x) {
+    if constexpr (QREG)
+      unpack_pair(dst, x);
+    else
+      unpack_chunk(dst, x);
+  };
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) pk[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * c, 0, 0);
+  for (int c = 0; c < NCT; ++c) fetch(c);
   pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   roff += rstep;
   noff += kBitsRows * 4;
@@ -231,9 +274,9 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   uint32_t pend = 0;  // slot value returned by the last publish (used a tile later)
 
   // chunk 0 of tile 0, then the refetch of chunk 0 for tile 1
-  unpack_chunk(row_role ? myA0 : myQ0, pk[0]);
-  if (row_role) tnorm[0][idx] = __uint_as_float(pn);
-  pk[0] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff, 0, 0);
+  unpack(my0, pk[0]);
+  if (stores_norm) tnorm[0][idx] = __uint_as_float(pn);
+  fetch(0);
   pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   __syncthreads();
 
@@ -261,11 +304,14 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
           }
       }
       if (wave_on) {
-        const uint32_t* qrow = &tQ[buf][(wave * 32 + col) * kBitsStride + 4 * h];
         const uint32_t* arow = &tA[buf][col * kBitsStride + 4 * h];
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
-          const i32x4 bq4 = *(const i32x4*)(qrow + 8 * v);
+          i32x4 bq4;
+          if constexpr (QREG)
+            bq4 = __builtin_bit_cast(i32x4, qf[c][v]);
+          else
+            bq4 = *(const i32x4*)&tQ[buf][(wave * 32 + col) * kBitsStride + 4 * h + 8 * v];
           const i32x8 bq = {bq4[0], bq4[1], bq4[2], bq4[3], 0, 0, 0, 0};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -279,16 +325,16 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
         }
       }
       // the next chunk (j of this tile, or chunk 0 of the next) into the
-      // other buffer, then the row refetch of chunk j one tile further
+      // other buffer, then the refetch of chunk j one tile further
       const int j = (c + 1) % NCT;
       const int nb = buf ^ 1;
-      unpack_chunk((row_role ? myA0 : myQ0) + nb * kBuf, pk[j]);
-      if (c == NCT - 1 && row_role) tnorm[(t + 1) & 1][idx] = __uint_as_float(pn);
+      unpack(my0 + nb * kBuf, pk[j]);
+      if (c == NCT - 1 && stores_norm) tnorm[(t + 1) & 1][idx] = __uint_as_float(pn);
       if (j == 0) {
         roff += rstep;
         noff += kBitsRows * 4;
       }
-      pk[j] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * j, 0, 0);
+      fetch(j);
       if (j == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
       if (c == NCT - 1) {
         if (wave_on) {
