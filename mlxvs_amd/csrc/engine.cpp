@@ -423,7 +423,13 @@ void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T
   const MergeGeometry g = merge_geometry(k, T);
   bool first = true;
   while ((int64_t)mseg * mT > 1024) {
-    const int gs = first ? g.gs : std::max(2, 1024 / g.keep);
+    // groups of 1,024 candidates, one wavefront each, when they fill the
+    // GPU; else (a small batch) groups of up to 4,096 selected by a
+    // workgroup each, so fewer levels
+    int gs = first ? g.gs : std::max(2, 1024 / g.keep);
+    if (nq * ((mseg + gs - 1) / gs) < 2048)
+      gs = first ? std::max(kern::kMaxMergeCandidates / T, (g.keep + T - 1) / T)
+                 : std::max(2, kern::kMaxMergeCandidates / g.keep);
     const int ngroups = (mseg + gs - 1) / gs;
     uint64_t* out = ar.take<uint64_t>((size_t)nq * ngroups * g.keep);
     uint64_t* sent = flags ? ar.take<uint64_t>((size_t)nq * ngroups) : nullptr;

@@ -866,18 +866,38 @@ __global__ __launch_bounds__(256, DH >= 64 ? 1 : 2) void stream_kernel(FusedArgs
 
 // ---- merge of segment lists ---------------------------------------------------
 
-__global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
+// A group's best `keep` ranks by an MSB-first radix select instead of a sort
+// (the next level sorts nothing it gets from here): one workgroup per
+// (query, group) of up to kMaxMergeCandidates ranks in LDS.  Each pass
+// histograms one 8-bit digit of the ranks that still match the chosen
+// prefix, and wavefront 0 finds the digit of the keep-th largest; the pass
+// loop ends as soon as the ranks matching the prefix are exactly the ones
+// still needed (ranks are distinct, so the keep-th largest is unique).  The
+// kept ranks go out unsorted, zero padded.  With k > T the first level also
+// writes a sentinel per group, the largest last entry among the group's full
+// lists, and later levels pass on the largest of their groups'.
+__global__ __launch_bounds__(256) void select_group_kernel(MergeGroupArgs a) {
   __shared__ uint64_t buf[kMaxMergeCandidates];
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t s_prefix, s_mask;
+  __shared__ int s_need, s_done, s_out;
   const int q = blockIdx.x, g = blockIdx.y;
   const int s0 = g * a.gs, s1 = min(a.nseg, s0 + a.gs);
   const int C = (s1 - s0) * a.T;
-  const int P = pow2_at_least(C > 1 ? C : 1);
   const uint64_t* src = a.part + ((int64_t)q * a.nseg + s0) * a.T;
-  for (int i = threadIdx.x; i < P; i += 256) buf[i] = i < C ? src[i] : 0;
-  __syncthreads();
+  int nz = 0;  // the thread's nonzero ranks
+  for (int i = threadIdx.x; i < C; i += 256) {
+    const uint64_t v = src[i];
+    buf[i] = v;
+    nz += v != 0;
+  }
+  if (threadIdx.x == 0) {
+    s_prefix = 0;
+    s_mask = 0;
+    s_done = 0;
+    s_out = 0;
+  }
   if (a.sentinel) {
-    // the largest last entry of the group's full lists, before the sort
-    // reorders buf (lists are read from src)
     __shared__ unsigned long long s_max;
     if (threadIdx.x == 0) s_max = 0;
     __syncthreads();
@@ -889,9 +909,87 @@ __global__ __launch_bounds__(256) void merge_group_kernel(MergeGroupArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) a.sentinel[(int64_t)q * a.ngroups + g] = s_max;
   }
-  bitonic_desc<256>(buf, P, IdentityOrder{});
-  uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.keep;
-  for (int i = threadIdx.x; i < a.keep; i += 256) dst[i] = i < P ? buf[i] : 0;
+  // the number of nonzero ranks: at most keep of them means all are kept
+  if (threadIdx.x == 0) s_need = 0;
+  __syncthreads();
+  atomicAdd(&s_need, nz);
+  __syncthreads();
+  const int total = s_need;
+  __syncthreads();
+  if (total > a.keep) {
+    if (threadIdx.x == 0) s_need = a.keep;
+    for (int d = 7; d >= 0; --d) {
+      hist[threadIdx.x] = 0;
+      __syncthreads();
+      const uint64_t pre = s_prefix, msk = s_mask;
+      for (int i = threadIdx.x; i < C; i += 256) {
+        const uint64_t v = buf[i];
+        if ((v & msk) == pre) atomicAdd(&hist[(uint32_t)(v >> (8 * d)) & 255u], 1u);
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        // lane l holds digits 255 - 4 l .. 252 - 4 l; counts above them by
+        // a suffix scan over the lanes
+        const int l = threadIdx.x;
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          c[u] = hist[255 - 4 * l - u];
+          sum += c[u];
+        }
+        uint32_t incl = sum;  // counts of digits >= 252 - 4 l
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t y = __shfl_up(incl, o);
+          if (l >= o) incl += y;
+        }
+        const uint32_t above = incl - sum;  // digits > 255 - 4 l
+        const uint32_t need = (uint32_t)s_need;
+        if (above < need && incl >= need) {
+          // the digit is in this lane's four
+          uint32_t acc = above;
+          int dig = 252 - 4 * l;
+          for (int u = 0; u < 4; ++u) {
+            if (acc + c[u] >= need) {
+              dig = 255 - 4 * l - u;
+              break;
+            }
+            acc += c[u];
+          }
+          const uint32_t cnt = hist[dig];
+          s_need = (int)(need - acc);
+          s_prefix = pre | ((uint64_t)dig << (8 * d));
+          s_mask = msk | (255ull << (8 * d));
+          // every rank with this prefix is needed: stop refining
+          s_done = cnt == need - acc ? 1 : 0;
+        }
+      }
+      __syncthreads();
+      if (s_done) break;
+    }
+    // ranks above the prefix bucket, plus the bucket's (all of it when done
+    // early, else exactly the one rank = prefix)
+    const uint64_t pre = s_prefix, msk = s_mask;
+    for (int i = threadIdx.x; i < C; i += 256) {
+      const uint64_t v = buf[i];
+      const bool take = (v & msk) > pre || (v & msk) == pre;
+      if (take && v != 0) {
+        const int o = atomicAdd(&s_out, 1);
+        a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < C; i += 256) {
+      const uint64_t v = buf[i];
+      if (v != 0) {
+        const int o = atomicAdd(&s_out, 1);
+        a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = s_out + threadIdx.x; i < a.keep; i += 256)
+    a.out[((int64_t)q * a.ngroups + g) * a.keep + i] = 0;
 }
 
 // One wavefront per query (four per workgroup) for up to 1,024 candidates:
@@ -1019,7 +1117,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
   return m;
 }
 
-// merge_group_kernel for groups of at most 64 E candidates: one wavefront per
+// The group merge for groups of at most 64 E candidates: one wavefront per
 // (query, group), the ranks sorted in registers (wave_bitonic), no LDS and
 // no barrier; several levels of it reduce the lists of a small batch (many
 // splits) to one wavefront's worth for merge_wave_kernel.
@@ -1610,7 +1708,7 @@ hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s) {
   const int C = a.gs * a.T;
   if (C > kMaxMergeCandidates || a.keep > C) return hipErrorInvalidValue;
   // a wavefront per group when there are enough groups to fill the GPU;
-  // fewer (a small batch) sort faster on a workgroup each
+  // fewer (a small batch), or larger groups, are selected on a workgroup each
   const int64_t waves = (int64_t)a.nq * a.ngroups;
   if (C <= 1024 && waves >= 2048) {
     const dim3 grid((unsigned)((waves + 3) / 4));
@@ -1626,7 +1724,7 @@ hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s) {
       hipLaunchKernelGGL(merge_group_wave_kernel<16>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(merge_group_kernel, dim3(a.nq, a.ngroups), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(select_group_kernel, dim3(a.nq, a.ngroups), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
