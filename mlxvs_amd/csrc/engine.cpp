@@ -400,10 +400,15 @@ MergeGeometry merge_geometry(int k, int T) {
   const int keep = k <= T ? T : k;
   return {keep, std::max(1024 / T, (keep + T - 1) / T)};
 }
-// Segment lists per query the merge takes in two levels.
+// Segment lists per query a split plan may give the merge (which takes any
+// number in levels): as many as three levels of 4,096-rank groups reduce,
+// which lets a small batch with a large k still have a split per
+// workgroup slot.
 int max_merge_segments(int k, int T) {
   const MergeGeometry g = merge_geometry(k, T);
-  return kern::kMaxMergeCandidates / g.keep * g.gs;
+  const int per = std::max(2, kern::kMaxMergeCandidates / g.keep);
+  const int64_t first = std::max(kern::kMaxMergeCandidates / T, (g.keep + T - 1) / T);
+  return (int)std::min<int64_t>(first * per, 1 << 20);
 }
 
 // Merges the segment lists part [nq][nseg][T] into ids / dists.  Up to
