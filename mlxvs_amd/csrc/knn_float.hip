@@ -111,7 +111,9 @@ __global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
     float s01 = acc[0] + acc[1], s23 = acc[2] + acc[3];
     float s45 = acc[4] + acc[5], s67 = acc[6] + acc[7];
     const float nn = (s01 + s23) + (s45 + s67);
-    a.norm[row0 + tid] = a.half_neg ? -0.5f * nn : nn;
+    // (a zero row's -|b|^2 / 2 is +0, not -0: the fused kernels start their
+    // accumulators there, and -0 + (-0) products would leave a -0 score)
+    a.norm[row0 + tid] = a.half_neg ? (nn > 0.0f ? -0.5f * nn : 0.0f) : nn;
   }
 }
 
@@ -1036,6 +1038,17 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, 
   }
 }
 
+// The largest of the wavefront's values.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)m, o), hi = __shfl_xor((uint32_t)(m >> 32), o);
+    const uint64_t y = ((uint64_t)hi << 32) | lo;
+    m = y > m ? y : m;
+  }
+  return m;
+}
+
 template <int E>
 __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
   const int lane = threadIdx.x & 63;
@@ -1049,6 +1062,66 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
   for (int e = 0; e < E; ++e) {
     const int i = lane * E + e;
     x[e] = i < C ? src[i] : 0;
+  }
+  const bool l2 = a.metric == kL2;
+  const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
+  // writes rank r as output slot i (id, distance)
+  auto emit = [&](int i, uint64_t r) {
+    const int64_t o = (int64_t)q * a.k + i;
+    if (r == 0) {
+      a.ids[o] = -1;
+      if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
+    } else {
+      a.ids[o] = id_of_rank(r);
+      const float sv = score_of_key((uint32_t)(r >> 32));
+      if (a.dists) {
+        if (a.dist_mode == 1) {
+          a.dists[o] = -sv;
+        } else if (l2) {
+          const float v = qn - sv;  // reference src/knn.cpp:126-129
+          a.dists[o] = v > 0.0f ? v : 0.0f;
+        } else {
+          a.dists[o] = sv;
+        }
+      }
+    }
+  };
+  if (E >= 4 && a.k <= 16 && !a.flags) {
+    // A few of many (k <= 16, no overflow check): k rounds of the
+    // wavefront's largest rank, each removed from its lane, instead of a
+    // sort of all 64 E; lane i keeps the i-th.
+    uint64_t lmax = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) lmax = x[e] > lmax ? x[e] : lmax;
+    uint64_t best = 0;
+    for (int i = 0; i < a.k; ++i) {
+      const uint64_t m = wave_max_u64(lmax);
+      if (lane == i) best = m;
+      if (m != 0 && lmax == m) {  // the lane that holds it (ranks are distinct)
+        uint64_t nm = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          x[e] = x[e] == m ? 0 : x[e];
+          nm = x[e] > nm ? x[e] : nm;
+        }
+        lmax = nm;
+      }
+    }
+    // output order: the rank order except that -0 and +0 scores tie (then
+    // the id decides); lane i's slot is the number of the k that precede it
+    const bool negz = lane < a.k && best != 0 && (uint32_t)(best >> 32) == 0x7fffffffu;
+    int slot = lane;
+    if (__builtin_amdgcn_ballot_w64(negz) != 0) {
+      const uint64_t mine = output_order(best);
+      slot = 0;
+      for (int j = 0; j < a.k; ++j) {
+        const uint32_t lo = __shfl((uint32_t)best, j), hi = __shfl((uint32_t)(best >> 32), j);
+        const uint64_t other = output_order(((uint64_t)hi << 32) | lo);
+        slot += (j != lane && (other > mine || (other == mine && j < lane))) ? 1 : 0;
+      }
+    }
+    if (lane < a.k) emit(slot, best);
+    return;
   }
   wave_bitonic<E>(x, lane, P, false);
   // the k-th best rank (element k - 1), broadcast
@@ -1077,44 +1150,11 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
     negz |= x[e] != 0 && (uint32_t)(x[e] >> 32) == 0x7fffffffu;
   }
   if (__builtin_amdgcn_ballot_w64(negz) != 0) wave_bitonic<E>(x, lane, P, true);
-  const bool l2 = a.metric == kL2;
-  const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = lane * E + e;
-    if (i < a.k) {
-      const uint64_t r = x[e];
-      const int64_t o = (int64_t)q * a.k + i;
-      if (r == 0) {
-        a.ids[o] = -1;
-        if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
-      } else {
-        a.ids[o] = id_of_rank(r);
-        const float sv = score_of_key((uint32_t)(r >> 32));
-        if (a.dists) {
-          if (a.dist_mode == 1) {
-            a.dists[o] = -sv;
-          } else if (l2) {
-            const float v = qn - sv;  // reference src/knn.cpp:126-129
-            a.dists[o] = v > 0.0f ? v : 0.0f;
-          } else {
-            a.dists[o] = sv;
-          }
-        }
-      }
-    }
+    if (i < a.k) emit(i, x[e]);
   }
-}
-
-// The largest of the wavefront's values.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)m, o), hi = __shfl_xor((uint32_t)(m >> 32), o);
-    const uint64_t y = ((uint64_t)hi << 32) | lo;
-    m = y > m ? y : m;
-  }
-  return m;
 }
 
 // The group merge for groups of at most 64 E candidates: one wavefront per

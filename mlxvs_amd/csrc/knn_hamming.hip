@@ -541,7 +541,8 @@ hipError_t bits_dispatch_t(const FusedArgs& a, hipStream_t s) {
 }
 
 // Popcounts of 64 rows per workgroup: one thread per (row, word), summed in
-// LDS; written times `scale` (1 or -1/2: exact for these integers).
+// LDS; written times `scale` (1 or -1/2: exact for these integers; +0 for
+// an empty row).
 constexpr int kPopRows = 64;
 __global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* words, int64_t n,
                                                             int W, float* out, float scale) {
@@ -555,7 +556,8 @@ __global__ __launch_bounds__(256) void popcount_rows_kernel(const uint32_t* word
     if (x) atomicAdd(&pop[e / W], __popc(x));
   }
   __syncthreads();
-  if (threadIdx.x < rows) out[row0 + threadIdx.x] = scale * (float)pop[threadIdx.x];
+  if (threadIdx.x < rows)
+    out[row0 + threadIdx.x] = pop[threadIdx.x] ? scale * (float)pop[threadIdx.x] : 0.0f;
 }
 
 // Popcounts of rows of L 16-byte vectors (L = 1, 2, 4, 8 or 16): one thread
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(256) void popcount_rows16_kernel(const u32x4* __res
     c = __popc(x[0]) + __popc(x[1]) + __popc(x[2]) + __popc(x[3]);
   }
   for (int o = L >> 1; o > 0; o >>= 1) c += __shfl_xor(c, o);
-  if (ok && (threadIdx.x & (L - 1)) == 0) out[e / L] = scale * (float)c;
+  if (ok && (threadIdx.x & (L - 1)) == 0) out[e / L] = c ? scale * (float)c : 0.0f;
 }
 
 template <int W, int T>

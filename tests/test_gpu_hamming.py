@@ -65,6 +65,21 @@ def test_ties_and_k(engine, oracle, k):
     assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
 
 
+@pytest.mark.parametrize("nq,k", [(1, 10), (64, 16), (64, 17), (3000, 10)])
+def test_zero_codes_keep_sign(engine, oracle, nq, k):
+    # zero rows against zero queries: distance +0 (an empty row's popcount
+    # must not reach the scores as -0), the zero rows in id order
+    rng = np.random.default_rng(nq + k)
+    x = rng.integers(0, 256, (30_000, 16), dtype=np.uint8)
+    x[rng.choice(30_000, 200, replace=False)] = 0
+    q = rng.integers(0, 256, (nq, 16), dtype=np.uint8)
+    q[::2] = 0
+    ids, dist = engine.hamming_knn(x, q, k)
+    oid, odist = oracle.hamming(x, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    assert not np.signbit(dist).any()
+
+
 def test_all_equal_rows(engine):
     x = np.zeros((50_000, 16), np.uint8)
     ids, dist = engine.hamming_knn(x, x[:3], 100)

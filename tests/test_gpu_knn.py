@@ -437,6 +437,27 @@ def test_small_batch_ties_keep_lowest_ids(engine):
     assert (ids == np.arange(16)).all() and (dist == 0).all()
 
 
+@pytest.mark.parametrize("nq", [1, 64, 3000])
+@pytest.mark.parametrize("k", [4, 16, 17])
+@pytest.mark.parametrize("metric", ["l2", "inner_product", "cosine"])
+def test_zero_scores_tie_and_keep_sign(engine, oracle, nq, k, metric):
+    # zero rows (scores of exactly 0 from -0 products too) among rows whose
+    # scores are worse: the best answers are the zero rows in id order, and
+    # zero distances come out as the reference's +0
+    rng = np.random.default_rng(nq + k)
+    base = -rng.integers(1, 4, (40_000, 32)).astype(np.float32)
+    base[rng.choice(40_000, 300, replace=False)] = 0.0
+    base[5::997] = -0.0
+    q = rng.integers(0, 3, (nq, 32)).astype(np.float32)
+    q[::3] = 0.0
+    q[1::7, :8] = -0.0
+    ids, dist = engine.brute_force_knn(base, q, k, metric)
+    oid, odist = oracle.knn(base, q, k, metric)
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(dist, odist)
+    assert np.array_equal(np.signbit(dist), np.signbit(odist))
+
+
 @pytest.mark.parametrize("nq", [1, 5, 32])
 @pytest.mark.parametrize("k", [17, 64, 100, 256])
 def test_small_batch_large_k_bit_exact(engine, oracle, nq, k):
