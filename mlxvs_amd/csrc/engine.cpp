@@ -895,34 +895,32 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   float* pdist = ar.take<float>((size_t)nq * P);
   float_knn(ss, {kc, kq, lists, nq, ld, false}, P,
             metric == kern::kInnerProduct ? kern::kInnerProduct : kern::kL2, probes, pdist);
-  std::vector<int32_t> hp((size_t)nq * P);
-  check_hip(hipMemcpyAsync(hp.data(), probes, sizeof(int32_t) * hp.size(), hipMemcpyDeviceToHost,
-                           s), "hipMemcpyAsync (probes)");
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-
-  // buffer columns of the probes and the buffer width (src/ivf.cpp:179-183)
-  std::vector<int32_t> slots((size_t)nq * P);
-  int64_t width = 1;
-  for (int64_t q = 0; q < nq; ++q) {
-    int64_t c = 0;
-    for (int p = 0; p < P; ++p) {
-      slots[(size_t)(q * P + p)] = (int32_t)c;
-      const int l = hp[(size_t)(q * P + p)];
-      c += off[(size_t)l + 1] - off[(size_t)l];
-    }
-    width = std::max(width, c);
-  }
-  if (width >= (int64_t(1) << 31)) invalid("mlxvs::ivf_flat_search", "too many candidates per query.");
-  int32_t* dslots = to_device(ar, s, slots);
   const kern::Metric km = metric == kern::kCosine ? kern::kInnerProduct : (kern::Metric)metric;
 
   const int T = list_len_float(k);
+  std::vector<int> order;  // host arrays copied from live until the last wait
   if (k <= T && kern::fused_supported(ld, T, false) &&
       2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
-    // fused: per-lane lists over every (query, probe) pair, then the merge
-    const IvfItems it = ivf_items(hp.data(), 0, nq, P, lists, off);
-    int* ditems = to_device(ar, s, it.items);
-    int* dpairs = to_device(ar, s, it.pairs);
+    // fused: per-lane lists over every (query, probe) pair, then the merge.
+    // The work items are planned on the device from the probes (no copy to
+    // the host and no wait), the lists longest first.
+    order.resize((size_t)lists);
+    for (int64_t l = 0; l < lists; ++l) order[(size_t)l] = (int)l;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      return off[(size_t)a + 1] - off[(size_t)a] > off[(size_t)b + 1] - off[(size_t)b];
+    });
+    const int64_t np = nq * P;
+    const int64_t max_items = kern::ivf_plan_max_items(np, lists);
+    if (max_items >= (int64_t(1) << 31) / 3) invalid("mlxvs::ivf_flat_search", "too many probes.");
+    int* dslots = ar.take<int>((size_t)np);
+    int* ditems = ar.take<int>((size_t)(3 * max_items));
+    int* dpairs = ar.take<int>((size_t)np);
+    int* nitems = ar.take<int>(1);
+    int* cnt = ar.take<int>((size_t)lists);
+    int* pos = ar.take<int>((size_t)lists);
+    kern::IvfPlanArgs pa{probes, nq, P, offsets, to_device(ar, s, order), (int)lists, cnt, pos,
+                         dslots, ditems, dpairs, nitems};
+    launch(s, "ivf_plan", [&] { return kern::launch_ivf_plan(pa, s); });
     const int nseg = 2 * P;
     // every (query, probe) pair is in one item, so every segment is written
     uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
@@ -933,7 +931,8 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots_n);
     launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots_n, bp.m, s); });
     kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, bp.m, bp.pubj,
-                       0, 0, ditems, dpairs, offsets, dslots, P, it.n, nullptr, width, 0};
+                       0, 0, ditems, dpairs, offsets, dslots, P, (int)max_items, nullptr, 0, 0,
+                       nitems};
     launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
     kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr, nullptr};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
@@ -941,6 +940,25 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
                         pad};
     launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
   } else {
+    std::vector<int32_t> hp((size_t)nq * P);
+    check_hip(hipMemcpyAsync(hp.data(), probes, sizeof(int32_t) * hp.size(), hipMemcpyDeviceToHost,
+                             s), "hipMemcpyAsync (probes)");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+
+    // buffer columns of the probes and the buffer width (src/ivf.cpp:179-183)
+    std::vector<int32_t> slots((size_t)nq * P);
+    int64_t width = 1;
+    for (int64_t q = 0; q < nq; ++q) {
+      int64_t c = 0;
+      for (int p = 0; p < P; ++p) {
+        slots[(size_t)(q * P + p)] = (int32_t)c;
+        const int l = hp[(size_t)(q * P + p)];
+        c += off[(size_t)l + 1] - off[(size_t)l];
+      }
+      width = std::max(width, c);
+    }
+    if (width >= (int64_t(1) << 31)) invalid("mlxvs::ivf_flat_search", "too many candidates per query.");
+    int32_t* dslots = to_device(ar, s, slots);
     // candidate buffers of blocks of queries, exact radix select
     // (reference src/ivf.cpp:357-409 with the buffers kept near 256 MB)
     const int64_t block = std::max<int64_t>(1, std::min<int64_t>(nq, (int64_t(1) << 26) / width));

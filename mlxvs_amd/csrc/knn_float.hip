@@ -219,6 +219,10 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   __shared__ __align__(16) float tnorm0[64];  // 64: a norm load writes 64 lanes
   __shared__ __align__(16) float tnorm1[64];
 
+  if constexpr (MODE != 0) {
+    // items counted on the device: the grid is an upper bound
+    if (a.n_items_dev && (int)blockIdx.x >= *a.n_items_dev) return;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, col = lane & 31;
@@ -1393,6 +1397,142 @@ __global__ void fill_f32_kernel(float* p, int64_t count, float v) {
   if (i < count) p[i] = v;
 }
 
+// IVF-Flat plan.  Step 1a (a wavefront per query): the query's buffer
+// column of each probe, an exclusive sum of its probes' list sizes.
+__global__ __launch_bounds__(256) void ivf_slots_kernel(IvfPlanArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  int carry = 0;
+  for (int p0 = 0; p0 < a.P; p0 += 64) {
+    const int p = p0 + lane;
+    const int64_t i = q * a.P + p;
+    const int l = p < a.P ? a.probes[i] : -1;
+    const int c = (l >= 0 && l < a.lists) ? a.offsets[l + 1] - a.offsets[l] : 0;
+    int x = c;  // inclusive wavefront scan
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      x += lane >= o ? y : 0;
+    }
+    if (p < a.P) a.slots[i] = carry + x - c;
+    carry += __shfl(x, 63);
+  }
+}
+
+// Pairs per workgroup of the LDS-binned count and fill: a list's global
+// counter then takes one atomic per workgroup (same-address atomics from
+// every workgroup serialise; binning cuts them 8,192-fold).
+constexpr int kPlanChunk = 8192;
+constexpr int kPlanLdsLists = 8192;
+
+// Step 1b: pairs per list, binned in LDS per chunk when the lists fit.
+__global__ __launch_bounds__(256) void ivf_count_kernel(IvfPlanArgs a) {
+  extern __shared__ int h[];  // [lists] when binned
+  const int64_t np = a.nq * a.P;
+  const bool binned = a.lists <= kPlanLdsLists;
+  const int64_t c0 = (int64_t)blockIdx.x * kPlanChunk;
+  const int64_t c1 = min(np, c0 + kPlanChunk);
+  if (binned) {
+    for (int b = threadIdx.x; b < a.lists; b += 256) h[b] = 0;
+    __syncthreads();
+  }
+  for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+    const int l = a.probes[i];
+    if (l < 0 || l >= a.lists) continue;
+    if (binned) atomicAdd(h + l, 1);
+    else atomicAdd(a.cnt + l, 1);
+  }
+  if (binned) {
+    __syncthreads();
+    for (int b = threadIdx.x; b < a.lists; b += 256)
+      if (h[b]) atomicAdd(a.cnt + b, h[b]);
+  }
+}
+
+// Step 2 (one workgroup): exclusive sums over the lists in `order` of their
+// pair counts (each list's first pair) and item counts (each list's first
+// item); a thread writes its list's items.
+__global__ __launch_bounds__(1024) void ivf_scan_kernel(IvfPlanArgs a) {
+  __shared__ int s_c[1024], s_i[1024];
+  __shared__ int carry_c, carry_i;
+  const int tid = threadIdx.x;
+  if (tid == 0) carry_c = carry_i = 0;
+  __syncthreads();
+  for (int r0 = 0; r0 < a.lists; r0 += 1024) {
+    const int r = r0 + tid;
+    const int l = r < a.lists ? a.order[r] : -1;
+    const int c = (l >= 0 && l < a.lists) ? a.cnt[l] : 0;
+    const int ni = (c + kQueriesPerBlock - 1) / kQueriesPerBlock;
+    s_c[tid] = c;
+    s_i[tid] = ni;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {  // inclusive scan
+      const int vc = tid >= o ? s_c[tid - o] : 0, vi = tid >= o ? s_i[tid - o] : 0;
+      __syncthreads();
+      s_c[tid] += vc;
+      s_i[tid] += vi;
+      __syncthreads();
+    }
+    const int start = carry_c + s_c[tid] - c, first = carry_i + s_i[tid] - ni;
+    if (c > 0) {
+      a.pos[l] = start;
+      for (int j = 0; j < ni; ++j) {
+        int* it = a.items + 3 * (int64_t)(first + j);
+        it[0] = l;
+        it[1] = start + j * kQueriesPerBlock;
+        it[2] = min(kQueriesPerBlock, c - j * kQueriesPerBlock);
+      }
+    }
+    __syncthreads();  // every thread has read the carries
+    if (tid == 1023) {
+      carry_c += s_c[1023];
+      carry_i += s_i[1023];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) a.n_items[0] = carry_i;
+}
+
+// Step 3: each pair to the next place of its list; binned, a chunk's pairs
+// take their ranks in LDS and the chunk one range of each list.
+__global__ __launch_bounds__(256) void ivf_fill_kernel(IvfPlanArgs a) {
+  extern __shared__ int h[];  // [2][lists] when binned: counts, then bases
+  const int64_t np = a.nq * a.P;
+  const bool binned = a.lists <= kPlanLdsLists;
+  const int64_t c0 = (int64_t)blockIdx.x * kPlanChunk;
+  const int64_t c1 = min(np, c0 + kPlanChunk);
+  if (!binned) {
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+      const int l = a.probes[i];
+      if (l < 0 || l >= a.lists) continue;
+      a.pairs[atomicAdd(a.pos + l, 1)] = (int)i;
+    }
+    return;
+  }
+  int* base = h + a.lists;
+  for (int b = threadIdx.x; b < a.lists; b += 256) h[b] = 0;
+  __syncthreads();
+  constexpr int PER = kPlanChunk / 256;
+  int rank[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t i = c0 + threadIdx.x + 256 * j;
+    const int l = i < c1 ? a.probes[i] : -1;
+    rank[j] = (l >= 0 && l < a.lists) ? atomicAdd(h + l, 1) : -1;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < a.lists; b += 256)
+    if (h[b]) base[b] = atomicAdd(a.pos + b, h[b]);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (rank[j] < 0) continue;
+    const int64_t i = c0 + threadIdx.x + 256 * j;
+    a.pairs[base[a.probes[i]] + rank[j]] = (int)i;
+  }
+}
+
 __global__ void zero_u32_kernel(uint32_t* p, int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < count) p[i] = 0u;
@@ -1733,6 +1873,25 @@ hipError_t launch_ivf_map(const IvfMapArgs& a, hipStream_t s) {
   const int64_t total = (int64_t)a.rows * a.k;
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(ivf_map_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+int64_t ivf_plan_max_items(int64_t pairs, int64_t lists) {
+  // sum over lists of ceil(c / 128) <= pairs / 128 + (lists with a pair)
+  return (pairs + kQueriesPerBlock - 1) / kQueriesPerBlock + std::min(lists, pairs) + 1;
+}
+
+hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s) {
+  const int64_t np = a.nq * a.P;
+  if (np <= 0 || a.lists <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((a.lists + 255) / 256)), dim3(256), 0, s,
+                     (uint32_t*)a.cnt, (int64_t)a.lists);
+  hipLaunchKernelGGL(ivf_slots_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  const bool binned = a.lists <= kPlanLdsLists;
+  const dim3 chunks((unsigned)((np + kPlanChunk - 1) / kPlanChunk));
+  hipLaunchKernelGGL(ivf_count_kernel, chunks, dim3(256), binned ? 4 * a.lists : 0, s, a);
+  hipLaunchKernelGGL(ivf_scan_kernel, dim3(1), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(ivf_fill_kernel, chunks, dim3(256), binned ? 8 * a.lists : 0, s, a);
   return hipGetLastError();
 }
 

@@ -80,6 +80,9 @@ struct FusedArgs {
   float* scores;         // scores mode: [bq][width] buffers of queries q0 ..
   int64_t width;
   int q0;
+  // when set, the item count is on the device (launch_ivf_plan) and
+  // n_items only bounds it: the workgroups past *n_items_dev return at once
+  const int* n_items_dev;
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
@@ -158,6 +161,30 @@ struct IvfMapArgs {
   float pad;             // distance of a missing neighbour
 };
 hipError_t launch_ivf_map(const IvfMapArgs& a, hipStream_t s);
+
+// The IVF-Flat work items on the device, from the probes (the host bucketing
+// without a round trip): pairs q * P + p grouped by list, the lists in
+// `order` (longest first), each list's pairs cut into items of up to 128;
+// slots[q * P + p] = the buffer column of the probe's first row (the sizes
+// of the query's earlier probes).  Items land in [0, *n_items) of an array
+// of ivf_plan_max_items(nq * P, lists) rows; the pairs' order within a list
+// is unspecified (each pair writes its own segments).
+struct IvfPlanArgs {
+  const int* probes;     // [nq][P], distinct lists per query
+  int64_t nq;
+  int P;
+  const int* offsets;    // [lists + 1]
+  const int* order;      // [lists] list ids, longest first
+  int lists;
+  int* cnt;              // [lists] scratch
+  int* pos;              // [lists] scratch
+  int* slots;            // [nq * P] out
+  int* items;            // [max_items][3] out: list, first pair, pairs
+  int* pairs;            // [nq * P] out
+  int* n_items;          // [1] out
+};
+int64_t ivf_plan_max_items(int64_t pairs, int64_t lists);
+hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s);
 
 // Fill a float array (candidate buffers start at -inf).
 hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s);

@@ -45,6 +45,25 @@ def test_ivf_integer_exact(oracle, metric, d, n_probes, k):
     assert np.array_equal(dist, wd)
 
 
+@pytest.mark.parametrize("lists,n_probes,nq", [(500, 100, 2000), (10_000, 80, 500)])
+def test_ivf_device_plan_many_pairs(oracle, lists, n_probes, nq):
+    # the work items planned on the device: many chunks of (query, probe)
+    # pairs, more than 64 probes per query, and (10,000 lists) more lists
+    # than the LDS bins hold
+    rng = np.random.default_rng(lists)
+    n, d = 30_000, 16
+    lab = rng.integers(0, lists, n)
+    order = np.argsort(lab, kind="stable")
+    x = int_rows(n, d, 5)[order]
+    off = np.concatenate([[0], np.cumsum(np.bincount(lab, minlength=lists))]).astype(np.int32)
+    c = int_rows(lists, d, 6)
+    q = int_rows(nq, d, 7)
+    ids, dist = mlxvs_amd.ivf_flat_search(c, x, order.astype(np.int32), off, "l2", q, 10,
+                                          n_probes=n_probes)
+    wi, wd = oracle.ivf_flat(c, x, order.astype(np.int32), off, q, 10, n_probes, "l2")
+    assert np.array_equal(ids, wi) and np.array_equal(dist, wd)
+
+
 def test_ivf_short_lists_padding(oracle):
     x = int_rows(500, 8, 3)
     c, data, ind, off = ivf_index(x, 50)
