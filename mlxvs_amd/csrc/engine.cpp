@@ -901,6 +901,11 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   std::vector<int> order;  // host arrays copied from live until the last wait
   if (k <= T && kern::fused_supported(ld, T, false) &&
       2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
+    // A small batch has few items (about one per probe): the lists' rows are
+    // then cut into parts of about 128 rows or more, a workgroup each.
+    const int64_t avg_rows = n / std::max<int64_t>(1, lists);
+    const int rs = (int)std::clamp<int64_t>(2048 / std::max<int64_t>(1, nq * P), 1,
+                                            std::clamp<int64_t>(avg_rows / 128, 1, 64));
     // fused: per-lane lists over every (query, probe) pair, then the merge.
     // The work items are planned on the device from the probes (no copy to
     // the host and no wait), the lists longest first.
@@ -921,7 +926,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     kern::IvfPlanArgs pa{probes, nq, P, offsets, to_device(ar, s, order), (int)lists, cnt, pos,
                          dslots, ditems, dpairs, nitems};
     launch(s, "ivf_plan", [&] { return kern::launch_ivf_plan(pa, s); });
-    const int nseg = 2 * P;
+    const int nseg = 2 * P * rs;
     // every (query, probe) pair is in one item, so every segment is written
     uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
     const int slots_n = kern::bound_slots_for(T);
@@ -930,12 +935,11 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     const BoundPlan bp = shared_bound(k, T, 1, nseg);
     uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots_n);
     launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots_n, bp.m, s); });
-    kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, T, k, part, gkey, bp.m, bp.pubj,
+    kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, rs, T, k, part, gkey, bp.m, bp.pubj,
                        0, 0, ditems, dpairs, offsets, dslots, P, (int)max_items, nullptr, 0, 0,
                        nitems};
     launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
-    kern::MergeArgs ma{part, nseg, T, k, (int)nq, metric, qnorm, 0, ids, dists, nullptr, nullptr};
-    launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
+    merge_lists(ar, s, part, nseg, T, k, nq, metric, qnorm, 0, ids, dists, nullptr);
     kern::IvfMapArgs mp{ids, dists, (int)nq, k, nullptr, 0, probes, dslots, offsets, indices, P,
                         pad};
     launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });

@@ -221,7 +221,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
 
   if constexpr (MODE != 0) {
     // items counted on the device: the grid is an upper bound
-    if (a.n_items_dev && (int)blockIdx.x >= *a.n_items_dev) return;
+    const int rs = a.nsplit > 1 ? a.nsplit : 1;
+    if (a.n_items_dev && (int)blockIdx.x / rs >= *a.n_items_dev) return;
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -250,17 +251,24 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     seg = split;
     idbase = (uint32_t)r0;
   } else {
-    const int* it = a.items + 3 * blockIdx.x;
+    // nsplit > 1 (MODE 1): the list's rows cut into nsplit parts, one
+    // workgroup and one segment pair per (item, part)
+    const int rs = a.nsplit > 1 ? a.nsplit : 1;
+    const int item = blockIdx.x / rs, rpart = blockIdx.x % rs;
+    const int* it = a.items + 3 * item;
     const int list = it[0], first = it[1], count = it[2];
-    r0 = a.offsets[list];
-    nrows = a.offsets[list + 1] - (int)r0;
+    const int lsize = a.offsets[list + 1] - a.offsets[list];
+    const int chunk = (lsize + rs - 1) / rs;
+    const int rr0 = min(lsize, rpart * chunk);
+    r0 = a.offsets[list] + rr0;
+    nrows = min(chunk, lsize - rr0);
     const int li = wave * 32 + col;
     wave_on = wave * 32 < count;
     qvalid = li < count;
     const int pair = qvalid ? a.pairs[first + li] : 0;
     q = pair / a.P;
-    seg = pair % a.P;
-    idbase = qvalid ? (uint32_t)a.slots[pair] : 0u;
+    seg = (pair % a.P) * rs + rpart;
+    idbase = qvalid ? (uint32_t)(a.slots[pair] + rr0) : 0u;
   }
   const int ld = a.ld;
   constexpr bool l2 = L2;
@@ -473,7 +481,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   }
 
   if (MODE != 2 && qvalid) {
-    const int nseg = MODE == 0 ? a.nsplit : a.P;
+    const int nseg = MODE == 0 ? a.nsplit : a.P * (a.nsplit > 1 ? a.nsplit : 1);
     uint64_t* dst = a.part + ((int64_t)q * (2 * nseg) + 2 * seg + h) * T;
 #pragma unroll
     for (int i = 0; i < T; ++i) dst[i] = stream_rank(K[i], I[i]);
@@ -1659,7 +1667,8 @@ bool t_ok(int T) { return T == 4 || T == 8 || T == 10 || T == 16; }
 template <int DH, int T>
 hipError_t ivf_inst(const FusedArgs& a, hipStream_t s, int mode) {
   if (a.n_items <= 0) return hipSuccess;
-  const dim3 grid(a.n_items);
+  if (mode == 2 && a.nsplit > 1) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((int64_t)a.n_items * (a.nsplit > 1 ? a.nsplit : 1)));
   if (mode == 1) {
     if (a.metric == kL2)
       hipLaunchKernelGGL((fused_kernel<false, DH, T, true, 1>), grid, dim3(256), 0, s, a);

@@ -58,7 +58,7 @@ struct FusedArgs {
   int ld;
   int metric;            // kInnerProduct / kL2 / kCosine (cosine == IP on unit rows)
   int64_t rows_per_split;
-  int nsplit;
+  int nsplit;            // IVF-Flat MODE 1: row parts per item (<= 1: whole lists)
   int T;                 // list length per lane
   int k;                 // neighbours wanted
   uint64_t* part;        // [nq][2*nsplit][T]

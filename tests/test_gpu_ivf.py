@@ -45,6 +45,20 @@ def test_ivf_integer_exact(oracle, metric, d, n_probes, k):
     assert np.array_equal(dist, wd)
 
 
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("nq", [1, 3, 40])
+@pytest.mark.parametrize("n_probes,k", [(1, 10), (7, 16), (20, 4), (64, 10)])
+def test_ivf_small_batch_row_parts(oracle, metric, nq, n_probes, k):
+    # few (query, probe) pairs: each list's rows are cut into parts scanned by
+    # workgroups of their own (columns offset by the part's first row)
+    x = int_rows(20_000, 32, 11)
+    q = int_rows(nq, 32, 12)
+    c, data, ind, off = ivf_index(x, 64)
+    ids, dist = mlxvs_amd.ivf_flat_search(c, data, ind, off, metric, q, k, n_probes=n_probes)
+    wi, wd = oracle.ivf_flat(c, data, ind, off, q, k, n_probes, metric)
+    assert np.array_equal(ids, wi) and np.array_equal(dist, wd)
+
+
 @pytest.mark.parametrize("lists,n_probes,nq", [(500, 100, 2000), (10_000, 80, 500)])
 def test_ivf_device_plan_many_pairs(oracle, lists, n_probes, nq):
     # the work items planned on the device: many chunks of (query, probe)
