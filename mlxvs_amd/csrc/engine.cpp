@@ -881,12 +881,17 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   }
   float* bnorm = nullptr;
   float* qnorm = nullptr;
+  // -|b|^2 / 2 of the rows (all of them, or with `need` the blocks of the
+  // probed lists), launched once the plan is known
+  auto base_norms = [&](const int* need) {
+    if (!l2) return;
+    kern::PrepArgs pb{kd, n, ld, ld, 0, bnorm, nullptr, nullptr, 0, 0, 1, need};
+    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+  };
   if (l2) {
     bnorm = ar.take<float>((size_t)std::max<int64_t>(n, 1));
     qnorm = ar.take<float>((size_t)nq);
-    kern::PrepArgs pb{kd, n, ld, ld, 0, bnorm, nullptr, nullptr, 0, 0, 1};
     kern::PrepArgs pq{kq, nq, ld, ld, 0, qnorm, nullptr, nullptr, 0, 0};
-    launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
     launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
   }
 
@@ -923,9 +928,13 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     int* nitems = ar.take<int>(1);
     int* cnt = ar.take<int>((size_t)lists);
     int* pos = ar.take<int>((size_t)lists);
+    // a small batch reads few lists: only their rows' norms
+    const int64_t nblk = (n + 255) / 256;
+    int* need = (l2 && np < lists) ? ar.take<int>((size_t)std::max<int64_t>(nblk, 1)) : nullptr;
     kern::IvfPlanArgs pa{probes, nq, P, offsets, to_device(ar, s, order), (int)lists, cnt, pos,
-                         dslots, ditems, dpairs, nitems};
+                         dslots, ditems, dpairs, nitems, need, nblk};
     launch(s, "ivf_plan", [&] { return kern::launch_ivf_plan(pa, s); });
+    base_norms(need);
     const int nseg = 2 * P * rs;
     // every (query, probe) pair is in one item, so every segment is written
     uint64_t* part = ar.take<uint64_t>((size_t)nq * nseg * T);
@@ -944,6 +953,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
                         pad};
     launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
   } else {
+    base_norms(nullptr);
     std::vector<int32_t> hp((size_t)nq * P);
     check_hip(hipMemcpyAsync(hp.data(), probes, sizeof(int32_t) * hp.size(), hipMemcpyDeviceToHost,
                              s), "hipMemcpyAsync (probes)");

@@ -58,6 +58,7 @@ template <bool F16, bool VEC>
 __global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
   constexpr int SS = 36;  // LDS row stride (floats): 16-byte rows, 8 rows hit distinct bank quads
   __shared__ __align__(16) float sh[256 * SS];
+  if (a.need && !a.need[blockIdx.x]) return;
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * 256;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -1484,6 +1485,8 @@ __global__ __launch_bounds__(1024) void ivf_scan_kernel(IvfPlanArgs a) {
     }
     const int start = carry_c + s_c[tid] - c, first = carry_i + s_i[tid] - ni;
     if (c > 0) {
+      if (a.need)  // the list's rows need their norms
+        for (int b = a.offsets[l] / 256; b < (a.offsets[l + 1] + 255) / 256; ++b) a.need[b] = 1;
       a.pos[l] = start;
       for (int j = 0; j < ni; ++j) {
         int* it = a.items + 3 * (int64_t)(first + j);
@@ -1895,6 +1898,9 @@ hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s) {
   if (np <= 0 || a.lists <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((a.lists + 255) / 256)), dim3(256), 0, s,
                      (uint32_t*)a.cnt, (int64_t)a.lists);
+  if (a.need && a.need_n > 0)
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((a.need_n + 255) / 256)), dim3(256), 0, s,
+                       (uint32_t*)a.need, a.need_n);
   hipLaunchKernelGGL(ivf_slots_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
   const bool binned = a.lists <= kPlanLdsLists;
   const dim3 chunks((unsigned)((np + kPlanChunk - 1) / kPlanChunk));

@@ -38,6 +38,8 @@ struct PrepArgs {
   int out_f16;              // out is binary16 (else fp32)
   int half_neg;             // launch_norms: write -|x|^2 / 2 (the base-row form the
                             // scoring kernels read), else |x|^2
+  const int* need;          // launch_norms: if set, only the 256-row blocks b with
+                            // need[b] != 0 are written
 };
 hipError_t launch_norms(const PrepArgs& a, hipStream_t s);
 hipError_t launch_transform(const PrepArgs& a, hipStream_t s);
@@ -182,6 +184,9 @@ struct IvfPlanArgs {
   int* items;            // [max_items][3] out: list, first pair, pairs
   int* pairs;            // [nq * P] out
   int* n_items;          // [1] out
+  int* need;             // [ceil(n / 256)] out (may be null): 1 for the 256-row
+                         // blocks of the probed lists, else 0 (launch_norms' need)
+  int64_t need_n;
 };
 int64_t ivf_plan_max_items(int64_t pairs, int64_t lists);
 hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s);
