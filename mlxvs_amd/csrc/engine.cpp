@@ -908,12 +908,12 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
       2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
     // A small batch has few items (about one per list it probes): the
     // lists' rows are then cut into parts of about 128 rows or more, a
-    // workgroup each, for about 2,048 workgroups.  Items expected: the lists
+    // workgroup each, for about 4,096 workgroups.  Items expected: the lists
     // that np random probes hit, lists (1 - e^(-np / lists)), plus np / 128.
     const int64_t avg_rows = n / std::max<int64_t>(1, lists);
     const double npairs = (double)nq * P;
     const double est = (double)lists * (1.0 - std::exp(-npairs / (double)lists)) + npairs / 128;
-    const int rs = (int)std::clamp<int64_t>((int64_t)(2048.0 / std::max(1.0, est)), 1,
+    const int rs = (int)std::clamp<int64_t>((int64_t)(4096.0 / std::max(1.0, est)), 1,
                                             std::clamp<int64_t>(avg_rows / 128, 1, 64));
     // fused: per-lane lists over every (query, probe) pair, then the merge.
     // The work items are planned on the device from the probes (no copy to
