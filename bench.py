@@ -27,7 +27,7 @@ The same JSON line carries:
   check         the last step's answers for the first 64 queries against the
                 float64 golden fixture (bit-exact, integer-valued data).
 
-Other workloads (c1, c2h, c3, c3cos, c3h, c4, c5, ivf) are for measurement runs; the
+Other workloads (c1, c2h, c3, c3cos, c3h, c4, c5, ivf, topk) are for measurement runs; the
 driver's line is the default.  --workload copy times a 1 GiB device copy, the
 reference reading for scaling HBM byte counters.
 """
@@ -108,6 +108,19 @@ def workload(name: str):
         return dict(kind="ivf", base=base, q=q, k=10, metric="l2", index=index, n_probes=20,
                     desc="ivf: IVF-Flat L2 k=10, c2 rows (1M x 128 fp32), 1024 lists, "
                          "20 probes, 10k queries")
+    if name == "topk":
+        # one merge step of the reference's tile loop as bench/bench_knn.cpp:73-80
+        # times it: the best k of every row of a [block, tile] score matrix,
+        # block = 4,096 queries and tile = 65,536 rows (src/knn.cpp:90-94),
+        # k = 10, first = true; the scores are L2 scores 2 q.b - |b|^2 of
+        # c2-like integer rows (synthetic normal values of that spread)
+        g = np.random.default_rng(5)
+        S = g.standard_normal((4096, 65536), dtype=np.float32)
+        S *= 2.0e5
+        S -= 2.0e6
+        return dict(kind="topk", base=S, q=S[:, :0], k=10, metric="topk",
+                    desc="topk: topk_merge of a 4,096 x 65,536 fp32 score matrix (one tile "
+                         "step of the reference loop), k=10, first=true")
     if name == "c5":
         cen = synth.c5_centres()
         x = synth.chunked(lambda lo, hi: synth.c5_rows(1, lo, hi, centres=cen), 200_000)
@@ -142,7 +155,10 @@ def cpu_baseline(w, sample: int):
     threads = os.cpu_count() or 1
     base, q = w["base"], w["q"][:sample]
     t0 = time.perf_counter()
-    if w["kind"] == "hamming":
+    if w["kind"] == "topk":
+        threads = 1  # the restatement merges rows on one core
+        oracle.topk_merge(base[:sample], None, None, 0, True, w["k"])
+    elif w["kind"] == "hamming":
         oracle.hamming(base, q, w["k"], nthreads=threads)
     elif w["kind"] == "self":
         x = oracle.f16_to_f32(base)
@@ -157,10 +173,14 @@ def cpu_baseline(w, sample: int):
     else:
         oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
     dt = time.perf_counter() - t0
+    if w["kind"] == "topk":
+        what = (f"first {sample} of {base.shape[0]} score rows of {base.shape[1]} scores, "
+                f"{dt:.1f} s")
+    else:
+        what = (f"first {sample} of {w['q'].shape[0]} queries against all {base.shape[0]} "
+                f"rows, {dt:.1f} s")
     return {"value": round(sample / dt, 2), "unit": "queries/s", "cores": threads,
-            "kind": "port",
-            "sample": f"first {sample} of {w['q'].shape[0]} queries against all "
-                      f"{base.shape[0]} rows, {dt:.1f} s"}
+            "kind": "port", "sample": what}
 
 
 def main() -> int:
@@ -202,12 +222,17 @@ def main() -> int:
         db = dix[1]
     else:
         db = _hip.DeviceBuffer.from_array(base)
-    dq = db if w["kind"] == "self" else _hip.DeviceBuffer.from_array(q)
+    if w["kind"] == "topk":
+        nq, n = base.shape  # score rows, scores per row
+    dq = db if w["kind"] in ("self", "topk") else _hip.DeviceBuffer.from_array(q)
     di = _hip.DeviceBuffer(nq * k * 4)
     dd = _hip.DeviceBuffer(nq * k * 4)
 
     def step():
-        if w["kind"] == "float":
+        if w["kind"] == "topk":
+            mlxvs_amd.topk_merge_device(db.value, nq, n, None, None, 0, True, k, di.value,
+                                        dd.value)
+        elif w["kind"] == "float":
             mlxvs_amd.brute_force_knn_device(db.value, n, dq.value, nq, d, k, w["metric"],
                                              di.value, dd.value,
                                              f16=base.dtype == np.float16)
@@ -239,6 +264,14 @@ def main() -> int:
     ids = di.download((nq, k), np.int32)
     dist = dd.download((nq, k), np.float32)
     check = None
+    if w["kind"] == "topk":
+        import oracle
+
+        m = 64
+        oi, os_ = oracle.topk_merge(base[:m], None, None, 0, True, k)
+        ok = np.array_equal(ids[:m], oi) and np.array_equal(dist[:m].view(np.uint32),
+                                                             os_.view(np.uint32))
+        check = f"first {m} rows vs the CPU restatement: {'bit-exact' if ok else 'MISMATCH'}"
     if args.workload in ("c1", "c2", "c2h", "c4"):
         fx = {"c1": "c1_full.npz", "c2": "c2_subset.npz", "c2h": "c2_subset.npz",
               "c4": "c4_subset.npz"}[args.workload]
@@ -255,7 +288,12 @@ def main() -> int:
     kname = max(scan or stages, key=lambda s_: stages[s_][1])
     cnt, tot = stages[kname]
     per = tot / max(cnt, 1) / 1e3  # seconds per launch
-    if w["kind"] == "ivf" and kname == "ivf_scan":
+    if w["kind"] == "topk":
+        # HBM: the score matrix read once, the [rows, k] ids and scores written
+        tbytes = (float(nq) * n * 4 + nq * k * 8) / (cnt / args.steps)
+        roof = {"bound": "hbm", "achieved": round(tbytes / per / 1e9, 1), "peak": PEAK_HBM,
+                "unit": "GB/s"}
+    elif w["kind"] == "ivf" and kname == "ivf_scan":
         # 2 d flops per (query, candidate row) of the probed lists
         c, data, ind, off = w["index"]
         probes = mlxvs_amd.kmeans_predict(q, c, w["n_probes"])
@@ -307,13 +345,15 @@ def main() -> int:
     sample = args.cpu_sample
     if sample is None:
         sample = {"c1": 100, "c2": 10000, "c2h": 2000, "c3": 16, "c3cos": 16, "c3h": 16,
-                  "c4": 256, "c5": 512, "ivf": 10000}[args.workload]
+                  "c4": 256, "c5": 512, "ivf": 10000, "topk": 4096}[args.workload]
     cpu = cpu_baseline(w, min(sample, nq)) if sample else None
+    if cpu and w["kind"] == "topk":
+        cpu["unit"] = "score rows/s"
 
     line = {
         "metric": METRIC if args.workload == "c2" else w["desc"],
         "value": round(nq / (ms_per_step / 1e3), 1),
-        "unit": "queries/s",
+        "unit": "score rows/s" if w["kind"] == "topk" else "queries/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,

@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #define MLXVS_API __attribute__((visibility("default")))
@@ -140,10 +141,32 @@ MLXVS_API void ivf_flat_search_device(const IvfFlatIndexView& index, const float
                                       int64_t nq, int k, int n_probes, int32_t* ids,
                                       float* distances, void* stream = nullptr);
 
+/**
+ * One merge step of brute_force_knn, exposed for tests and benchmarks: the
+ * best k of each row of scores (float32 [nq, t], the id of column c being
+ * id_offset + c) together with the running lists ids / best (int32 /
+ * float32 [nq, k]), which are ignored (and may be null) when first is set.
+ * Returns the merged (ids, scores) [nq, k], best first: float score
+ * descending (-0 and +0 equal), then id ascending; among entries of equal
+ * score the lowest ids are the ones kept; -1 / -inf past min(k, t + (first
+ * ? 0 : k)) entries.  1 <= k <= 256.  Replaces reference
+ * include/mlxvs/mlxvs.h:892-905 (src/knn.cpp:37-69).
+ */
+MLXVS_API std::pair<std::vector<int32_t>, std::vector<float>> topk_merge(
+    const Rows& scores, const int32_t* ids, const float* best, int id_offset, bool first, int k,
+    void* stream = nullptr);
+/** topk_merge on device arrays: scores [nq, t], ids / best [nq, k] (null
+ * when first), out_ids / out_scores [nq, k] (out_scores may be null; the
+ * outputs may be the running arrays themselves).  Enqueues one kernel and
+ * returns; uses no workspace. */
+MLXVS_API void topk_merge_device(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                                 const float* best, int id_offset, bool first, int k,
+                                 int32_t* out_ids, float* out_scores, void* stream = nullptr);
+
 /** Frees the per-device workspace kept between calls. */
 MLXVS_API void release_workspace();
 
-/** "0.16.1-mi355x". */
+/** "0.16.1", the reference version this library replaces. */
 MLXVS_API const char* version();
 
 /** Per-stage kernel timing with HIP events (off by default).  Enabling or

@@ -67,7 +67,8 @@ typedef enum {
  */
 MLXVS_C_API const char* mlxvs_last_error(void);
 
-/** Library version string, "0.16.1-mi355x".  Replaces src/c_api.cpp:194-196. */
+/** Library version string, "0.16.1" (the reference version this library
+ * replaces).  Replaces src/c_api.cpp:194-196. */
 MLXVS_C_API const char* mlxvs_version(void);
 
 /**
@@ -248,6 +249,49 @@ MLXVS_C_API int mlxvs_knn_self_graph_device(
     mlxvs_metric metric,
     int32_t* ids,
     float* distances,
+    void* stream);
+
+/**
+ * One merge step of the exact k-NN: the best k of each row of scores
+ * (float32 [nq, t], row-major; column c has id id_offset + c) together with
+ * the running lists ids (int32 [nq, k]) and best (float32 [nq, k]) unless
+ * first != 0 (then ids and best are not read and may be NULL).  Writes
+ * out_ids / out_scores [nq, k] (out_scores may be NULL), best first: score
+ * descending with -0 equal to +0, then id ascending; among entries of equal
+ * key the lowest (unsigned) ids are kept; -1 / -inf past min(k, t + (first ?
+ * 0 : k)) entries.  1 <= k <= 256.  Extension: exposes mlxvs::topk_merge
+ * (reference include/mlxvs/mlxvs.h:892-905, src/knn.cpp:37-69), which the
+ * reference binds to C++ only.  Host arrays.
+ */
+MLXVS_C_API int mlxvs_topk_merge(
+    const float* scores,
+    int64_t nq,
+    int64_t t,
+    const int32_t* ids,
+    const float* best,
+    int32_t id_offset,
+    int32_t first,
+    int32_t k,
+    int32_t* out_ids,
+    float* out_scores);
+
+/**
+ * mlxvs_topk_merge on device memory, enqueued on stream (a hipStream_t);
+ * returns without waiting.  out_ids / out_scores may be ids / best
+ * themselves (each row's running entries are read before it is written).
+ * Uses no workspace.
+ */
+MLXVS_C_API int mlxvs_topk_merge_device(
+    const float* scores,
+    int64_t nq,
+    int64_t t,
+    const int32_t* ids,
+    const float* best,
+    int32_t id_offset,
+    int32_t first,
+    int32_t k,
+    int32_t* out_ids,
+    float* out_scores,
     void* stream);
 
 /**

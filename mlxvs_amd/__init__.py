@@ -37,6 +37,8 @@ __all__ = [
     "ivf_flat_search",
     "kmeans_predict",
     "library_path",
+    "topk_merge",
+    "topk_merge_device",
 ]
 __version__ = "0.16.1"
 
@@ -73,6 +75,8 @@ def _load():
         "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
+        "mlxvs_topk_merge": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp],
+        "mlxvs_topk_merge_device": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp, vp],
         "mlxvs_release_workspace": [],
         "mlxvs_profile": [ctypes.c_int],
         "mlxvs_profile_report": [ctypes.c_char_p, i64],
@@ -257,6 +261,52 @@ def kmeans_predict(x, centroids, m=1, *, tile_rows=65536, stream=None):
     _check(_L().mlxvs_kmeans_predict(_ptr(xa), xa.shape[0], _ptr(ca), ca.shape[0], xa.shape[1],
                                      f16, m, _ptr(labels)))
     return labels
+
+
+def topk_merge(scores, ids, best, id_offset, first, k, *, stream=None):
+    """One merge step of the exact k-NN: ``(ids int32 [nq, k], scores float32
+    [nq, k])``, the best k of every row of ``scores`` (float32 [nq, t]; the id
+    of column c is ``id_offset + c``) together with the running lists ``ids``
+    / ``best`` ([nq, k]) unless ``first``.
+
+    Best first: score descending (-0.0 equal to +0.0), then id ascending;
+    among equal scores the lowest ids are kept; -1 / -inf past
+    ``min(k, t + (0 if first else k))`` entries.  Mirrors the C++ entry
+    reference include/mlxvs/mlxvs.h:892-905 (src/knn.cpp:37-69), which the
+    reference does not bind to Python.  ``stream`` must be None (host arrays
+    go through the null stream; ``topk_merge_device`` takes a stream).
+    """
+    op = "mlxvs::topk_merge"
+    if stream is not None:
+        raise ValueError(f"[{op}] host arrays run on the null stream; use topk_merge_device "
+                         "for a stream")
+    s = np.asarray(scores)
+    if s.ndim != 2 or s.dtype != np.float32:
+        raise ValueError(f"[{op}] scores must be float32 [nq, t]")
+    s = np.ascontiguousarray(s)
+    k = int(k)
+    nq, t = s.shape
+    first = bool(first)
+    ip = bp = None
+    if not first:
+        pi = np.ascontiguousarray(np.asarray(ids), dtype=np.int32)
+        pb = np.ascontiguousarray(np.asarray(best), dtype=np.float32)
+        if pi.shape != (nq, k) or pb.shape != (nq, k):
+            raise ValueError(f"[{op}] ids and best must be [nq, k] = [{nq}, {k}]")
+        ip, bp = _ptr(pi), _ptr(pb)
+    out_ids = np.empty((nq, max(k, 0)), dtype=np.int32)
+    out_s = np.empty((nq, max(k, 0)), dtype=np.float32)
+    _check(_L().mlxvs_topk_merge(_ptr(s), nq, t, ip, bp, int(id_offset), int(first), k,
+                                 _ptr(out_ids), _ptr(out_s)))
+    return out_ids, out_s
+
+
+def topk_merge_device(scores_ptr, nq, t, ids_ptr, best_ptr, id_offset, first, k, out_ids_ptr,
+                      out_scores_ptr, *, stream=None):
+    """mlxvs_topk_merge_device on device pointers (ints); enqueues only."""
+    _check(_L().mlxvs_topk_merge_device(scores_ptr, nq, t, ids_ptr, best_ptr, int(id_offset),
+                                        int(bool(first)), int(k), out_ids_ptr, out_scores_ptr,
+                                        stream))
 
 
 def brute_force_knn_device(base_ptr, n, queries_ptr, nq, d, k, metric, ids_ptr,

@@ -184,6 +184,30 @@ int mlxvs_knn_self_graph_device(const void* rows, int64_t n, int32_t d, int32_t 
   });
 }
 
+int mlxvs_topk_merge(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                     const float* best, int32_t id_offset, int32_t first, int32_t k,
+                     int32_t* out_ids, float* out_scores) {
+  return guarded([&] {
+    require(nq >= 0 && t >= 0 && t < (1LL << 31), "scores must be float32 [nq, t]");
+    require(out_ids != nullptr || nq == 0, "out_ids must not be NULL.");
+    auto r = mlxvs::topk_merge(mlxvs::Rows{scores, nq, (int32_t)t, mlxvs::Dtype::Float32}, ids,
+                               best, id_offset, first != 0, k);
+    if (!r.first.empty()) std::memcpy(out_ids, r.first.data(), r.first.size() * sizeof(int32_t));
+    if (out_scores && !r.second.empty())
+      std::memcpy(out_scores, r.second.data(), r.second.size() * sizeof(float));
+  });
+}
+
+int mlxvs_topk_merge_device(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                            const float* best, int32_t id_offset, int32_t first, int32_t k,
+                            int32_t* out_ids, float* out_scores, void* stream) {
+  return guarded([&] {
+    require(nq >= 0, "scores must be float32 [nq, t]");
+    mlxvs::topk_merge_device(scores, nq, t, ids, best, id_offset, first != 0, k, out_ids,
+                             out_scores, stream);
+  });
+}
+
 int mlxvs_profile(int enable) {
   return guarded([&] { mlxvs::profile(enable != 0); });
 }

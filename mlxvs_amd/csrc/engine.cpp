@@ -24,6 +24,7 @@
 #include <stdexcept>
 #include <string>
 #include <tuple>
+#include <utility>
 #include <vector>
 
 #include "knn_kernels.h"
@@ -1277,6 +1278,80 @@ void knn_self_graph_device(const Rows& rows, int k, Metric metric, int32_t* ids,
              ids, distances);
 }
 
+// ---- topk_merge (reference src/knn.cpp:37-69) -------------------------------------
+//
+// The reference checks the scores' shape and dtype, then k (src/knn.cpp:
+// 46-54); it reads the running lists without checking them, so here they
+// must only be present unless `first`.
+
+namespace {
+
+void topk_merge_args(const Rows& scores, const void* ids, const void* best, bool first, int k,
+                     const char* op) {
+  if (scores.dtype != Dtype::Float32 || scores.n < 0 || scores.d < 0 ||
+      scores.n >= (int64_t(1) << 31) || (scores.data == nullptr && scores.n * scores.d > 0))
+    invalid(op, "scores must be float32 [nq, t]");
+  if (k < 1 || k > kern::kMaxK) invalid(op, "k must be in [1, 256]");
+  if (!first && scores.n > 0 && (ids == nullptr || best == nullptr))
+    invalid(op, "ids and best [nq, k] must not be NULL unless first.");
+}
+
+void topk_merge_launch(hipStream_t s, const float* scores, int64_t nq, int64_t t,
+                       const int32_t* ids, const float* best, int id_offset, bool first, int k,
+                       int32_t* out_ids, float* out_scores) {
+  kern::TopkMergeArgs ta{scores, nq, t, first ? nullptr : ids, first ? nullptr : best,
+                         id_offset, k, out_ids, out_scores, 0};
+  launch(s, "topk_merge", [&] { return kern::launch_topk_merge(ta, s); });
+}
+
+}  // namespace
+
+std::pair<std::vector<int32_t>, std::vector<float>> topk_merge(const Rows& scores,
+                                                               const int32_t* ids,
+                                                               const float* best, int id_offset,
+                                                               bool first, int k, void* stream) {
+  const char* op = "mlxvs::topk_merge";
+  topk_merge_args(scores, ids, best, first, k, op);
+  const int64_t nq = scores.n, t = scores.d;
+  std::pair<std::vector<int32_t>, std::vector<float>> out;
+  out.first.resize((size_t)(nq * k));
+  out.second.resize((size_t)(nq * k));
+  if (nq == 0) return out;
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const float* ds = (const float*)upload(ar, s, scores);
+  const int32_t* di = nullptr;
+  const float* db = nullptr;
+  if (!first) {
+    di = (const int32_t*)upload(ar, s, Rows{ids, nq, k, Dtype::Float32});
+    db = (const float*)upload(ar, s, Rows{best, nq, k, Dtype::Float32});
+  }
+  int32_t* oi = ar.take<int32_t>((size_t)(nq * k));
+  float* os = ar.take<float>((size_t)(nq * k));
+  topk_merge_launch(s, ds, nq, t, di, db, id_offset, first, k, oi, os);
+  check_hip(hipMemcpyAsync(out.first.data(), oi, sizeof(int32_t) * nq * k, hipMemcpyDeviceToHost,
+                           s), "hipMemcpyAsync (ids)");
+  check_hip(hipMemcpyAsync(out.second.data(), os, sizeof(float) * nq * k, hipMemcpyDeviceToHost,
+                           s), "hipMemcpyAsync (scores)");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return out;
+}
+
+void topk_merge_device(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                       const float* best, int id_offset, bool first, int k, int32_t* out_ids,
+                       float* out_scores, void* stream) {
+  const char* op = "mlxvs::topk_merge";
+  if (t < 0 || t >= (int64_t(1) << 31)) invalid(op, "scores must be float32 [nq, t]");
+  topk_merge_args(Rows{scores, nq, (int32_t)t, Dtype::Float32}, ids, best, first, k, op);
+  if (nq > 0 && out_ids == nullptr) invalid(op, "out_ids must not be NULL.");
+  if (nq == 0) return;
+  (void)current_device();  // "no HIP device" rather than a launch failure
+  // no workspace: the kernel keeps everything in registers and LDS
+  topk_merge_launch((hipStream_t)stream, scores, nq, t, ids, best, id_offset, first, k, out_ids,
+                    out_scores);
+}
+
 void release_workspace() {
   std::lock_guard<std::mutex> lock(g_mutex);
   int dev = current_device();
@@ -1287,7 +1362,7 @@ void release_workspace() {
   }
 }
 
-const char* version() { return "0.16.1-mi355x"; }
+const char* version() { return "0.16.1"; }
 
 void profile(bool enable) {
   std::lock_guard<std::mutex> g(g_prof_mutex);

@@ -334,6 +334,26 @@ hipError_t launch_hamming_scores(const HammingScoresArgs& a, hipStream_t s);
 hipError_t launch_gather_f32(const float* in, const int* sel, int rows, int d,
                              float* out, hipStream_t s);
 
+// mlxvs::topk_merge (topk_merge.hip): the best k of each score row [t]
+// (ids id_offset + column) together with, unless prev_scores is null, the
+// row's k running entries; written best first in the reference's output
+// order, -1 / -inf past the candidates.  One workgroup per row reads the row
+// once.  ids / out_scores may alias prev_ids / prev_scores (a row's running
+// entries are read before its outputs are written).
+struct TopkMergeArgs {
+  const float* scores;      // [nq][t]
+  int64_t nq;
+  int64_t t;
+  const int32_t* prev_ids;  // [nq][k], null when first
+  const float* prev_scores; // [nq][k], null when first
+  int id_offset;
+  int k;                    // 1 .. kMaxK
+  int32_t* ids;             // [nq][k] out
+  float* out_scores;        // [nq][k] out (may be null)
+  int64_t row0;             // first row of a launch (set by the launcher)
+};
+hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s);
+
 // Self-graph post-pass: drop each row's own id from a k+1 list and re-order
 // by distance (src/all_neighbors.cpp:56-95).
 struct SelfDropArgs {

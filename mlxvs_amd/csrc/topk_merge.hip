@@ -1,0 +1,420 @@
+// gfx950 kernel of mlxvs::topk_merge: the best k of every row of a score
+// matrix [nq, t] (ids id_offset + column), together with a running list of
+// k (id, score) pairs unless `first`, best first.
+//
+// Reference: src/knn.cpp:37-69 launches src/kernels.h:37-229, one Metal
+// threadgroup per row that reads the row 8-9 times (four 8-bit radix passes
+// over the keys, up to four over the ids of the tied entries, a gather) and
+// sorts the winners with a bitonic network.  Semantics kept:
+//   * candidates: the t scores (id id_offset + column) and, unless first,
+//     the k running entries; keff = min(k, candidates);
+//   * kept: every entry whose order-preserving key (topk_common.h key_of)
+//     is above the keff-th largest key, and of the entries equal to it the
+//     ones of lowest unsigned id;
+//   * output: the keff kept entries by float score descending (-0 == +0),
+//     then unsigned id ascending; slots keff .. k - 1 are -1 / -inf.
+// Both selection rules at once are "largest 64-bit rank" (rank_of: key in
+// the high word, ~id in the low word), so one selection over ranks is the
+// reference's two.
+//
+// Here one workgroup per row reads the row once from HBM, in chunks of
+// NT * PER scores held in registers, and keeps the running best (at most k
+// ranks, unsorted) in LDS from chunk to chunk.  Per chunk:
+//   1. a lower bound L on the k-th best key: every thread's largest key,
+//      each wavefront's j-th largest of its 64 maxima (a bitonic network over
+//      lane shuffles), j = ceil(k / wavefronts), and the smallest of those:
+//      the wavefronts' top-j maxima are wavefronts * j >= k distinct
+//      elements at or above it.  Once the running list holds k, its
+//      selection threshold bounds too (k entries at or above it).
+//   2. the elements with key >= L -- typically k and a few more -- and the
+//      running entries at or above L go to a candidate buffer in LDS (one
+//      atomic per wavefront and element slot that has any).
+//   3. an MSB-first radix select over the candidates' ranks keeps the best
+//      min(k, entries seen).  When the candidates overflow the buffer (many
+//      keys equal to L) the same select runs over the registers instead.
+// After the last chunk the kept ranks are sorted in the output order and
+// written.  The chunk's registers are the only copy of the row, so HBM sees
+// its 4 t bytes once (plus 8 k bytes of running entries when not first).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "knn_kernels.h"
+#include "topk_common.h"
+
+namespace mlxvs::kern {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Candidate ranks one workgroup holds in LDS per chunk.
+constexpr int kCandCap = 4096;
+
+// State of one radix select (in LDS).  After radix_pick, the wanted ranks
+// are those with (r & mask) > prefix, and of those with (r & mask) ==
+// prefix all of them when `done`, else `need` of them (equal ranks are
+// equal (score, id) pairs, so which copies does not matter).
+struct PickState {
+  uint64_t prefix;
+  uint64_t mask;
+  int need;
+  int done;
+  int taken;
+  int tie;
+};
+
+// MSB-first radix select of the `want` largest ranks among those `visit`
+// hands to f (each thread its own), 8 bits per pass.  A pass histograms
+// the digit of the ranks still matching the prefix; wavefront 0 finds the
+// digit of the want-th largest and stops the passes once the ranks matching
+// the new prefix are exactly the ones still needed.  All threads call it.
+template <int NT, typename Visit>
+__device__ void radix_pick(Visit visit, int want, uint32_t* hist, PickState& st) {
+  if (threadIdx.x == 0) {
+    st.prefix = 0;
+    st.mask = 0;
+    st.need = want;
+    st.done = 0;
+    st.taken = 0;
+    st.tie = 0;
+  }
+  for (int dg = 7; dg >= 0; --dg) {
+    for (int i = threadIdx.x; i < 256; i += NT) hist[i] = 0;
+    __syncthreads();
+    const uint64_t pre = st.prefix, msk = st.mask;
+    const int sh = 8 * dg;
+    visit([&](uint64_t r) {
+      if ((r & msk) == pre) atomicAdd(&hist[(uint32_t)(r >> sh) & 255u], 1u);
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      // lane l holds digits 255 - 4 l .. 252 - 4 l; the counts above them by
+      // a scan over the lanes
+      const int l = threadIdx.x;
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        c[u] = hist[255 - 4 * l - u];
+        sum += c[u];
+      }
+      uint32_t incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o);
+        if (l >= o) incl += y;
+      }
+      const uint32_t above = incl - sum;
+      const uint32_t need = (uint32_t)st.need;
+      if (above < need && incl >= need) {
+        uint32_t acc = above;
+        int dig = 252 - 4 * l;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (acc + c[u] >= need) {
+            dig = 255 - 4 * l - u;
+            break;
+          }
+          acc += c[u];
+        }
+        const uint32_t cnt = hist[dig];
+        st.need = (int)(need - acc);
+        st.prefix = pre | ((uint64_t)dig << sh);
+        st.mask = msk | (255ull << sh);
+        st.done = cnt == need - acc ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    if (st.done) break;
+  }
+}
+
+// Writes the ranks radix_pick chose into out (unordered).  Ends without a
+// barrier.
+template <typename Visit>
+__device__ void radix_gather(Visit visit, PickState& st, uint64_t* out) {
+  const uint64_t pre = st.prefix, msk = st.mask;
+  const bool done = st.done != 0;
+  const int need = st.need;
+  visit([&](uint64_t r) {
+    const uint64_t m = r & msk;
+    bool take = m > pre;
+    if (!take && m == pre) take = done || atomicAdd(&st.tie, 1) < need;
+    if (take) out[atomicAdd(&st.taken, 1)] = r;
+  });
+}
+
+// key_nz of a score in four bit operations (sign mask, or, xor, max): the
+// order-preserving key, with the one NaN whose key is 0 taking key 1 so that
+// 0 can mark "no element".
+__device__ __forceinline__ uint32_t key_bits(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t m = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
+  return max(u ^ m, 1u);
+}
+
+// The wavefront's values sorted descending (lane 0 the largest): a bitonic
+// network whose partner exchanges are lane shuffles.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t o = __shfl_xor(v, stride);
+      const bool lo = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;
+      v = (lo == desc) ? max(v, o) : min(v, o);
+    }
+  }
+  return v;
+}
+
+// Loads the thread's share of the chunk at c0 (VEC: 16-byte vectors, lane
+// e % 4 of vector e / 4 is element e) through a buffer resource whose range
+// is the chunk's valid scores: the chunk base and the element steps are
+// scalar, the only per-lane address is the thread's offset, and reads past
+// the range return 0.
+template <int NT, int PER, bool VEC>
+__device__ __forceinline__ void load_chunk(floatx4 (&x)[PER / 4], const float* row, int64_t c0,
+                                           int64_t valid) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(row + c0), (short)0, (int)(valid * 4), 0x00020000);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) {
+    if constexpr (VEC) {
+      x[i] = __builtin_bit_cast(floatx4,
+                                __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * tid, 16 * i * NT, 0));
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        x[i][u] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * tid, 4 * (4 * i + u) * NT, 0));
+    }
+  }
+}
+
+template <int NT, int PER, bool VEC>
+__global__ __launch_bounds__(NT) void topk_merge_kernel(TopkMergeArgs a) {
+  static_assert(NT >= kMaxK && NT % 64 == 0 && PER % 4 == 0, "shape");
+  constexpr int NW = NT / 64;
+  constexpr int64_t CHUNK = (int64_t)NT * PER;
+  __shared__ uint64_t buf[kCandCap];
+  __shared__ uint64_t tmp[kMaxK];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wbound[NW];
+  __shared__ PickState st;
+  __shared__ int s_cnt;  // entries in buf; above kCandCap: overflowed
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t q = a.row0 + blockIdx.x;
+  const int k = a.k;
+  const float* row = a.scores + q * a.t;
+  const uint32_t idoff = (uint32_t)a.id_offset;
+  // column of element e relative to the thread's first one in a chunk
+  auto step_of = [&](int e) -> uint32_t {
+    return VEC ? (uint32_t)((e >> 2) * NT * 4 + (e & 3)) : (uint32_t)(e * NT);
+  };
+
+  // The buffer holds the running entries first, then the candidates
+  // appended since; a compaction keeps the best min(k, seen) of it.
+  int64_t seen = 0;
+  if (a.prev_scores) {
+    if (tid < k) {
+      const int64_t o = q * k + tid;
+      buf[tid] = ((uint64_t)key_nz(a.prev_scores[o]) << 32) | (uint32_t)(~(uint32_t)a.prev_ids[o]);
+    }
+    seen = k;
+  }
+  if (tid == 0) s_cnt = (int)seen;
+  // L: a lower bound on the k-th best key of everything seen, so no entry
+  // below it is needed; it only grows
+  uint32_t L = 1;
+  bool overflow = false;
+
+  // keeps the best `want` ranks of buf[0 .. cnt) in buf[0 .. want); with
+  // want == k the threshold also bounds the k-th best
+  auto compact = [&](int cnt, int want) {
+    auto visit = [&](auto f) {
+      for (int i = tid; i < cnt; i += NT) f(buf[i]);
+    };
+    radix_pick<NT>(visit, want, hist, st);
+    radix_gather(visit, st, tmp);
+    __syncthreads();
+    for (int i = tid; i < want; i += NT) buf[i] = tmp[i];
+    if (tid == 0) s_cnt = want;
+    if (want == k) L = max(L, (uint32_t)((st.prefix & st.mask) >> 32));
+    __syncthreads();
+  };
+
+  // appends (key, id) to the buffer for the lanes with p set (one atomic
+  // per wavefront)
+  auto append = [&](bool p, uint32_t kk, uint32_t id) {
+    const uint64_t b = __builtin_amdgcn_ballot_w64(p);
+    if (b == 0) return;
+    const int leader = __builtin_ctzll(b);
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd((uint32_t*)&s_cnt, (uint32_t)__builtin_popcountll(b));
+    base = __shfl(base, leader);
+    if (p) {
+      const uint32_t pos =
+          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                           __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+      if (pos < (uint32_t)kCandCap) buf[pos] = ((uint64_t)kk << 32) | (uint32_t)(~id);
+    }
+  };
+
+  // One chunk (its scores in x, valid of them): the first chunk's bound,
+  // the count check and compaction, then the appends.  FULL chunks compare
+  // the scores themselves; the partial last chunk works on keys, 0 past the
+  // row.  With `next`, the following chunk's loads go out first and land in
+  // x while this one is filtered.  Returns false on overflow.
+  floatx4 x[PER / 4];
+  auto chunk = [&](auto full_c, int ci, int64_t c0, int64_t valid, int64_t next) -> bool {
+    constexpr bool FULL = decltype(full_c)::value;
+    float xs[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) xs[e] = x[e >> 2][e & 3];
+    if (next > 0) load_chunk<NT, PER, VEC>(x, row, c0 + CHUNK, next);
+    const uint32_t id0 = idoff + (uint32_t)c0 + (uint32_t)(VEC ? 4 * tid : tid);
+    uint32_t key[FULL ? 1 : PER];
+    uint32_t mx = 0;
+    if constexpr (!FULL) {
+      const int rem = (int)valid - (VEC ? 4 * tid : tid);  // elements from the thread's first
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        key[e] = rem > (int)step_of(e) ? key_bits(xs[e]) : 0u;
+        mx = max(mx, key[e]);
+      }
+    }
+    if (ci == 0) {
+      // the first chunk's bound: each wavefront's j-th largest thread
+      // maximum, j = ceil(k / wavefronts); the smallest of those has
+      // wavefronts * j >= k distinct elements at or above it.  (Every
+      // thread maximum is one of its elements: fmaxf passes over NaNs.)
+      if constexpr (FULL) {
+        float mf = xs[0];
+#pragma unroll
+        for (int e = 1; e < PER; ++e) mf = fmaxf(mf, xs[e]);
+        mx = key_bits(mf);
+      }
+      const int j = (k + NW - 1) / NW;
+      const uint32_t lw = __shfl(wave_sort_desc(mx, lane), j - 1);
+      if (lane == 0) wbound[w] = lw;
+    }
+    // the previous chunk's appends are all in
+    __syncthreads();
+    if (ci == 0) {
+      uint32_t lc = 0xffffffffu;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) lc = min(lc, wbound[i]);
+      L = max(L, lc);
+    }
+    const int cnt = s_cnt;
+    if (cnt > kCandCap) return false;
+    if (cnt > kCandCap / 2) compact(cnt, (int)(seen < k ? seen : k));
+    seen += valid;
+    // candidates: the chunk's elements at or above L
+    if constexpr (FULL) {
+      // key(x) >= L implies !(x < score(L)) (-0 and +0 compare equal and
+      // NaN passes: a superset, which the selection sorts out)
+      const float lf = score_of_key(L);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const bool p = !(xs[e] < lf);
+        if (__builtin_amdgcn_ballot_w64(p) != 0) append(p, key_bits(xs[e]), id0 + step_of(e));
+      }
+    } else {
+      if (__builtin_amdgcn_ballot_w64(mx >= L) != 0) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) append(key[e] >= L, key[e], id0 + step_of(e));
+      }
+    }
+    return true;
+  };
+
+  const int64_t nfull = a.t / CHUNK;
+  const int64_t tail = a.t - nfull * CHUNK;
+  if (a.t > 0) load_chunk<NT, PER, VEC>(x, row, 0, nfull > 0 ? CHUNK : tail);
+  int ci = 0;
+  for (; ci < nfull && !overflow; ++ci) {
+    const int64_t c0 = (int64_t)ci * CHUNK;
+    const int64_t next = ci + 1 < nfull ? CHUNK : tail;
+    overflow = !chunk(std::true_type{}, ci, c0, CHUNK, next);
+  }
+  if (tail > 0 && !overflow) overflow = !chunk(std::false_type{}, ci, nfull * CHUNK, tail, 0);
+  if (!overflow) {
+    __syncthreads();
+    overflow = s_cnt > kCandCap;
+  }
+
+  if (overflow) seen = (a.prev_scores ? k : 0) + a.t;
+  const int keff = (int)(seen < k ? seen : k);
+  if (overflow) {
+    // more candidates than the buffer holds (many keys equal to L): an
+    // exact select over the whole row, read again from memory, and the
+    // running entries (rare; it keeps the common path's registers free)
+    __syncthreads();
+    uint64_t prevr = 0;
+    if (a.prev_scores && tid < k) {
+      const int64_t o = q * k + tid;
+      prevr = ((uint64_t)key_nz(a.prev_scores[o]) << 32) | (uint32_t)(~(uint32_t)a.prev_ids[o]);
+    }
+    auto visit = [&](auto f) {
+      for (int64_t c = tid; c < a.t; c += NT)
+        f(((uint64_t)key_nz(row[c]) << 32) | (uint32_t)(~(idoff + (uint32_t)c)));
+      if (a.prev_scores && tid < k) f(prevr);
+    };
+    radix_pick<NT>(visit, keff, hist, st);
+    radix_gather(visit, st, tmp);
+    __syncthreads();
+    for (int i = tid; i < keff; i += NT) buf[i] = tmp[i];
+    __syncthreads();
+  } else {
+    const int cnt = s_cnt;
+    if (cnt > keff) compact(cnt, keff);
+  }
+
+  // the output order (float score descending with -0 == +0, then id)
+  const int P = pow2_at_least(keff > 1 ? keff : 1);
+  for (int i = keff + tid; i < P; i += NT) buf[i] = 0;
+  __syncthreads();
+  bitonic_desc<NT>(buf, P, OutputOrder{});
+  for (int i = tid; i < k; i += NT) {
+    const uint64_t r = i < keff ? buf[i] : 0ull;
+    const int64_t o = q * k + i;
+    a.ids[o] = r ? id_of_rank(r) : -1;
+    if (a.out_scores) a.out_scores[o] = r ? score_of_key((uint32_t)(r >> 32)) : -INFINITY;
+  }
+}
+
+template <int NT, int PER>
+hipError_t topk_inst(TopkMergeArgs a, bool vec, hipStream_t s) {
+  // rows per launch: the grid's work-items stay below 2^32
+  constexpr int64_t kRows = int64_t(1) << 20;
+  for (int64_t r0 = 0; r0 < a.nq; r0 += kRows) {
+    a.row0 = r0;
+    const unsigned g = (unsigned)std::min<int64_t>(kRows, a.nq - r0);
+    if (vec)
+      hipLaunchKernelGGL((topk_merge_kernel<NT, PER, true>), dim3(g), dim3(NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((topk_merge_kernel<NT, PER, false>), dim3(g), dim3(NT), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s) {
+  if (a.nq <= 0) return hipSuccess;
+  if (a.k < 1 || a.k > kMaxK || a.t < 0) return hipErrorInvalidValue;
+  // 16-byte vectors when every row starts 16-byte aligned
+  const bool vec = a.t % 4 == 0 && (uintptr_t)a.scores % 16 == 0;
+  if (a.t <= 1024) return topk_inst<256, 4>(a, vec, s);
+  if (a.t <= 4096) return topk_inst<256, 16>(a, vec, s);
+  return topk_inst<256, 32>(a, vec, s);
+}
+
+}  // namespace mlxvs::kern

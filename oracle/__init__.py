@@ -48,9 +48,10 @@ def lib():
         L.oracle_pack_words.argtypes = [vp, i64, ci, vp]
         L.oracle_key.argtypes = [ctypes.c_float]
         L.oracle_ivf_flat.argtypes = [vp, ci, vp, vp, vp, ci, ci, vp, i64, ci, ci, ci, vp, vp]
+        L.oracle_topk_merge.argtypes = [vp, i64, i64, vp, vp, ctypes.c_int32, ci, ci, vp, vp]
         L.oracle_key.restype = ctypes.c_uint32
         for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_self_graph_rows",
-                  "oracle_hamming",
+                  "oracle_hamming", "oracle_topk_merge",
                   "oracle_f16_to_f32", "oracle_pack_words"):
             getattr(L, f).restype = ci
         _lib = L
@@ -86,6 +87,25 @@ def knn(base, queries, k, metric="l2", nthreads=None):
     if rc:
         raise ValueError(f"oracle_knn_f32 rejected the arguments ({rc})")
     return ids, dist
+
+
+def topk_merge(scores, ids, best, id_offset, first, k):
+    """Restated topk_merge (src/knn.cpp:37-69, src/kernels.h:37-229): the
+    merged (ids int32 [nq, k], scores float32 [nq, k]), best first."""
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    nq, t = s.shape
+    pi = pb = None
+    if not first:
+        pi = np.ascontiguousarray(ids, dtype=np.int32)
+        pb = np.ascontiguousarray(best, dtype=np.float32)
+    out_i = np.empty((nq, k), np.int32)
+    out_s = np.empty((nq, k), np.float32)
+    rc = lib().oracle_topk_merge(_p(s), nq, t, None if first else _p(pi),
+                                 None if first else _p(pb), int(id_offset), int(bool(first)), k,
+                                 _p(out_i), _p(out_s))
+    if rc:
+        raise ValueError(f"oracle_topk_merge rejected the arguments ({rc})")
+    return out_i, out_s
 
 
 def ivf_flat(centers, data, indices, offsets, queries, k, n_probes, metric="l2",

@@ -19,6 +19,12 @@
  *      Merging tile by tile (src/knn.cpp:104-121) selects the same set as one
  *      selection over all rows, because every tile's ids are larger than the
  *      ids already kept; so the restatement selects once over all rows.
+ *  - topk_merge itself          src/knn.cpp:37-69, src/kernels.h:37-229
+ *      (oracle_topk_merge): the t scores of a row (id id_offset + column,
+ *      int32 arithmetic, src/kernels.h:119, 168) and, unless first, the k
+ *      running entries (:74, 170) are the candidates; keff = min(k,
+ *      candidates) (:48-49); kept: the keff largest by (key, then lowest
+ *      unsigned id) (:68-147); output as above (:196-228).
  *  - hamming_knn                src/ivf.cpp:1343-1403, 1121-1135, 1183-1242,
  *      src/ivf_kernels.h:549-595: popcount of XOR over little-endian uint32
  *      words (zero padded), ascending, lowest id among equal distances;
@@ -126,6 +132,52 @@ static int before_cmp(const void* pa, const void* pb) {
   if ((uint32_t)a->id != (uint32_t)b->id)
     return (uint32_t)a->id < (uint32_t)b->id ? -1 : 1;
   return 0;
+}
+
+/* ---- topk_merge ---------------------------------------------------------- */
+
+/* One merge step per row (src/knn.cpp:37-69 / src/kernels.h:37-229).  The
+ * kept set is the keff largest ranks: rank_of orders by key, then by lowest
+ * unsigned id, which is the reference's two radix selections (keys above the
+ * keff-th, then the lowest ids among the keys equal to it).  Entries of equal
+ * rank are equal (score, id) pairs, so which copies are kept does not show.
+ * The heap keeps the keff best; they are then sorted by before_cmp. */
+int oracle_topk_merge(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                      const float* best, int32_t id_offset, int first, int k,
+                      int32_t* out_ids, float* out_scores) {
+  if (nq < 0 || t < 0 || k < 1 || k > 256) return ORACLE_EINVAL;
+  if (!first && nq > 0 && (!ids || !best)) return ORACLE_EINVAL;
+  const int64_t total = t + (first ? 0 : k);
+  const int keff = (int)(total < k ? total : k);
+  uint64_t hv[256];
+  float hs[256];
+  int32_t hid[256];
+  pair_t sel[256];
+  for (int64_t q = 0; q < nq; ++q) {
+    heap_t h = {hv, hs, hid, 0, keff};
+    if (keff > 0) {
+      const float* row = scores + q * t;
+      for (int64_t c = 0; c < t; ++c) {
+        /* int32 arithmetic, wrapping as the reference's id_offset + (int)i */
+        const int32_t id = (int32_t)((uint32_t)id_offset + (uint32_t)c);
+        heap_push(&h, rank_of(row[c], id), row[c], id);
+      }
+      if (!first)
+        for (int j = 0; j < k; ++j)
+          heap_push(&h, rank_of(best[q * k + j], ids[q * k + j]), best[q * k + j],
+                    ids[q * k + j]);
+    }
+    for (int i = 0; i < h.size; ++i) {
+      sel[i].s = hs[i];
+      sel[i].id = hid[i];
+    }
+    qsort(sel, (size_t)h.size, sizeof(pair_t), before_cmp);
+    for (int i = 0; i < k; ++i) {
+      out_ids[q * k + i] = i < h.size ? sel[i].id : -1;
+      if (out_scores) out_scores[q * k + i] = i < h.size ? sel[i].s : -INFINITY;
+    }
+  }
+  return ORACLE_OK;
 }
 
 /* ---- float32 arithmetic ------------------------------------------------- */

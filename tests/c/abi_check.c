@@ -27,7 +27,7 @@ int main(void) {
   float dist[16];
   uint8_t codes[8] = {0};
   printf("mlxvs %s, C API %d\n", mlxvs_version(), MLXVS_C_API_VERSION);
-  check(strcmp(mlxvs_version(), "0.16.1-mi355x") == 0, "version");
+  check(strcmp(mlxvs_version(), "0.16.1") == 0, "version");
   check(MLXVS_INNER_PRODUCT == 0 && MLXVS_L2 == 1 && MLXVS_COSINE == 2, "metric values");
   check(MLXVS_OK == 0 && MLXVS_ERROR_INVALID_ARGUMENT == 1 && MLXVS_ERROR_IO == 2 &&
             MLXVS_ERROR_INTERNAL == 3, "status values");
@@ -54,6 +54,18 @@ int main(void) {
   check(st == MLXVS_ERROR_INVALID_ARGUMENT, "self graph n < 2");
   st = mlxvs_knn_self_graph(rows, 2, 4, 0, 256, MLXVS_L2, ids, dist);
   check(st == MLXVS_ERROR_INVALID_ARGUMENT, "self graph k = 256");
+
+  float scores[6] = {0};
+  st = mlxvs_topk_merge(scores, 2, 3, NULL, NULL, 0, 1, 0, ids, dist);
+  check(st == MLXVS_ERROR_INVALID_ARGUMENT &&
+            strstr(mlxvs_last_error(), "[mlxvs::topk_merge] k must be in [1, 256]") != NULL,
+        "topk_merge k = 0");
+  st = mlxvs_topk_merge(scores, 2, 3, NULL, NULL, 0, 0, 2, ids, dist);
+  check(st == MLXVS_ERROR_INVALID_ARGUMENT, "topk_merge running lists NULL unless first");
+  st = mlxvs_topk_merge(scores, 2, 3, NULL, NULL, 0, 1, 2, NULL, dist);
+  check(st == MLXVS_ERROR_INVALID_ARGUMENT, "topk_merge NULL out_ids");
+  st = mlxvs_topk_merge(scores, 0, 3, NULL, NULL, 0, 1, 2, ids, dist);
+  check(st == MLXVS_OK, "topk_merge with no rows does nothing");
 
   st = mlxvs_profile(0);
   check(st == MLXVS_OK && strlen(mlxvs_last_error()) == 0, "success clears the error");

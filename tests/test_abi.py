@@ -90,6 +90,18 @@ def test_python_argument_errors(engine):
         engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 0)
     with pytest.raises(ValueError, match="1 <= k <= 255"):
         engine.all_neighbors(np.zeros((4, 3), np.float32), 300)
+    # topk_merge: the reference's checks and messages (src/knn.cpp:46-54)
+    with pytest.raises(ValueError, match=r"scores must be float32 \[nq, t\]"):
+        engine.topk_merge(np.zeros((2, 3), np.float64), None, None, 0, True, 1)
+    with pytest.raises(ValueError, match=r"scores must be float32 \[nq, t\]"):
+        engine.topk_merge(np.zeros(3, np.float32), None, None, 0, True, 1)
+    with pytest.raises(ValueError, match=r"k must be in \[1, 256\]"):
+        engine.topk_merge(np.zeros((2, 3), np.float32), None, None, 0, True, 0)
+    with pytest.raises(ValueError, match=r"k must be in \[1, 256\]"):
+        engine.topk_merge(np.zeros((2, 3), np.float32), None, None, 0, True, 257)
+    with pytest.raises(ValueError, match=r"\[nq, k\]"):
+        engine.topk_merge(np.zeros((2, 3), np.float32), np.zeros((2, 2), np.int32),
+                          np.zeros((2, 2), np.float32), 0, False, 3)
 
 
 def test_no_cpu_fallback_without_gpu(engine):
@@ -107,4 +119,4 @@ def test_metric_enum_values(engine):
     assert int(engine.Metric.inner_product) == 0
     assert int(engine.Metric.l2) == 1
     assert int(engine.Metric.cosine) == 2
-    assert engine.version() == "0.16.1-mi355x"
+    assert engine.version() == "0.16.1"

@@ -310,3 +310,89 @@ def test_ivf_flat_short_lists_and_cosine(oracle):
     qn = q / np.linalg.norm(q, axis=1, keepdims=True)
     wi, wd = ivf_float64(c, data, ind, off, qn, 5, 4, "cosine")
     np.testing.assert_allclose(dist, wd, atol=1e-6)
+
+
+# ---- topk_merge (src/knn.cpp:37-69, src/kernels.h:37-229) ----------------------
+
+def _lexsort_best(S, k, id_offset=0):
+    """The k best columns of every row by (score desc, id asc) in float64,
+    ids id_offset + column (id_offset >= 0, so id order is column order)."""
+    nq, t = S.shape
+    keff = min(k, t)
+    ids = np.full((nq, k), -1, np.int64)
+    sc = np.full((nq, k), -np.inf, np.float64)
+    col = np.arange(t)
+    for i in range(nq):
+        o = np.lexsort((col, -S[i].astype(np.float64)))[:keff]
+        ids[i, :keff] = o + id_offset
+        sc[i, :keff] = S[i, o]
+    return ids, sc
+
+
+@pytest.mark.parametrize("t,k,off", [(1000, 10, 0), (777, 256, 5000), (40, 100, 7),
+                                     (5000, 1, 123)])
+def test_topk_merge_integer_scores_lexsort(oracle, t, k, off):
+    # inner products of small integers: exact in float32, many ties
+    b, q = int_rows(t, 8, 11, hi=4), int_rows(12, 8, 12, hi=4)
+    S = (q.astype(np.float64) @ b.T.astype(np.float64)).astype(np.float32)
+    ids, sc = oracle.topk_merge(S, None, None, off, True, k)
+    want_i, want_s = _lexsort_best(S, k, off)
+    assert np.array_equal(ids, want_i) and np.array_equal(sc, want_s.astype(np.float32))
+
+
+def test_topk_merge_tiles_equal_one_merge(oracle):
+    # the reference's brute_force_knn merges tile after tile (src/knn.cpp:104-121):
+    # chained merges with the running lists equal one merge over the whole row
+    S = np.random.default_rng(3).integers(-50, 50, (20, 3000)).astype(np.float32)
+    k = 37
+    one_i, one_s = oracle.topk_merge(S, None, None, 0, True, k)
+    ids = best = None
+    for t0 in range(0, 3000, 700):
+        ids, best = oracle.topk_merge(S[:, t0:t0 + 700], ids, best, t0, t0 == 0, k)
+    assert np.array_equal(ids, one_i) and np.array_equal(best, one_s)
+
+
+def test_topk_merge_matches_the_pinned_knn(oracle):
+    # L2 scores 2 q.b - |b|^2 (src/knn.cpp:111-116) of integer rows merged once
+    # give the ids of the brute-force restatement pinned above
+    b, q = int_rows(2000, 16, 21), int_rows(30, 16, 22)
+    bb = (b.astype(np.float64) ** 2).sum(1)
+    S = (2.0 * (q.astype(np.float64) @ b.T.astype(np.float64)) - bb).astype(np.float32)
+    ids, _ = oracle.topk_merge(S, None, None, 0, True, 16)
+    kid, _ = oracle.knn(b, q, 16, "l2")
+    assert np.array_equal(ids, kid)
+
+
+def test_topk_merge_known_answers(oracle):
+    # all scores equal: the lowest ids
+    ids, sc = oracle.topk_merge(np.full((1, 50), 2.5, np.float32), None, None, 100, True, 4)
+    assert ids.tolist() == [[100, 101, 102, 103]] and (sc == 2.5).all()
+    # ascending scores: the last columns, best first
+    ids, sc = oracle.topk_merge(np.arange(10, dtype=np.float32)[None], None, None, 0, True, 3)
+    assert ids.tolist() == [[9, 8, 7]] and sc.tolist() == [[9, 8, 7]]
+    # fewer candidates than k: -1 / -inf padding (src/kernels.h:224-228)
+    ids, sc = oracle.topk_merge(np.array([[1, 3, 2]], np.float32), None, None, 0, True, 5)
+    assert ids.tolist() == [[1, 2, 0, -1, -1]]
+    assert sc[0, :3].tolist() == [3, 2, 1] and (sc[0, 3:] == -np.inf).all()
+    # +0 outranks -0 when selecting (key order), but they are equal when
+    # sorting (float compare), so the lower id comes first
+    S = np.array([[-0.0, 0.0]], np.float32)
+    ids, sc = oracle.topk_merge(S, None, None, 0, True, 1)
+    assert ids.tolist() == [[1]] and not np.signbit(sc[0, 0])
+    ids, sc = oracle.topk_merge(S, None, None, 0, True, 2)
+    assert ids.tolist() == [[0, 1]] and np.signbit(sc[0, 0]) and not np.signbit(sc[0, 1])
+    # ids compare unsigned: -2 and -1 (id_offset -2) lose to 0 and 1
+    ids, _ = oracle.topk_merge(np.zeros((1, 4), np.float32), None, None, -2, True, 2)
+    assert ids.tolist() == [[0, 1]]
+    # running lists take part unless first; the initial -1 / -inf entries are
+    # candidates too
+    prev_i = np.array([[-1, -1, -1, -1]], np.int32)
+    prev_s = np.full((1, 4), -np.inf, np.float32)
+    ids, sc = oracle.topk_merge(np.array([[5, 4]], np.float32), prev_i, prev_s, 10, False, 4)
+    assert ids.tolist() == [[10, 11, -1, -1]] and sc[0, 2:].tolist() == [-np.inf, -np.inf]
+    ids, _ = oracle.topk_merge(np.array([[5, 4]], np.float32), np.array([[3, 7]], np.int32),
+                               np.array([[4.5, 9]], np.float32), 10, False, 2)
+    assert ids.tolist() == [[7, 10]]
+    ids, _ = oracle.topk_merge(np.array([[5, 4]], np.float32), np.array([[3, 7]], np.int32),
+                               np.array([[4.5, 9]], np.float32), 10, True, 2)
+    assert ids.tolist() == [[10, 11]]
