@@ -76,6 +76,20 @@ MLXVS_API void brute_force_knn_device(const Rows& base, const Rows& queries, int
                                       void* stream = nullptr);
 
 /**
+ * brute_force_knn_device with no allocation: the workspace comes from a
+ * fixed device array of 64 MiB per GPU that the library holds until the
+ * process ends (no hipMalloc, hipFree or allocating call).  No counterpart
+ * in the reference: for callers that cannot allocate (graph capture,
+ * serving loops).  Sizes whose workspace exceeds the array, k > 16 and
+ * shapes the fused kernels do not take are rejected with invalid_argument
+ * before anything is enqueued.  Calls that overlap on one GPU share the
+ * array and race.
+ */
+MLXVS_API void brute_force_knn_device_noalloc(const Rows& base, const Rows& queries, int k,
+                                              Metric metric, int32_t* ids, float* distances,
+                                              void* stream = nullptr);
+
+/**
  * Exact Hamming k-NN of bit-packed uint8 rows [n, bytes] for bit-packed
  * queries [nq, bytes]; 1 <= k <= 256.  Replaces reference
  * include/mlxvs/mlxvs.h:775-784.

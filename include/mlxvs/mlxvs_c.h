@@ -227,6 +227,32 @@ MLXVS_C_API int mlxvs_brute_force_knn_device(
     float* distances,
     void* stream);
 
+/**
+ * mlxvs_brute_force_knn_device without allocating: no counterpart in the
+ * reference; for callers that cannot call hipMalloc (code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation).  Its
+ * workspace (norms, per-lane lists, bounds, merge levels) is a fixed device
+ * array of 64 MiB on each GPU the library runs on, held until the process
+ * ends; the call itself allocates nothing.  Limits: k <= 16, a workspace of
+ * at most 64 MiB (about 10,000 queries against 1,000,000 rows of 128 dims
+ * at k = 10) and shapes the fused kernels take; anything else returns
+ * MLXVS_ERROR_INVALID_ARGUMENT before any work is enqueued.  Enqueued on
+ * stream, returns without waiting.  Calls that overlap on one GPU share the
+ * array and race: order them (one stream, or events).
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_device_noalloc(
+    const void* base,
+    int64_t n,
+    const void* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
 /** mlxvs_hamming_knn on device memory (see mlxvs_brute_force_knn_device). */
 MLXVS_C_API int mlxvs_hamming_knn_device(
     const uint8_t* rows,

@@ -73,6 +73,8 @@ def _load():
         "mlxvs_ivf_flat_search_device": [vp, i64, vp, i64, vp, vp, i32, ctypes.c_int, vp, i64,
                                          i32, i32, vp, vp, vp],
         "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
+        "mlxvs_brute_force_knn_device_noalloc": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int,
+                                                 vp, vp, vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_topk_merge": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp],

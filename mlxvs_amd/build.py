@@ -22,7 +22,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libmlxvs_c.so"
 
-SOURCES = ["knn_float.hip", "knn_hamming.hip", "topk_merge.hip", "engine.cpp", "c_api.cpp"]
+SOURCES = ["knn_float.hip", "knn_hamming.hip", "topk_merge.hip", "scratch.hip", "engine.cpp", "c_api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

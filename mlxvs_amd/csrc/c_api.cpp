@@ -163,6 +163,19 @@ int mlxvs_brute_force_knn_device(const void* base, int64_t n, const void* querie
   });
 }
 
+int mlxvs_brute_force_knn_device_noalloc(const void* base, int64_t n, const void* queries,
+                                         int64_t nq, int32_t d, int32_t f16, int32_t k,
+                                         mlxvs_metric metric, int32_t* ids, float* distances,
+                                         void* stream) {
+  return guarded([&] {
+    require(ids != nullptr || nq == 0, "ids must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto b = host_rows(base, n, d, t);
+    auto q = host_rows(queries, nq, d, t);
+    mlxvs::brute_force_knn_device_noalloc(b, q, k, to_metric(metric), ids, distances, stream);
+  });
+}
+
 int mlxvs_hamming_knn_device(const uint8_t* rows, int64_t n, const uint8_t* queries,
                              int64_t nq, int32_t bytes, int32_t k, int32_t* ids,
                              float* distances, void* stream) {

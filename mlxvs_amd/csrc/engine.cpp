@@ -60,10 +60,17 @@ struct ProfRec {
 std::vector<ProfRec> g_prof_pending;
 std::map<std::string, std::pair<int64_t, double>> g_prof_totals;
 
+// A dry run (t_dry) plans a call without launching anything, to size its
+// workspace; t_noprof keeps a call from creating timing events (the
+// no-allocation entry point).
+thread_local bool t_dry = false;
+thread_local bool t_noprof = false;
+
 template <typename F>
 void launch(hipStream_t s, const char* stage, F&& f) {
-  bool prof;
-  {
+  if (t_dry) return;
+  bool prof = false;
+  if (!t_noprof) {
     std::lock_guard<std::mutex> g(g_prof_mutex);
     prof = g_prof_on;
   }
@@ -117,7 +124,17 @@ int current_device() {
 // makes calls on different streams safe to issue back to back.
 class Arena {
  public:
+  Arena() = default;
+  // Over a caller's fixed memory [base, base + size): never allocates, and a
+  // request past the end throws invalid_argument naming `op` (base may be a
+  // dummy address for a dry run that only counts the bytes).
+  Arena(char* base, size_t size, const char* op) : fixed_(true), op_(op) {
+    chunks_.push_back({base, size, 0});
+  }
   ~Arena() = default;  // device memory is reclaimed at process exit
+
+  bool fixed() const { return fixed_; }
+  size_t used() const { return chunks_.empty() ? 0 : chunks_[0].used; }
 
   void begin(hipStream_t s) {
     if (done_) check_hip(hipStreamWaitEvent(s, done_, 0), "hipStreamWaitEvent");
@@ -138,6 +155,13 @@ class Arena {
         c.used += bytes;
         return p;
       }
+    }
+    if (fixed_) {
+      char msg[160];
+      snprintf(msg, sizeof msg,
+               "the call needs more than the %zu MiB of scratch the no-allocation entry "
+               "holds.", chunks_[0].size >> 20);
+      invalid(op_, msg);
     }
     size_t total = 0;
     for (auto& c : chunks_) total += c.size;
@@ -170,6 +194,7 @@ class Arena {
   // kept across calls; a copy into pageable memory goes through a staged,
   // slower path.
   int* host_ints(size_t count) {
+    if (fixed_) invalid(op_, "this call would read the merge flags back to the host.");
     if (count > host_count_) {
       if (host_) (void)hipHostFree(host_);
       host_ = nullptr;
@@ -200,12 +225,15 @@ class Arena {
   hipEvent_t done_ = nullptr;
   int* host_ = nullptr;
   size_t host_count_ = 0;
+  bool fixed_ = false;
+  const char* op_ = "";
 };
 
 std::mutex g_mutex;
 std::map<int, std::unique_ptr<Arena>> g_arenas;
 
-// Holds the device's arena for the duration of one call.
+// Holds the device's arena for the duration of one call, or a caller's
+// fixed arena (no lock, no ordering with other calls, no allocation).
 class Session {
  public:
   explicit Session(hipStream_t s) : lock_(g_mutex), stream_(s) {
@@ -215,7 +243,9 @@ class Session {
     arena_ = slot.get();
     arena_->begin(s);
   }
+  Session(hipStream_t s, Arena& fixed) : stream_(s), arena_(&fixed) {}
   ~Session() {
+    if (arena_->fixed()) return;
     try {
       arena_->end(stream_);
     } catch (...) {
@@ -225,7 +255,7 @@ class Session {
   hipStream_t stream() const { return stream_; }
 
  private:
-  std::lock_guard<std::mutex> lock_;
+  std::unique_lock<std::mutex> lock_;
   hipStream_t stream_;
   Arena* arena_ = nullptr;
 };
@@ -598,6 +628,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   };
 
   if (!plan.ok) {
+    // the exhaustive path stages its query list from the host
+    if (ar.fixed()) invalid("mlxvs::brute_force_knn_noalloc", "these sizes need the exhaustive path, which the no-allocation entry does not take.");
     const float *eb, *eq;
     fp32_rows(kbase, n, &eb);
     fp32_rows(kq, nq, &eq);
@@ -1145,6 +1177,55 @@ void brute_force_knn_device(const Rows& base, const Rows& queries, int k, Metric
   float_knn(ss, {base.data, queries.data, base.n, queries.n, base.d,
                  base.dtype == Dtype::Float16},
             k, (int)metric, ids, dists);
+}
+
+void brute_force_knn_device_noalloc(const Rows& base, const Rows& queries, int k,
+                                    Metric metric, int32_t* ids, float* distances,
+                                    void* stream) {
+  const char* op = "mlxvs::brute_force_knn_noalloc";
+  float_args(base, queries, k, metric, op);
+  if (ids == nullptr && queries.n * k > 0) invalid(op, "ids must not be NULL.");
+  // k > 16 reads the merge's overflow flags back to the host
+  if (base.n > 0 && k > 16) invalid(op, "k must be at most 16.");
+  const int64_t nq = queries.n;
+  const FloatInputs in{base.data, queries.data, base.n, nq, base.d, base.dtype == Dtype::Float16};
+  const size_t odist = distances ? 0 : (size_t)std::max<int64_t>(1, nq * k);
+  struct Flags {
+    Flags(bool dry) : d(t_dry), p(t_noprof) {
+      t_dry = dry;
+      t_noprof = true;
+    }
+    ~Flags() {
+      t_dry = d;
+      t_noprof = p;
+    }
+    bool d, p;
+  };
+  (void)current_device();  // "no HIP device" before any planning
+  // size the workspace first: a dry run of the same plan that launches
+  // nothing and hands out addresses of a dummy range
+  size_t need = 0;
+  {
+    Flags f(true);
+    Arena meas((char*)(uintptr_t)4096, ~size_t(0) >> 1, op);
+    Session ss((hipStream_t)stream, meas);
+    float* dists = distances ? distances : meas.take<float>(odist);
+    float_knn(ss, in, k, (int)metric, ids, dists);
+    need = meas.used();
+  }
+  if (need > kern::kScratchBytes) {
+    char msg[200];
+    snprintf(msg, sizeof msg,
+             "these sizes need %zu MiB of scratch, more than the %zu MiB the no-allocation "
+             "entry holds.", (need + (1 << 20) - 1) >> 20, kern::kScratchBytes >> 20);
+    invalid(op, msg);
+  }
+  char* scratch = (char*)kern::scratch_address();
+  Flags f(false);
+  Arena fixed(scratch, kern::kScratchBytes, op);
+  Session ss((hipStream_t)stream, fixed);
+  float* dists = distances ? distances : fixed.take<float>(odist);
+  float_knn(ss, in, k, (int)metric, ids, dists);
 }
 
 std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m,

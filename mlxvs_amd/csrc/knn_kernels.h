@@ -354,6 +354,13 @@ struct TopkMergeArgs {
 };
 hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s);
 
+// Device scratch of the no-allocation entry point (scratch.hip): a fixed
+// array of kScratchBytes per GPU, held until the process ends.  Returns its
+// device address on the current device (hipGetSymbolAddress on the first
+// call per device).
+constexpr size_t kScratchBytes = size_t(64) << 20;
+void* scratch_address();
+
 // Self-graph post-pass: drop each row's own id from a k+1 list and re-order
 // by distance (src/all_neighbors.cpp:56-95).
 struct SelfDropArgs {
