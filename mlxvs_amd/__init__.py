@@ -20,7 +20,6 @@ from __future__ import annotations
 
 import ctypes
 import enum
-import os
 from pathlib import Path
 
 import numpy as np
@@ -42,10 +41,8 @@ __all__ = [
 ]
 __version__ = "0.16.1"
 
-# MLXVS_LIBRARY selects another build of the same library (e.g. an
-# experimental variant); the default is the in-tree build.
-_LIB_PATH = Path(os.environ.get("MLXVS_LIBRARY") or
-                 Path(__file__).resolve().parent / "libmlxvs_c.so")
+# the in-tree build (python -m mlxvs_amd.build)
+_LIB_PATH = Path(__file__).resolve().parent / "libmlxvs_c.so"
 
 # mlxvs_status (include/mlxvs/mlxvs_c.h)
 OK, INVALID_ARGUMENT, IO_ERROR, INTERNAL = 0, 1, 2, 3

@@ -1,117 +1,141 @@
-"""cuVS index files: a 4-byte dtype prefix, then every scalar and array as
-one NumPy ``.npy`` (format 1.0) record, little endian.
+"""The record framing of cuVS / RAFT index files.
 
-The layout of reference python/mlxvs/cuvs/_serialize.py, which follows
-RAFT's ``numpy_serializer``: the header dict is written without a trailing
-comma and padded with 1 to 64 spaces and a newline so that magic, version,
-length and header end on a multiple of 64 bytes; one-byte types (and bool)
-carry no byte order, binary16 is ``<e2`` (``<f2`` in a prefix of format 6 or
-later).  Readers accept any valid format 1.0 record.
+An index file starts with a 4-byte type tag (the dataset's element type as
+text, NUL padded) and continues as a run of NumPy ``.npy`` format-1.0
+records, one per scalar or array, all little endian.  RAFT's
+``numpy_serializer`` (which cuVS uses, and which the reference's Python
+package reproduces in python/mlxvs/cuvs/_serialize.py) frames them in a way
+NumPy's own writer does not, and cuVS's readers expect that framing:
+
+* the header dictionary has no trailing comma after its last entry;
+* it is followed by 1 to 64 spaces and a newline, so that the payload
+  starts on a 64-byte boundary of the record;
+* one-byte types carry no byte order (``|u1``, ``|i1``; a bool is written
+  as ``|u1``), and binary16 is ``<e2`` -- except in the type tag of files of
+  format version 6 and later, where it reads ``<f2``.
+
+NumPy's reader (``numpy.lib.format``) accepts every record written here.
 """
 
 from __future__ import annotations
 
 import ast
 import struct
+from typing import BinaryIO
 
 import numpy as np
 
-MAGIC = b"\x93NUMPY"
+# element types and the type text written for each
+_CODES = (
+    (np.float32, "<f4"),
+    (np.float64, "<f8"),
+    (np.float16, "<e2"),
+    (np.int8, "|i1"),
+    (np.uint8, "|u1"),
+    (np.int32, "<i4"),
+    (np.uint32, "<u4"),
+    (np.int64, "<i8"),
+    (np.uint64, "<u8"),
+)
+_TEXT_OF = {np.dtype(t): text for t, text in _CODES}
+_TEXT_OF[np.dtype(np.bool_)] = "|u1"
+_TYPE_OF = {text: np.dtype(t) for t, text in _CODES}
+_TYPE_OF["<f2"] = np.dtype(np.float16)
+_TYPE_OF["|b1"] = np.dtype(np.bool_)
 
-_DESCR = {
-    np.dtype(np.float32): "<f4",
-    np.dtype(np.float64): "<f8",
-    np.dtype(np.float16): "<e2",
-    np.dtype(np.int8): "|i1",
-    np.dtype(np.uint8): "|u1",
-    np.dtype(np.bool_): "|u1",
-    np.dtype(np.int32): "<i4",
-    np.dtype(np.uint32): "<u4",
-    np.dtype(np.int64): "<i8",
-    np.dtype(np.uint64): "<u8",
-}
-_TYPES = {
-    "<f4": np.float32, "<f8": np.float64, "<e2": np.float16, "<f2": np.float16,
-    "|i1": np.int8, "|u1": np.uint8, "<i4": np.int32, "<u4": np.uint32,
-    "<i8": np.int64, "<u8": np.uint64, "|b1": np.bool_,
-}
-
-
-def _shape_text(shape) -> str:
-    dims = [str(int(s)) for s in shape]
-    if not dims:
-        return "()"
-    if len(dims) == 1:
-        return f"({dims[0]},)"
-    return "(" + ", ".join(dims) + ")"
+_LEAD = b"\x93NUMPY\x01\x00"  # magic string and format version 1.0
+_ALIGN = 64
 
 
-def header_bytes(dtype, shape) -> bytes:
-    """The record header of an array of `dtype` and `shape`."""
-    text = (f"{{'descr': '{_DESCR[np.dtype(dtype)]}', 'fortran_order': False, "
-            f"'shape': {_shape_text(shape)}}}")
-    fixed = len(MAGIC) + 2 + 2
-    spaces = 64 - (fixed + len(text) + 1) % 64  # 1 .. 64
-    body = text.encode("latin1") + b" " * spaces + b"\n"
-    return MAGIC + b"\x01\x00" + struct.pack("<H", len(body)) + body
+def _type_text(dtype) -> str:
+    try:
+        return _TEXT_OF[np.dtype(dtype)]
+    except KeyError:
+        raise ValueError(f"no cuVS record type for {np.dtype(dtype)}") from None
 
 
-def write_scalar(f, value, dtype) -> None:
-    f.write(header_bytes(dtype, ()))
-    f.write(np.asarray(value, dtype=dtype).astype(np.dtype(dtype).newbyteorder("<")).tobytes())
+def record_header(dtype, shape) -> bytes:
+    """Lead, header length and padded header dictionary of one record."""
+    shape = tuple(int(s) for s in shape)
+    meta = f"{{'descr': '{_type_text(dtype)}', 'fortran_order': False, 'shape': {shape}}}"
+    used = len(_LEAD) + 2 + len(meta) + 1  # the newline ends the header
+    meta += " " * (_ALIGN - used % _ALIGN) + "\n"
+    return _LEAD + struct.pack("<H", len(meta)) + meta.encode("latin1")
 
 
-def write_array(f, a, dtype=None) -> None:
-    a = np.ascontiguousarray(a, dtype=dtype)
-    f.write(header_bytes(a.dtype, a.shape))
-    f.write(a.astype(a.dtype.newbyteorder("<"), copy=False).tobytes())
+class RecordWriter:
+    """Appends records to a binary file object."""
+
+    def __init__(self, f: BinaryIO):
+        self._f = f
+
+    def scalar(self, value, dtype) -> None:
+        dt = np.dtype(dtype)
+        self._f.write(record_header(dt, ()))
+        self._f.write(np.asarray(value, dtype=dt).astype(dt.newbyteorder("<")).tobytes())
+
+    def array(self, a, dtype=None) -> None:
+        a = np.ascontiguousarray(a, dtype=dtype)
+        self._f.write(record_header(a.dtype, a.shape))
+        self._f.write(a.astype(a.dtype.newbyteorder("<"), copy=False).tobytes())
 
 
-def read_header(f):
-    """(dtype, shape) of the next record."""
-    head = f.read(10)
-    if len(head) < 10 or head[:6] != MAGIC:
-        raise ValueError("not a cuVS index file: missing a NumPy record")
-    if head[6] != 1:
-        raise ValueError(f"unsupported NumPy record version {head[6]}.{head[7]}")
-    (hlen,) = struct.unpack("<H", head[8:10])
-    d = ast.literal_eval(f.read(hlen).decode("latin1").strip())
-    if d.get("fortran_order"):
-        raise ValueError("Fortran-ordered arrays are not supported")
-    if d["descr"] not in _TYPES:
-        raise ValueError(f"unsupported dtype {d['descr']!r}")
-    return np.dtype(_TYPES[d["descr"]]), tuple(d["shape"])
+class RecordReader:
+    """Takes records from a binary file object, one at a time."""
+
+    def __init__(self, f: BinaryIO):
+        self._f = f
+
+    def _take(self, count: int) -> bytes:
+        raw = self._f.read(count)
+        if len(raw) != count:
+            raise ValueError("the cuVS index file ends inside a record")
+        return raw
+
+    def header(self):
+        """(dtype, shape) of the next record."""
+        lead = self._take(len(_LEAD) + 2)
+        if lead[:6] != _LEAD[:6]:
+            raise ValueError("not a cuVS index file: expected a NumPy record")
+        if lead[6] != 1:
+            raise ValueError(f"NumPy record format {lead[6]}.{lead[7]} is not read here "
+                             "(RAFT writes 1.0)")
+        (size,) = struct.unpack("<H", lead[8:10])
+        meta = ast.literal_eval(self._take(size).decode("latin1").strip())
+        if not isinstance(meta, dict) or meta.get("fortran_order", False):
+            raise ValueError("cuVS records hold C-ordered arrays only")
+        dt = _TYPE_OF.get(meta.get("descr"))
+        if dt is None:
+            raise ValueError(f"record type {meta.get('descr')!r} is not a cuVS type")
+        return dt, tuple(int(s) for s in meta["shape"])
+
+    def _payload(self, dt: np.dtype, shape) -> np.ndarray:
+        count = int(np.prod(shape, dtype=np.int64)) if shape else 1
+        raw = self._take(count * dt.itemsize)
+        return np.frombuffer(raw, dtype=dt.newbyteorder("<")).astype(dt).reshape(shape)
+
+    def scalar(self):
+        dt, shape = self.header()
+        if shape:
+            raise ValueError(f"expected a scalar record, found one of shape {shape}")
+        return self._payload(dt, shape).item()
+
+    def array(self) -> np.ndarray:
+        dt, shape = self.header()
+        return self._payload(dt, shape)
 
 
-def read_scalar(f):
-    dtype, shape = read_header(f)
-    if shape:
-        raise ValueError(f"expected a scalar, found shape {shape}")
-    raw = f.read(dtype.itemsize)
-    if len(raw) != dtype.itemsize:
-        raise ValueError("truncated cuVS index file")
-    return np.frombuffer(raw, dtype=dtype.newbyteorder("<"))[0].item()
+def type_tag(dtype, version: int) -> bytes:
+    """The 4-byte type tag that opens an index file of format `version`."""
+    text = _type_text(dtype)
+    if text == "<e2" and version >= 6:
+        text = "<f2"
+    return text.encode("latin1").ljust(4, b"\0")
 
 
-def read_array(f) -> np.ndarray:
-    dtype, shape = read_header(f)
-    count = int(np.prod(shape)) if shape else 1
-    raw = f.read(count * dtype.itemsize)
-    if len(raw) != count * dtype.itemsize:
-        raise ValueError("truncated cuVS index file")
-    return np.frombuffer(raw, dtype=dtype.newbyteorder("<")).astype(dtype).reshape(shape)
-
-
-def dtype_prefix(dtype, version: int) -> bytes:
-    """The 4-byte dtype prefix of an index file."""
-    s = _DESCR[np.dtype(dtype)]
-    if s == "<e2" and version >= 6:
-        s = "<f2"
-    return s.encode().ljust(4, b"\0")
-
-
-def read_prefix(f) -> np.dtype:
-    s = f.read(4).rstrip(b"\0").decode("latin1")
-    if s not in _TYPES:
-        raise ValueError(f"unknown dtype prefix {s!r}")
-    return np.dtype(_TYPES[s])
+def read_type_tag(f: BinaryIO) -> np.dtype:
+    """The element type named by a file's opening tag."""
+    text = f.read(4).rstrip(b"\0").decode("latin1")
+    if text not in _TYPE_OF:
+        raise ValueError(f"the file's type tag {text!r} names no cuVS type")
+    return _TYPE_OF[text]

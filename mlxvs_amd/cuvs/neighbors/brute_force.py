@@ -1,191 +1,192 @@
-"""cuVS's ``cuvs.neighbors.brute_force`` on the exact k-NN engine.
+"""cuVS's ``cuvs.neighbors.brute_force`` (build / search / save / load) on the
+exact k-NN engine.
 
-Mirrors reference python/mlxvs/cuvs/neighbors/brute_force.py: ``build`` keeps
-the rows and a cuVS distance type, ``search`` answers with the fused k-NN
-(``brute_force_knn``, or ``hamming_knn`` for bit-packed rows) and returns
-``(distances float32, neighbors int64)`` in cuVS's units, ``save`` / ``load``
-use cuVS's brute-force file format (version 0; :mod:`mlxvs_amd.cuvs._serialize`),
-which cuVS's own ``brute_force.load`` reads.
+The public names and arguments are cuVS's, as the reference's compatibility
+module python/mlxvs/cuvs/neighbors/brute_force.py keeps them.  Search runs
+the fused k-NN (``brute_force_knn``, or ``hamming_knn`` for bit-packed rows)
+and reports cuVS's distance units.  Files are cuVS's brute-force format,
+version 0, readable by cuVS's own ``brute_force.load``.
 
-The engine's metrics are the ones this index takes: ``"sqeuclidean"``
-(L2Expanded), ``"euclidean"`` / ``"l2"`` (L2SqrtExpanded),
-``"inner_product"``, ``"cosine"`` (CosineExpanded) and ``"bitwise_hamming"``.
-The reference's element-wise pairwise metrics (cityblock, chebyshev, ...)
-and its prefilters run outside the fused path and are not part of this
-engine; asking for them raises ``ValueError``.
+Distance types served: ``"sqeuclidean"`` (L2Expanded), ``"euclidean"`` /
+``"l2"`` (L2SqrtExpanded), ``"cosine"`` (CosineExpanded),
+``"inner_product"`` and ``"bitwise_hamming"``.  cuVS's element-wise
+pairwise metrics (cityblock, chebyshev, minkowski, ...) and prefilters are
+evaluated outside a fused top-k path and are not offered: they raise
+``ValueError``.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+from typing import Callable, Optional
+
 import numpy as np
 
-from mlxvs_amd.cuvs import _serialize as io
+from mlxvs_amd.cuvs._serialize import RecordReader, RecordWriter, read_type_tag, type_tag
 
 __all__ = ["Index", "build", "load", "save", "search"]
 
-# cuVS DistanceType values (reference python/mlxvs/cuvs/distance.py:12-32)
-L2Expanded = 0
-L2SqrtExpanded = 1
-CosineExpanded = 2
-InnerProduct = 6
-BitwiseHamming = 20
 
-DISTANCE_TYPES = {
-    "sqeuclidean": L2Expanded,
-    "euclidean": L2SqrtExpanded,
-    "l2": L2SqrtExpanded,
-    "inner_product": InnerProduct,
-    "cosine": CosineExpanded,
-    "bitwise_hamming": BitwiseHamming,
-}
-_NAMES = {L2Expanded: "sqeuclidean", L2SqrtExpanded: "euclidean", CosineExpanded: "cosine",
-          InnerProduct: "inner_product", BitwiseHamming: "bitwise_hamming"}
-# engine metric of each distance type
-_ENGINE = {L2Expanded: "l2", L2SqrtExpanded: "l2", InnerProduct: "inner_product",
-           CosineExpanded: "cosine"}
+@dataclass(frozen=True)
+class _Distance:
+    """A cuVS distance type and how this module serves it."""
 
-_SERIALIZATION_VERSION = 0
+    code: int                  # cuVS DistanceType value
+    name: str                  # cuVS metric name
+    engine: Optional[str]      # engine metric (None: Hamming on packed bits)
+    norms: Optional[str]       # the norms record a file carries: "squared", "plain"
+    units: Callable[[np.ndarray], np.ndarray]  # engine output -> cuVS distance
 
 
-def _metric_type(metric) -> int:
+# cuVS DistanceType values (cuvs/distance/distance.hpp, as the reference's
+# python/mlxvs/cuvs/distance.py:12-32 lists them)
+_DISTANCES = (
+    _Distance(0, "sqeuclidean", "l2", "squared", lambda d: np.maximum(d, 0)),
+    _Distance(1, "euclidean", "l2", "squared", lambda d: np.sqrt(np.maximum(d, 0))),
+    _Distance(2, "cosine", "cosine", "plain", lambda s: 1 - s),
+    _Distance(6, "inner_product", "inner_product", None, lambda s: s),
+    _Distance(20, "bitwise_hamming", None, None, lambda d: d),
+)
+_BY_CODE = {d.code: d for d in _DISTANCES}
+_BY_NAME = {d.name: d for d in _DISTANCES}
+_BY_NAME["l2"] = _BY_CODE[1]
+
+FORMAT_VERSION = 0
+
+
+def _distance(metric) -> _Distance:
     if isinstance(metric, str):
-        if metric not in DISTANCE_TYPES:
-            raise ValueError(f"metric {metric!r} is not supported by this engine; one of "
-                             + ", ".join(repr(m) for m in DISTANCE_TYPES))
-        return DISTANCE_TYPES[metric]
-    t = int(metric)
-    if t not in _NAMES:
-        raise ValueError(f"distance type {t} is not supported by this engine")
-    return t
+        found = _BY_NAME.get(metric)
+    else:
+        found = _BY_CODE.get(int(metric))
+    if found is None:
+        served = ", ".join(sorted(_BY_NAME))
+        raise ValueError(f"metric {metric!r} is not supported here (served: {served})")
+    return found
 
 
 class Index:
-    """A brute-force index: the dataset and its distance type."""
+    """A brute-force index: the rows and their cuVS distance type."""
 
     def __init__(self):
-        self.trained = False
-        self._dataset = None
-        self._metric = L2Expanded
+        self._rows: Optional[np.ndarray] = None
+        self._distance = _BY_CODE[0]
         self._metric_arg = 2.0
 
     @property
-    def dataset(self):
-        return self._dataset
+    def trained(self) -> bool:
+        return self._rows is not None
+
+    @property
+    def dataset(self) -> Optional[np.ndarray]:
+        return self._rows
+
+    @property
+    def metric(self) -> str:
+        return self._distance.name
+
+    @property
+    def distance_type(self) -> int:
+        return self._distance.code
 
     def __len__(self):
-        return 0 if self._dataset is None else self._dataset.shape[0]
+        return 0 if self._rows is None else int(self._rows.shape[0])
 
     def __repr__(self):
-        return f"Index(type=BruteForce, metric={_NAMES.get(self._metric)})"
+        return f"brute_force.Index(rows={len(self)}, metric={self.metric!r})"
 
 
-def build(dataset, metric="sqeuclidean", metric_arg=2.0, resources=None):
-    """The index of ``dataset`` [n, dim] (float32 / float16 rows, or bit-packed
-    uint8 rows for ``"bitwise_hamming"``), as cuVS's ``brute_force.build``."""
-    x = np.asarray(dataset)
-    if x.ndim != 2:
-        raise ValueError("dataset must be a matrix")
-    t = _metric_type(metric)
-    if t == BitwiseHamming and x.dtype != np.uint8:
-        raise ValueError("bitwise_hamming needs bit-packed uint8 rows")
+def _index(rows: np.ndarray, dist: _Distance, metric_arg: float) -> Index:
+    if dist.code == 20 and rows.dtype != np.uint8:
+        raise ValueError("bitwise_hamming indexes bit-packed uint8 rows")
     idx = Index()
-    idx._dataset = np.ascontiguousarray(x)
-    idx._metric = t
+    idx._rows = np.ascontiguousarray(rows)
+    idx._distance = dist
     idx._metric_arg = float(metric_arg)
-    idx.trained = True
     return idx
 
 
-def _to_cuvs(scores: np.ndarray, t: int) -> np.ndarray:
-    """Engine outputs (squared L2, inner product, cosine similarity) as cuVS's
-    distances (reference python/mlxvs/cuvs/neighbors/_common.py:39-48)."""
-    if t == L2SqrtExpanded:
-        return np.sqrt(np.maximum(scores, 0))
-    if t == L2Expanded:
-        return np.maximum(scores, 0)
-    if t == CosineExpanded:
-        return 1 - scores
-    return scores
+def build(dataset, metric="sqeuclidean", metric_arg=2.0, resources=None) -> Index:
+    """The index of ``dataset`` (float32 / float16 rows ``[n, dim]``, or
+    bit-packed uint8 rows for ``"bitwise_hamming"``); the rows are kept."""
+    rows = np.asarray(dataset)
+    if rows.ndim != 2:
+        raise ValueError(f"the dataset must be a matrix [n, dim], got {rows.ndim} dimensions")
+    return _index(rows, _distance(metric), metric_arg)
 
 
 def search(index, queries, k, neighbors=None, distances=None, resources=None,
            prefilter=None):
-    """The k nearest rows of every query, as cuVS's ``brute_force.search``.
-
-    Returns ``(distances float32 [nq, k], neighbors int64 [nq, k])``,
-    nearest first (largest inner product first); ``neighbors`` /
-    ``distances`` given as arrays are filled in place.  -1 where fewer than
-    k rows exist.
+    """``(distances float32 [nq, k], neighbors int64 [nq, k])`` of every query,
+    nearest first (for inner product, largest first); -1 past the rows there
+    are.  Given ``neighbors`` / ``distances`` arrays are filled and returned.
     """
     from mlxvs_amd import brute_force_knn, hamming_knn
 
-    if not index.trained:
-        raise ValueError("Index needs to be built before calling search.")
+    if not getattr(index, "trained", False):
+        raise ValueError("search needs a built index (see brute_force.build)")
     if prefilter is not None and getattr(prefilter, "type", "none") != "none":
-        raise ValueError("prefilters are not supported by this engine")
+        raise ValueError("prefilters are not offered by this exact engine")
+    dist = index._distance
     q = np.asarray(queries)
-    t = index._metric
-    if t == BitwiseHamming:
-        ids, dist = hamming_knn(index._dataset, q, k)
+    if dist.engine is None:
+        ids, out = hamming_knn(index._rows, q, k)
     else:
-        ids, scores = brute_force_knn(index._dataset, q, k, _ENGINE[t])
-        dist = _to_cuvs(scores, t)
-    ids = np.where(ids < 0, -1, ids).astype(np.int64)
-    dist = np.asarray(dist, dtype=np.float32)
+        ids, raw = brute_force_knn(index._rows, q, k, dist.engine)
+        out = dist.units(raw)
+    ids = ids.astype(np.int64)
+    ids[ids < 0] = -1
+    out = np.asarray(out, dtype=np.float32)
     if distances is not None:
-        distances[...] = dist
-        dist = distances
+        distances[...] = out
+        out = distances
     if neighbors is not None:
         neighbors[...] = ids
         ids = neighbors
-    return dist, ids
+    return out, ids
 
 
-def save(filename, index, include_dataset=True, resources=None):
-    """Writes the index in cuVS's brute-force format (version 0): dtype prefix,
-    version, rows, dim, distance type, metric arg, the dataset flag and rows,
-    then the norms flag and the rows' norms (squared for L2, plain for
-    cosine) -- reference python/mlxvs/cuvs/neighbors/brute_force.py:142-165."""
-    data = np.asarray(index._dataset)
-    t = index._metric
+def save(filename, index, include_dataset=True, resources=None) -> None:
+    """Writes ``index`` as a cuVS brute-force file (format 0).
+
+    After the type tag: version, rows, dim, distance type and metric
+    argument; a flag and the dataset; a flag and, for the L2 types, the
+    rows' squared norms (cosine: their norms), which cuVS reads back
+    instead of recomputing them.
+    """
+    rows = np.asarray(index._rows)
+    dist = index._distance
     with open(filename, "wb") as f:
-        f.write(io.dtype_prefix(data.dtype, 6))
-        io.write_scalar(f, _SERIALIZATION_VERSION, np.int32)
-        io.write_scalar(f, data.shape[0], np.uint64)
-        io.write_scalar(f, data.shape[1], np.uint64)
-        io.write_scalar(f, t, np.int32)
-        io.write_scalar(f, index._metric_arg, np.float32)
-        io.write_scalar(f, bool(include_dataset), np.bool_)
+        f.write(type_tag(rows.dtype, 6))
+        w = RecordWriter(f)
+        for value, dtype in ((FORMAT_VERSION, np.int32), (rows.shape[0], np.uint64),
+                             (rows.shape[1], np.uint64), (dist.code, np.int32),
+                             (index._metric_arg, np.float32)):
+            w.scalar(value, dtype)
+        w.scalar(bool(include_dataset), np.bool_)
         if include_dataset:
-            io.write_array(f, data)
-        has_norms = t in (L2Expanded, L2SqrtExpanded, CosineExpanded)
-        io.write_scalar(f, has_norms, np.bool_)
-        if has_norms:
-            x = data.astype(np.float32)
-            norms = np.sum(x * x, axis=1)
-            if t == CosineExpanded:
-                norms = np.sqrt(norms)
-            io.write_array(f, norms.astype(np.float32))
+            w.array(rows)
+        w.scalar(dist.norms is not None, np.bool_)
+        if dist.norms is not None:
+            x = rows.astype(np.float32)
+            sq = (x * x).sum(axis=1)
+            w.array((sq if dist.norms == "squared" else np.sqrt(sq)).astype(np.float32))
 
 
-def load(filename, resources=None):
-    """Reads an index written by :func:`save` or by cuVS."""
+def load(filename, resources=None) -> Index:
+    """Reads a brute-force file written by :func:`save` or by cuVS."""
     with open(filename, "rb") as f:
-        dtype = io.read_prefix(f)
-        ver = io.read_scalar(f)
-        if ver != _SERIALIZATION_VERSION:
-            raise ValueError(f"serialization version mismatch, expected "
-                             f"{_SERIALIZATION_VERSION}, got {ver}")
-        io.read_scalar(f)  # rows
-        io.read_scalar(f)  # dim
-        metric = io.read_scalar(f)
-        metric_arg = io.read_scalar(f)
-        if not io.read_scalar(f):
-            raise ValueError("the file holds no dataset; brute force needs it")
-        data = io.read_array(f).astype(dtype, copy=False)
-    idx = Index()
-    idx._dataset = np.ascontiguousarray(data)
-    idx._metric = _metric_type(int(metric))
-    idx._metric_arg = float(metric_arg)
-    idx.trained = True
-    return idx
+        dtype = read_type_tag(f)
+        r = RecordReader(f)
+        version = r.scalar()
+        if version != FORMAT_VERSION:
+            raise ValueError(f"brute-force file format {version} is not read here "
+                             f"(expected {FORMAT_VERSION})")
+        n, dim, code, metric_arg = r.scalar(), r.scalar(), r.scalar(), r.scalar()
+        if not r.scalar():
+            raise ValueError("this file was saved without its dataset, which a brute-force "
+                             "index cannot do without")
+        rows = r.array().astype(dtype, copy=False)
+    if rows.shape != (n, dim):
+        raise ValueError(f"the dataset record is {rows.shape}, the file says ({n}, {dim})")
+    return _index(rows, _distance(int(code)), metric_arg)

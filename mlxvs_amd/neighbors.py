@@ -1,93 +1,128 @@
-"""A scikit-learn style front end over the exact k-NN engine.
+"""scikit-learn's ``NearestNeighbors`` interface over the exact k-NN engine.
 
-Mirrors reference python/mlxvs/_neighbors.py:18-96 (``NearestNeighbors``):
-``fit(X)`` keeps the rows, ``kneighbors(Q)`` returns NumPy
-``(distances, indices)`` nearest first in scikit-learn's units -- Euclidean
-distance for ``"euclidean"`` (the square root of the engine's squared L2),
-cosine distance ``1 - cos`` for ``"cosine"``, the squared L2 as it is for
-``"sqeuclidean"`` / ``"l2"`` -- and int64 indices.  ``kneighbors()`` without
-queries answers for the fitted rows themselves with each row's own index
-dropped (the single-cluster brute-force self graph).
+The class keeps the public surface of reference python/mlxvs/_neighbors.py
+(constructor arguments, ``fit``, ``kneighbors``, the fitted attributes and
+scikit-learn's distance units).  Each metric name resolves to the metric
+the engine computes plus a conversion into scikit-learn's units:
 
-Only ``algorithm="brute"`` exists here: the reference's ``"nn_descent"``
-builds an approximate graph, which is outside this engine.
+=============  ==============  ==========================================
+name           engine metric   reported distance
+=============  ==============  ==========================================
+euclidean      squared L2      its square root
+sqeuclidean    squared L2      as computed
+l2             squared L2      as computed
+cosine         cosine sim.     1 - similarity
+=============  ==============  ==========================================
+
+``kneighbors()`` without queries asks for the fitted rows' own neighbours
+and leaves every row out of its own list (the single-cluster self graph of
+``all_neighbors``).  The engine is exact only, so ``algorithm`` is
+``"brute"``; the reference's approximate ``"nn_descent"`` graph is refused.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+from typing import Callable, Optional
+
 import numpy as np
 
-_METRICS = {  # reference python/mlxvs/_neighbors.py:10-15
-    "euclidean": "l2",
-    "sqeuclidean": "l2",
-    "l2": "l2",
-    "cosine": "cosine",
+
+@dataclass(frozen=True)
+class _Units:
+    engine: str                                           # engine metric name
+    convert: Optional[Callable[[np.ndarray], np.ndarray]]  # None: as computed
+
+
+_UNITS = {
+    "euclidean": _Units("l2", np.sqrt),
+    "sqeuclidean": _Units("l2", None),
+    "l2": _Units("l2", None),
+    "cosine": _Units("cosine", lambda sim: 1.0 - sim),
 }
 
 
+def _units_of(metric: str) -> _Units:
+    try:
+        return _UNITS[metric]
+    except (KeyError, TypeError):
+        known = ", ".join(_UNITS)
+        raise ValueError(f"unknown metric {metric!r} for NearestNeighbors "
+                         f"(known: {known})") from None
+
+
+def _check_algorithm(algorithm: str) -> None:
+    if algorithm == "brute":
+        return
+    if algorithm == "nn_descent":
+        raise ValueError("algorithm 'nn_descent' builds an approximate graph, which this "
+                         "exact engine does not provide; use algorithm='brute'")
+    raise ValueError(f"algorithm {algorithm!r} is not available; this engine searches "
+                     "with algorithm='brute'")
+
+
 class NearestNeighbors:
-    """Exact nearest neighbours with scikit-learn's interface.
+    """Exact k nearest neighbours, scikit-learn style.
 
     Args:
-        n_neighbors (int): Neighbours per query.
+        n_neighbors (int): Neighbours returned per query by default.
         metric (str): ``"euclidean"``, ``"sqeuclidean"``, ``"l2"`` or
           ``"cosine"``.
         algorithm (str): ``"brute"``.
-        n_clusters (int): Accepted for signature compatibility; must be 1.
+        n_clusters (int): Kept for signature compatibility (the reference
+          uses it with NN-Descent only).
     """
 
     def __init__(self, n_neighbors=5, *, metric="euclidean", algorithm="brute", n_clusters=1):
-        if metric not in _METRICS:
-            names = ", ".join(repr(m) for m in _METRICS)
-            raise ValueError(f"unknown metric {metric!r}; one of {names}")
-        if algorithm == "nn_descent":
-            raise ValueError("algorithm 'nn_descent' (approximate) is not part of this "
-                             "engine; use 'brute'")
-        if algorithm != "brute":
-            raise ValueError("algorithm must be 'brute' or 'nn_descent'")
+        self._units = _units_of(metric)
+        _check_algorithm(algorithm)
         self.n_neighbors = n_neighbors
         self.metric = metric
         self.algorithm = algorithm
         self.n_clusters = n_clusters
+        self._rows: Optional[np.ndarray] = None
 
     def fit(self, X, y=None):
-        """Keep the rows ``X [n, d]`` (float16 rows stay float16)."""
-        x = np.asarray(X)
-        if x.ndim != 2:
-            raise ValueError("X must be 2-D [n, d]")
-        self._fit_X = np.ascontiguousarray(x)
-        self.n_samples_fit_ = x.shape[0]
-        self.n_features_in_ = x.shape[1]
+        """Remember the rows ``X [n, d]`` (float16 rows are kept as float16
+        and searched on the fp16 MFMA path); returns ``self``."""
+        rows = np.asarray(X)
+        if rows.ndim != 2:
+            raise ValueError(f"fit expects a 2-D array of rows [n, d]; got shape {rows.shape}")
+        self._rows = np.ascontiguousarray(rows)
+        self.n_samples_fit_, self.n_features_in_ = rows.shape
         return self
 
+    def _neighbours_wanted(self, n_neighbors, self_query: bool) -> int:
+        k = self.n_neighbors if n_neighbors is None else int(n_neighbors)
+        # a fitted row is not a candidate in its own list
+        most = self.n_samples_fit_ - (1 if self_query else 0)
+        if not 1 <= k <= most:
+            whose = "each fitted row has" if self_query else "the fitted data has"
+            raise ValueError(f"n_neighbors={k} is out of range: {whose} {most} candidate rows "
+                             f"(1 <= n_neighbors <= {most})")
+        return k
+
     def kneighbors(self, X=None, n_neighbors=None, return_distance=True):
-        """The neighbours of each row of ``X``, or of each fitted row.
+        """Neighbours of the rows of ``X`` -- or, without ``X``, of every
+        fitted row, excluding the row itself -- nearest first.
 
-        Without ``X`` a row is not its own neighbour, as in scikit-learn.
-
-        Returns:
-            ``(distances float32, indices int64)`` ``[nq, n_neighbors]``, or
-            only the indices with ``return_distance=False``.
+        Returns ``(distances float32, indices int64)`` of shape
+        ``[queries, n_neighbors]``, or only the indices when
+        ``return_distance`` is false.
         """
         from mlxvs_amd import all_neighbors, brute_force_knn
 
-        if not hasattr(self, "_fit_X"):
-            raise RuntimeError("call fit(X) first")
-        k = self.n_neighbors if n_neighbors is None else n_neighbors
-        limit = self.n_samples_fit_ - (1 if X is None else 0)
-        if not 1 <= k <= limit:
-            raise ValueError(f"n_neighbors must be in [1, {limit}], got {k}")
-        metric = _METRICS[self.metric]
+        if self._rows is None:
+            raise RuntimeError("this NearestNeighbors is not fitted yet: call fit(X) first")
+        k = self._neighbours_wanted(n_neighbors, X is None)
         if X is None:
-            ids, dist = all_neighbors(self._fit_X, k, metric)
+            ids, raw = all_neighbors(self._rows, k, self._units.engine)
         else:
-            ids, dist = brute_force_knn(self._fit_X, X, k, metric)
-        ids = ids.astype(np.int64)
+            ids, raw = brute_force_knn(self._rows, X, k, self._units.engine)
+        indices = np.asarray(ids, dtype=np.int64)
         if not return_distance:
-            return ids
-        dist = np.array(dist, dtype=np.float32)
-        if self.metric == "euclidean":
-            dist = np.sqrt(dist)
-        elif self.metric == "cosine":
-            dist = 1.0 - dist
-        return dist, ids
+            return indices
+        dist = np.asarray(raw, dtype=np.float32)
+        if self._units.convert is not None:
+            dist = self._units.convert(dist).astype(np.float32, copy=False)
+        return dist, indices
