@@ -157,21 +157,21 @@ def cpu_baseline(w, sample: int):
     t0 = time.perf_counter()
     if w["kind"] == "topk":
         threads = 1  # the restatement merges rows on one core
-        oracle.topk_merge(base[:sample], None, None, 0, True, w["k"])
+        out = oracle.topk_merge(base[:sample], None, None, 0, True, w["k"])
     elif w["kind"] == "hamming":
-        oracle.hamming(base, q, w["k"], nthreads=threads)
+        out = oracle.hamming(base, q, w["k"], nthreads=threads)
     elif w["kind"] == "self":
         x = oracle.f16_to_f32(base)
-        oracle.knn(x, x[:sample], w["k"] + 1, w["metric"], nthreads=threads)
+        out = oracle.knn(x, x[:sample], w["k"] + 1, w["metric"], nthreads=threads)
     elif w["kind"] == "ivf":
         c, data, ind, off = w["index"]
-        oracle.ivf_flat(c, data, ind, off, q, w["k"], w["n_probes"], w["metric"],
-                        nthreads=threads)
+        out = oracle.ivf_flat(c, data, ind, off, q, w["k"], w["n_probes"], w["metric"],
+                              nthreads=threads)
     elif base.dtype == np.float16:
-        oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), w["k"], w["metric"],
-                   nthreads=threads)
+        out = oracle.knn(oracle.f16_to_f32(base), oracle.f16_to_f32(q), w["k"], w["metric"],
+                         nthreads=threads)
     else:
-        oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
+        out = oracle.knn(base, q, w["k"], w["metric"], nthreads=threads)
     dt = time.perf_counter() - t0
     if w["kind"] == "topk":
         what = (f"first {sample} of {base.shape[0]} score rows of {base.shape[1]} scores, "
@@ -180,7 +180,41 @@ def cpu_baseline(w, sample: int):
         what = (f"first {sample} of {w['q'].shape[0]} queries against all {base.shape[0]} "
                 f"rows, {dt:.1f} s")
     return {"value": round(sample / dt, 2), "unit": "queries/s", "cores": threads,
-            "kind": "port", "sample": what}
+            "cpu": cpu_model(), "kind": "port", "sample": what}, out
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_api_ms(w, reps: int = 3):
+    """The reference's full call as a caller sees it: the C-ABI entry on host
+    arrays, copies in and out included (median of `reps` after a warm-up;
+    bench/bench_knn.cpp:20-33, 83-87 time brute_force_knn the same way)."""
+    import mlxvs_amd
+
+    if w["kind"] == "float":
+        fn = lambda: mlxvs_amd.brute_force_knn(w["base"], w["q"], w["k"], w["metric"])  # noqa
+    elif w["kind"] == "hamming":
+        fn = lambda: mlxvs_amd.hamming_knn(w["base"], w["q"], w["k"])  # noqa: E731
+    elif w["kind"] == "topk":
+        fn = lambda: mlxvs_amd.topk_merge(w["base"], None, None, 0, True, w["k"])  # noqa
+    else:
+        return None
+    fn()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        t.append((time.perf_counter() - t0) * 1e3)
+    return round(sorted(t)[len(t) // 2], 3)
 
 
 def main() -> int:
@@ -189,6 +223,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="c2")
+    ap.add_argument("--e2e", type=int, default=1,
+                    help="also time the host C-ABI call with its copies (e2e_ms; 0: skip)")
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="queries timed on the CPU restatement (0: skip)")
     ap.add_argument("--nq", type=int, default=None,
@@ -346,9 +382,26 @@ def main() -> int:
     if sample is None:
         sample = {"c1": 100, "c2": 10000, "c2h": 2000, "c3": 16, "c3cos": 16, "c3h": 16,
                   "c4": 256, "c5": 512, "ivf": 10000, "topk": 4096}[args.workload]
-    cpu = cpu_baseline(w, min(sample, nq)) if sample else None
+    cpu, cpu_out = cpu_baseline(w, min(sample, nq)) if sample else (None, None)
     if cpu and w["kind"] == "topk":
         cpu["unit"] = "score rows/s"
+    # the whole GPU answer for the queries the CPU restatement answered
+    # (bit-exact on integer-valued data; float data: ids and distances to
+    # the tolerances the tests use)
+    if cpu_out is not None and w["kind"] in ("float", "hamming", "topk") and not args.nq:
+        oi, od = cpu_out
+        m = oi.shape[0]
+        if w["kind"] == "topk":
+            same = np.array_equal(ids[:m], oi) and np.array_equal(dist[:m].view(np.uint32),
+                                                                  od.view(np.uint32))
+        elif args.workload in ("c1", "c2", "c2h", "c4"):
+            same = np.array_equal(ids[:m], oi) and np.array_equal(dist[:m], od)
+        else:
+            same = None
+        if same is not None:
+            full = f"{m} of {nq} rows vs the CPU restatement: {'bit-exact' if same else 'MISMATCH'}"
+            check = full if check is None else f"{full}; {check}"
+    e2e = host_api_ms(w) if args.e2e else None
 
     line = {
         "metric": METRIC if args.workload == "c2" else w["desc"],
@@ -368,10 +421,11 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": cpu,
         "stages_ms_per_step": {s: round(v[1] / args.steps, 4) for s, v in stages.items()},
+        "e2e_ms": e2e,
         "check": check,
     }
     print(json.dumps(line), flush=True)
-    return 0 if (check is None or "bit-exact" in check) else 1
+    return 1 if (check is not None and "MISMATCH" in check) else 0
 
 
 if __name__ == "__main__":

@@ -12,7 +12,7 @@ fixture stores a digest of its inputs so that generator drift is caught.
 Fixtures (all .npz, loadable with allow_pickle=False):
   c1_full.npz       configuration c1 in full: 100 queries x 10,000 rows, L2, k=10
   c2_subset.npz     configuration c2, first 64 queries x all 1,000,000 rows, L2, k=10
-  c3_subset.npz     configuration c3 on its first 100,000 rows, first 16 queries,
+  c3_subset.npz     configuration c3 on its first 100,000 rows, first 256 queries,
                     inner product and cosine, k=10 (float64 ids and scores)
   c4_subset.npz     configuration c4, first 32 queries x all 1,000,000 codes, k=100
   c5_subset.npz     configuration c5 self graph, first 32 rows x all 200,000 rows,
@@ -118,7 +118,7 @@ def make_c2():
 
 def make_c3():
     cen = synth.c3_centres()
-    q = synth.c3_rows(2, 0, 16, centres=cen)
+    q = synth.c3_rows(2, 0, 256, centres=cen)
     gen = lambda lo, hi: synth.c3_rows(1, lo, hi, centres=cen)  # noqa: E731
     ids_ip, sc_ip, dg = chunked_topk(q, gen, 100_000, 10, ip_scores, chunk=25_000)
     ids_cos, sc_cos, _ = chunked_topk(q, gen, 100_000, 10, cos_scores, chunk=25_000)

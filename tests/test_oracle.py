@@ -141,7 +141,7 @@ def test_c3_golden(oracle):
     g = np.load(GOLDEN / "c3_subset.npz")
     for metric, key in (("inner_product", "ip"), ("cosine", "cos")):
         ids, dist = oracle.knn(base, q, 10, metric)
-        np.testing.assert_allclose(dist, g["score_" + key], atol=1e-4)
+        np.testing.assert_allclose(dist, g["score_" + key][:16], atol=1e-4)
         s = oracle.exact_scores(q, base, metric)
         assert oracle.recall(ids, s, 10) == 1.0
 
