@@ -219,6 +219,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   __shared__ __align__(16) E tile1[TR * ROWE];
   __shared__ __align__(16) float tnorm0[64];  // 64: a norm load writes 64 lanes
   __shared__ __align__(16) float tnorm1[64];
+  // lists of 16 over 64-row tiles (k > 10, often k > 16: many lanes pass)
+  // append their candidates to a per-lane buffer first (CandBuf)
+  constexpr bool BUF = MODE != 2 && RB == 2 && T == 16;
+  constexpr int CB = 6;
+  __shared__ uint64_t cbuf[BUF ? CB * 256 : 1];
 
   if constexpr (MODE != 0) {
     // items counted on the device: the grid is an upper bound
@@ -341,12 +346,13 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
+  CandBuf<CB> cb(&cbuf[BUF ? tid : 0]);
   // the filter: the score of K[T-1] or better, for L2 on half scores
-  // (filter_of) (NaN -- every candidate passes -- while the list has room
-  // and nothing better is known)
-  // (+inf for a lane without a query: nothing passes, so it never
-  // lengthens the wavefront's drain)
-  float thr = qvalid ? score_of_key(0u) : INFINITY;
+  // (filter_of); while the list has room and nothing better is known every
+  // candidate passes: NaN, or -inf for the buffered select, whose pass test
+  // is the sign of x - thr (+inf for a lane without a query: nothing
+  // passes, so it never lengthens the wavefront's drain)
+  float thr = qvalid ? (BUF ? -INFINITY : score_of_key(0u)) : INFINITY;
   // All lanes of a query -- in every workgroup -- filter with the shared
   // lower bound on its k-th best score (SharedBound), raised with relaxed
   // atomic max operations as the segment lists fill.
@@ -428,17 +434,17 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
         thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
       bool inserted = false;
       // lists of 16 (k > 10, often k > 16: many lanes pass): the two blocks
-      // drain together; for shorter lists the pair's registers cost more
-      // than it saves
-      if constexpr (MODE != 2 && RB == 2 && T == 16) {
+      // drain together into the candidate buffer; for shorter lists the
+      // pair's registers cost more than it saves
+      if constexpr (BUF) {
         float sc0[16], sc1[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           sc0[i] = acc[0][i];
           sc1[i] = acc[1][i];
         }
-        inserted = select_pair<T, L2>(K, I, thr, sc0, sc1, h, idbase + (uint32_t)(t * TR),
-                                      nrows - t * TR);
+        inserted = select_pair_buf<T, L2, CB>(K, I, thr, sc0, sc1, h,
+                                              idbase + (uint32_t)(t * TR), nrows - t * TR, cb);
       } else
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
@@ -480,6 +486,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     step(tile0, tnorm0, tile1, tnorm1, t);
     if (t + 1 < ntiles) step(tile1, tnorm1, tile0, tnorm0, t + 1);
   }
+  // what is left in the candidate buffer (a wavefront-uniform loop)
+  if constexpr (BUF) flush_buf<T, L2, CB>(K, I, thr, cb);
 
   if (MODE != 2 && qvalid) {
     const int nseg = MODE == 0 ? a.nsplit : a.P * (a.nsplit > 1 ? a.nsplit : 1);

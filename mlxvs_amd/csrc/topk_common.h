@@ -221,6 +221,90 @@ __device__ __forceinline__ bool select_pair(uint32_t (&K)[T], uint32_t (&I)[T], 
   return any;
 }
 
+// sc0 or sc1 [i & 15] by bit 4 of i: a select tree within each block, then
+// one select between the blocks (31 selects and no dynamic index, which the
+// compiler would otherwise stage through scratch memory).
+__device__ __forceinline__ float pick32(const float (&sc0)[16], const float (&sc1)[16], int i) {
+  const float a = pick16(sc0, i & 15), b = pick16(sc1, i & 15);
+  return (i & 16) ? b : a;
+}
+
+// A lane's candidate buffer: B entries in LDS at stride 256 (entry e of the
+// lane at slot[256 e]; the workgroup's 256 lanes side by side), each the
+// candidate's key (high word) and id.  Candidates that pass the lane's
+// threshold are appended (about 45 instructions an iteration) instead of
+// being inserted into the sorted list (a T-slot insertion each); the buffer
+// is merged into the list when some lane of the wavefront has B entries, or
+// at the end, so that the insertions of many tiles run in the same
+// iterations across the wavefront's lanes.
+template <int B>
+struct CandBuf {
+  uint64_t* slot;  // this lane's entry 0
+  int cnt = 0;
+  __device__ __forceinline__ explicit CandBuf(uint64_t* lane0) : slot(lane0) {}
+};
+
+// Merges a lane's buffer into its list in append (increasing id) order and
+// raises the lane's own filter; the loop runs as often as the fullest
+// lane's buffer needs.
+template <int T, bool HALF, int B>
+__device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                          CandBuf<B>& cb) {
+#pragma unroll
+  for (int e = 0; e < B; ++e) {
+    if (__builtin_amdgcn_ballot_w64(e < cb.cnt) == 0) break;
+    const uint64_t v = e < cb.cnt ? cb.slot[256 * e] : 0ull;
+    stream_insert<T>(K, I, (uint32_t)(v >> 32), (uint32_t)v);
+  }
+  cb.cnt = 0;
+  thr = fmaxf(thr, filter_of<HALF>(score_of_key(K[T - 1] + 1u)));
+}
+
+// select_pair with the candidate buffer: the same filter and the same lists
+// once the buffer is flushed.  Returns whether the list changed (a flush
+// took place), which is when the lane's shared-bound key may have risen.
+template <int T, bool HALF, int B>
+__device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
+                                                const float (&sc0)[16], const float (&sc1)[16],
+                                                int h, uint32_t id0, int lim, CandBuf<B>& cb) {
+  float mx0 = fmaxf(fmaxf(sc0[0], sc0[1]), sc0[2]), mx1 = fmaxf(fmaxf(sc1[0], sc1[1]), sc1[2]);
+#pragma unroll
+  for (int i = 3; i < 15; i += 2) {
+    mx0 = fmaxf(fmaxf(mx0, sc0[i]), sc0[i + 1]);
+    mx1 = fmaxf(fmaxf(mx1, sc1[i]), sc1[i + 1]);
+  }
+  const float mx = fmaxf(fmaxf(mx0, sc0[15]), fmaxf(mx1, sc1[15]));
+  if (__builtin_amdgcn_ballot_w64(!(mx < thr)) == 0) return false;
+  // the failing positions: the sign of x - thr (x >= thr gives +0 or more),
+  // shifted in one per funnel shift, position i ending at bit i.  thr must
+  // be a number or -inf here (no NaN): -inf passes everything, and inf - inf
+  // is the positive default NaN
+  uint32_t fm = 0;
+#pragma unroll
+  for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc1[i] - thr), 31);
+#pragma unroll
+  for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc0[i] - thr), 31);
+  uint32_t pm = ~fm;
+  if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
+  bool flushed = false;
+  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+    if (__builtin_amdgcn_ballot_w64(cb.cnt == B) != 0) {
+      flush_buf<T, HALF, B>(K, I, thr, cb);
+      flushed = true;
+    }
+    if (pm) {
+      const int i = __builtin_ctz(pm);
+      const float x = HALF ? 2.0f * pick32(sc0, sc1, i) : pick32(sc0, sc1, i);
+      const int j = i & 15;
+      const int m = (i & 16 ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
+      cb.slot[256 * cb.cnt] = ((uint64_t)key_nz(x) << 32) | (uint32_t)(id0 + m);
+      ++cb.cnt;
+      pm &= pm - 1u;
+    }
+  }
+  return flushed;
+}
+
 // The rank (see rank_of) of a stream-list slot, 0 for an empty one.
 __device__ __forceinline__ uint64_t stream_rank(uint32_t k, uint32_t id) {
   return k ? (((uint64_t)k << 32) | (uint32_t)(~id)) : 0ull;
