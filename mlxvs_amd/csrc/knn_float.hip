@@ -346,7 +346,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   uint32_t K[T], I[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
-  CandBuf<CB> cb(&cbuf[BUF ? tid : 0]);
+  CandBuf<CB, 256> cb(&cbuf[BUF ? tid : 0]);
   // the filter: the score of K[T-1] or better, for L2 on half scores
   // (filter_of); while the list has room and nothing better is known every
   // candidate passes: NaN, or -inf for the buffered select, whose pass test
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
           sc0[i] = acc[0][i];
           sc1[i] = acc[1][i];
         }
-        inserted = select_pair_buf<T, L2, CB>(K, I, thr, sc0, sc1, h,
+        inserted = select_pair_buf<T, L2, CB, 256>(K, I, thr, sc0, sc1, h,
                                               idbase + (uint32_t)(t * TR), nrows - t * TR, cb);
       } else
 #pragma unroll
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     if (t + 1 < ntiles) step(tile1, tnorm1, tile0, tnorm0, t + 1);
   }
   // what is left in the candidate buffer (a wavefront-uniform loop)
-  if constexpr (BUF) flush_buf<T, L2, CB>(K, I, thr, cb);
+  if constexpr (BUF) flush_buf<T, L2, CB, 256>(K, I, thr, cb);
 
   if (MODE != 2 && qvalid) {
     const int nseg = MODE == 0 ? a.nsplit : a.P * (a.nsplit > 1 ? a.nsplit : 1);

@@ -229,15 +229,15 @@ __device__ __forceinline__ float pick32(const float (&sc0)[16], const float (&sc
   return (i & 16) ? b : a;
 }
 
-// A lane's candidate buffer: B entries in LDS at stride 256 (entry e of the
-// lane at slot[256 e]; the workgroup's 256 lanes side by side), each the
+// A lane's candidate buffer: B entries in LDS at stride S (entry e of the
+// lane at slot[S e]; the workgroup's S lanes side by side), each the
 // candidate's key (high word) and id.  Candidates that pass the lane's
 // threshold are appended (about 45 instructions an iteration) instead of
 // being inserted into the sorted list (a T-slot insertion each); the buffer
 // is merged into the list when some lane of the wavefront has B entries, or
 // at the end, so that the insertions of many tiles run in the same
 // iterations across the wavefront's lanes.
-template <int B>
+template <int B, int S>
 struct CandBuf {
   uint64_t* slot;  // this lane's entry 0
   int cnt = 0;
@@ -247,13 +247,13 @@ struct CandBuf {
 // Merges a lane's buffer into its list in append (increasing id) order and
 // raises the lane's own filter; the loop runs as often as the fullest
 // lane's buffer needs.
-template <int T, bool HALF, int B>
+template <int T, bool HALF, int B, int S>
 __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
-                                          CandBuf<B>& cb) {
+                                          CandBuf<B, S>& cb) {
 #pragma unroll
   for (int e = 0; e < B; ++e) {
     if (__builtin_amdgcn_ballot_w64(e < cb.cnt) == 0) break;
-    const uint64_t v = e < cb.cnt ? cb.slot[256 * e] : 0ull;
+    const uint64_t v = e < cb.cnt ? cb.slot[S * e] : 0ull;
     stream_insert<T>(K, I, (uint32_t)(v >> 32), (uint32_t)v);
   }
   cb.cnt = 0;
@@ -263,10 +263,10 @@ __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], fl
 // select_pair with the candidate buffer: the same filter and the same lists
 // once the buffer is flushed.  Returns whether the list changed (a flush
 // took place), which is when the lane's shared-bound key may have risen.
-template <int T, bool HALF, int B>
+template <int T, bool HALF, int B, int S>
 __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                                 const float (&sc0)[16], const float (&sc1)[16],
-                                                int h, uint32_t id0, int lim, CandBuf<B>& cb) {
+                                                int h, uint32_t id0, int lim, CandBuf<B, S>& cb) {
   float mx0 = fmaxf(fmaxf(sc0[0], sc0[1]), sc0[2]), mx1 = fmaxf(fmaxf(sc1[0], sc1[1]), sc1[2]);
 #pragma unroll
   for (int i = 3; i < 15; i += 2) {
@@ -289,7 +289,7 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
   bool flushed = false;
   while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
     if (__builtin_amdgcn_ballot_w64(cb.cnt == B) != 0) {
-      flush_buf<T, HALF, B>(K, I, thr, cb);
+      flush_buf<T, HALF, B, S>(K, I, thr, cb);
       flushed = true;
     }
     if (pm) {
@@ -297,7 +297,7 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
       const float x = HALF ? 2.0f * pick32(sc0, sc1, i) : pick32(sc0, sc1, i);
       const int j = i & 15;
       const int m = (i & 16 ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
-      cb.slot[256 * cb.cnt] = ((uint64_t)key_nz(x) << 32) | (uint32_t)(id0 + m);
+      cb.slot[S * cb.cnt] = ((uint64_t)key_nz(x) << 32) | (uint32_t)(id0 + m);
       ++cb.cnt;
       pm &= pm - 1u;
     }
