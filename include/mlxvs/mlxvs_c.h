@@ -188,8 +188,11 @@ MLXVS_C_API int mlxvs_ivf_flat_search(
     float* distances);
 
 /** mlxvs_ivf_flat_search with every array in device memory, enqueued on
- * stream (a hipStream_t); returns once the results are written (the search
- * reads the probes back to the host to group them by list). */
+ * stream (a hipStream_t).  It reads the offsets back to the host first (a
+ * copy and a wait); with k <= 16 the work items are then planned on the
+ * device and the call returns once the work is enqueued, with k > 16 it also
+ * reads the probes back to group them by list and returns once the results
+ * are written. */
 MLXVS_C_API int mlxvs_ivf_flat_search_device(
     const float* centers,
     int64_t lists,

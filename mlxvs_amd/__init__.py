@@ -141,6 +141,14 @@ def _rows(x, name: str, op: str) -> np.ndarray:
     return a
 
 
+def _host_stream(stream, op: str, device_fn: str) -> None:
+    """Host-array calls run on the null stream; a caller's stream is refused
+    rather than ignored (the *_device entry points take one)."""
+    if stream not in (None, 0):
+        raise ValueError(f"[{op}] host arrays are copied on the null stream; use {device_fn} "
+                         "to run on a stream")
+
+
 def _ptr(a: np.ndarray):
     return a.ctypes.data_as(ctypes.c_void_p)
 
@@ -155,10 +163,12 @@ def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stre
     ``(ids int32 [nq, k], distances float32 [nq, k])``, nearest first:
     squared L2 ascending, otherwise similarity descending; -1 / +-inf where
     fewer than k rows exist.  ``tile_rows`` is accepted for compatibility
-    (the result does not depend on it); ``stream`` is a hipStream_t handle
-    (int) or None.
+    (the result does not depend on it).  ``stream`` must be None or 0: the
+    host arrays go through the null stream (``brute_force_knn_device`` runs
+    on a given hipStream_t).
     """
     op = "mlxvs::brute_force_knn"
+    _host_stream(stream, op, "brute_force_knn_device")
     b = _rows(base, "base", op)
     q = _rows(queries, "queries", op)
     if b.shape[1] != q.shape[1]:
@@ -187,8 +197,10 @@ def hamming_knn(rows, queries, k, *, stream=None):
     ``rows`` uint8 [n, bytes] (as numpy.packbits), ``queries`` uint8
     [nq, bytes], k <= 256.  Returns ``(ids int32, distances float32)``
     [nq, k], nearest first, lowest id first among equal distances.
+    ``stream`` must be None or 0 (``hamming_knn_device`` takes a stream).
     """
     op = "mlxvs::hamming_knn"
+    _host_stream(stream, op, "hamming_knn_device")
     r = np.asarray(rows)
     q = np.asarray(queries)
     if r.ndim != 2 or r.dtype != np.uint8 or q.ndim != 2 or q.dtype != np.uint8:
@@ -243,8 +255,10 @@ def kmeans_predict(x, centroids, m=1, *, tile_rows=65536, stream=None):
     both are, else float32), ``1 <= m <= clusters`` (at most 256 here).
     Squared L2 with the lowest centroid index first among equal distances
     (the reference's argmin for m = 1).  Returns int32 ``[n, m]``.
+    ``stream`` must be None or 0 (host arrays, the null stream).
     """
     op = "mlxvs::kmeans_predict"
+    _host_stream(stream, op, "brute_force_knn_device")
     xa = _rows(x, "x", op)
     ca = _rows(centroids, "centroids", op)
     if xa.shape[1] != ca.shape[1]:

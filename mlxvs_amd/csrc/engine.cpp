@@ -29,6 +29,7 @@
 
 #include "knn_kernels.h"
 #include "mlxvs/mlxvs.hpp"
+#include "plan.h"
 
 namespace mlxvs {
 namespace {
@@ -888,6 +889,13 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   hipStream_t s = ss.stream();
   const bool l2 = metric == kern::kL2;
   const float pad = l2 ? INFINITY : -INFINITY;
+  // (query, probe) pairs are numbered in int32 by the plan and the kernels
+  if (nq * P >= (int64_t(1) << 31))
+    invalid("mlxvs::ivf_flat_search", "too many (query, probe) pairs: nq * n_probes must be below 2^31.");
+  // the longest list: a workgroup's rows must fit one 32-bit buffer range
+  int64_t maxlen = 0;
+  for (int64_t l = 0; l < lists; ++l)
+    maxlen = std::max<int64_t>(maxlen, off[(size_t)l + 1] - off[(size_t)l]);
   // fp32 operands with a row length that is a multiple of 4 floats (zero
   // padded copies when d is not, or a pointer is not 16-byte aligned)
   const int ld = round_up(d, 4);
@@ -937,17 +945,20 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
 
   const int T = list_len_float(k);
   std::vector<int> order;  // host arrays copied from live until the last wait
+  // A small batch has few items (about one per list it probes): the lists'
+  // rows are then cut into parts of about 128 rows or more, a workgroup
+  // each, for about 4,096 workgroups.  Items expected: the lists that np
+  // random probes hit, lists (1 - e^(-np / lists)), plus np / 128.  Lists
+  // longer than a buffer range takes are cut into as many parts as they need.
+  const int64_t avg_rows = n / std::max<int64_t>(1, lists);
+  const double npairs = (double)nq * P;
+  const double est = (double)lists * (1.0 - std::exp(-npairs / (double)lists)) + npairs / 128;
+  const int rs = plan::ivf_row_parts(
+      (int)std::clamp<int64_t>((int64_t)(4096.0 / std::max(1.0, est)), 1,
+                               std::clamp<int64_t>(avg_rows / 128, 1, 64)),
+      maxlen, ld);
   if (k <= T && kern::fused_supported(ld, T, false) &&
-      2 * (int64_t)P * T <= kern::kMaxMergeCandidates) {
-    // A small batch has few items (about one per list it probes): the
-    // lists' rows are then cut into parts of about 128 rows or more, a
-    // workgroup each, for about 4,096 workgroups.  Items expected: the lists
-    // that np random probes hit, lists (1 - e^(-np / lists)), plus np / 128.
-    const int64_t avg_rows = n / std::max<int64_t>(1, lists);
-    const double npairs = (double)nq * P;
-    const double est = (double)lists * (1.0 - std::exp(-npairs / (double)lists)) + npairs / 128;
-    const int rs = (int)std::clamp<int64_t>((int64_t)(4096.0 / std::max(1.0, est)), 1,
-                                            std::clamp<int64_t>(avg_rows / 128, 1, 64));
+      2 * (int64_t)P * T <= kern::kMaxMergeCandidates && rs > 0) {
     // fused: per-lane lists over every (query, probe) pair, then the merge.
     // The work items are planned on the device from the probes (no copy to
     // the host and no wait), the lists longest first.
@@ -1026,9 +1037,12 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
       launch(s, "prep", [&] { return kern::launch_fill_f32(S, cnt * width, -INFINITY, s); });
       kern::FusedArgs fa{kd, kq, bnorm, n, (int)nq, ld, km, 0, 0, 4, k, nullptr, nullptr, 0, 0,
                          0, 0, ditems, dpairs, offsets, dslots, P, it.n, S, width, (int)q0};
+      // whole lists per workgroup: the fused kernel when the longest fits
+      // its 32-bit buffer range, else the VALU kernel (64-bit indexing)
+      const bool fused = kern::fused_supported(ld, 4, false) &&
+                         maxlen <= plan::rows_per_range(ld);
       launch(s, "ivf_scan", [&] {
-        return kern::fused_supported(ld, 4, false) ? kern::launch_ivf_scores(fa, s)
-                                                   : kern::launch_ivf_scores_any(fa, s);
+        return fused ? kern::launch_ivf_scores(fa, s) : kern::launch_ivf_scores_any(fa, s);
       });
       kern::SelectArgs se{S, width, cnt, k, qsel + q0, metric, qnorm, 0, ids, dists};
       launch(s, "select", [&] { return kern::launch_select(se, s); });
@@ -1280,7 +1294,9 @@ Neighbors ivf_flat_search(const IvfFlatIndexView& index, const Rows& queries, in
   const float* dd = index.n ? (const float*)upload(ar, s, Rows{index.data, index.n, d, Dtype::Float32})
                             : nullptr;
   const float* dq = (const float*)upload(ar, s, queries);
-  int32_t* di = to_device(ar, s, std::vector<int32_t>(index.indices, index.indices + index.n));
+  // (int32 ids: 4-byte elements, as Float32)
+  int32_t* di = index.n ? (int32_t*)upload(ar, s, Rows{index.indices, index.n, 1, Dtype::Float32})
+                        : ar.take<int32_t>(1);
   int32_t* doff = to_device(ar, s, off);
   int32_t* ids = ar.take<int32_t>((size_t)nq * k);
   float* dists = ar.take<float>((size_t)nq * k);

@@ -73,6 +73,17 @@ def test_c_program_against_the_header(tmp_path):
     assert "all tests passed" in r.stdout
 
 
+def test_ivf_range_planning(tmp_path):
+    # the IVF-Flat scan's row parts keep every workgroup inside one 32-bit
+    # buffer range (host arithmetic, mlxvs_amd/csrc/plan.h)
+    exe = tmp_path / "plan_check"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror",
+                    f"-I{ROOT / 'mlxvs_amd' / 'csrc'}", str(ROOT / "tests" / "c" / "plan_check.cpp"),
+                    "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and "all tests passed" in r.stdout, r.stdout + r.stderr
+
+
 def test_python_argument_errors(engine):
     with pytest.raises(ValueError, match="same number of columns"):
         engine.brute_force_knn(np.zeros((4, 3)), np.zeros((2, 5)), 1)
@@ -90,6 +101,11 @@ def test_python_argument_errors(engine):
         engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 0)
     with pytest.raises(ValueError, match="1 <= k <= 255"):
         engine.all_neighbors(np.zeros((4, 3), np.float32), 300)
+    # a stream given to a host-array call is refused, not ignored
+    with pytest.raises(ValueError, match="brute_force_knn_device"):
+        engine.brute_force_knn(np.zeros((4, 3)), np.zeros((2, 3)), 1, stream=12345)
+    with pytest.raises(ValueError, match="hamming_knn_device"):
+        engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 1, stream=7)
     # topk_merge: the reference's checks and messages (src/knn.cpp:46-54)
     with pytest.raises(ValueError, match=r"scores must be float32 \[nq, t\]"):
         engine.topk_merge(np.zeros((2, 3), np.float64), None, None, 0, True, 1)
