@@ -191,29 +191,10 @@ class Arena {
     }
   }
 
-  // Pinned host memory for small device-to-host reads (the merge's flags),
-  // kept across calls; a copy into pageable memory goes through a staged,
-  // slower path.
-  int* host_ints(size_t count) {
-    if (fixed_) invalid(op_, "this call would read the merge flags back to the host.");
-    if (count > host_count_) {
-      if (host_) (void)hipHostFree(host_);
-      host_ = nullptr;
-      host_count_ = 0;
-      check_hip(hipHostMalloc((void**)&host_, count * sizeof(int), hipHostMallocDefault),
-                "hipHostMalloc");
-      host_count_ = count;
-    }
-    return host_;
-  }
-
   void release() {
     if (done_) (void)hipEventSynchronize(done_);
     for (auto& c : chunks_) (void)hipFree(c.ptr);
     chunks_.clear();
-    if (host_) (void)hipHostFree(host_);
-    host_ = nullptr;
-    host_count_ = 0;
   }
 
  private:
@@ -224,8 +205,6 @@ class Arena {
   };
   std::vector<Chunk> chunks_;
   hipEvent_t done_ = nullptr;
-  int* host_ = nullptr;
-  size_t host_count_ = 0;
   bool fixed_ = false;
   const char* op_ = "";
 };
@@ -391,18 +370,6 @@ struct FloatInputs {
 
 // Exhaustive exact k-NN for the queries listed in qsel (device ints), on
 // fp32 rows of stride ld.
-// Queries whose merge flag is set (the flags array has nq entries).
-std::vector<int> flagged(Arena& ar, hipStream_t s, const int* flags, int64_t nq) {
-  int* hflags = ar.host_ints((size_t)nq);
-  std::vector<int> redo;
-  check_hip(hipMemcpyAsync(hflags, flags, sizeof(int) * nq, hipMemcpyDeviceToHost, s),
-            "hipMemcpyAsync");
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-  for (int64_t i = 0; i < nq; ++i)
-    if (hflags[i]) redo.push_back((int)i);
-  return redo;
-}
-
 void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
                       const float* queries, int ld, const float* bnorm,
                       const float* qnorm, int64_t n, int d, int metric,
@@ -669,24 +636,16 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   merge_lists(ar, s, part, nseg, T, k, nq, metric, qnorm, 0, ids, dists, flags);
   if (T >= k) return;
 
-  // k > T: queries whose lists may have dropped a member go exhaustive.
-  const std::vector<int> redo = flagged(ar, s, flags, nq);
-  if (redo.empty()) return;
+  // k > T: the queries whose lists may have dropped a member are redone on
+  // the device (the merge's flags never travel to the host)
   if (l2 && use_stream) {
-    // the streamed scan summed its row norms itself; the exhaustive path
-    // reads them
+    // the streamed scan summed its row norms itself; the redo reads them
     kern::PrepArgs pb{in.base, n, d, d, f16, bnorm, nullptr, nullptr, 0, 0, 1};
     launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
   }
-  const float *eb, *eq;
-  fp32_rows(kbase, n, &eb);
-  fp32_rows(kq, nq, &eq);
-  int* qsel = ar.take<int>(redo.size());
-  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
-            "hipMemcpyAsync");
-  exhaustive_float(ar, s, eb, eq, kld, bnorm, qnorm, n, d, metric, qsel, (int)redo.size(), k,
-                   ids, dists);
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  kern::RedoArgs ra{kbase, kq, l2 ? bnorm : nullptr, qnorm, flags, n, (int)nq, kld, kld,
+                    kf16 ? 1 : 0, 0, metric, 0, k, ids, dists};
+  launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
 }
 
 // ---- Hamming path --------------------------------------------------------------------
@@ -775,8 +734,10 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   int* flags = T < k ? ar.take<int>((size_t)nq) : nullptr;
   merge_lists(ar, s, part, nseg, T, k, nq, kern::kL2, qpop, 0, ids, dists, flags);
   if (T >= k) return true;
-  const std::vector<int> redo = flagged(ar, s, flags, nq);
-  if (!redo.empty()) hamming_exhaustive(ar, s, bw, qw, ldw, n, redo, k, ids, dists);
+  // flagged queries redone on the device over the packed words
+  kern::RedoArgs ra{bw, qw, nullptr, nullptr, flags, n, (int)nq, ldw, ldw, 0, 1, kern::kL2, 1,
+                    k, ids, dists};
+  launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
   return true;
 }
 
@@ -813,8 +774,10 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
                        nullptr};
     launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
     if (T >= k) return;
-    redo = flagged(ar, s, flags, nq);
-    if (redo.empty()) return;
+    kern::RedoArgs ra{bw, qw, nullptr, nullptr, flags, n, (int)nq, Wp, Wp, 0, 1, kern::kL2, 1,
+                      k, ids, dists};
+    launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
+    return;
   } else {
     redo.resize((size_t)nq);
     for (int64_t i = 0; i < nq; ++i) redo[(size_t)i] = (int)i;

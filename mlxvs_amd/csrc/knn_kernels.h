@@ -354,6 +354,33 @@ struct TopkMergeArgs {
 };
 hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s);
 
+// Exhaustive redo of the queries the merge flagged (flags[q] != 0; all when
+// flags is null), on the device: each is scored against every row and its
+// best k written to ids / dists in the output order, as the select path
+// would.  Float rows: scores q.b, or 2 (q.b + bnorm) for L2, over the first
+// d of ld values (binary16 when f16); words: Hamming over packed uint32
+// words (d words of row stride ld), score -popcount, distances with
+// dist_mode 1.
+struct RedoArgs {
+  const void* base;      // [n][ld] rows
+  const void* queries;   // [nq][ld]
+  const float* bnorm;    // [n] -|b|^2 / 2 (L2 float) else null
+  const float* qnorm;    // [nq] |q|^2 (L2 float, dist_mode 0) else null
+  const int* flags;      // [nq] or null
+  int64_t n;
+  int nq;
+  int ld;
+  int d;
+  int f16;
+  int words;             // packed Hamming words instead of float rows
+  int metric;
+  int dist_mode;         // 0 float metric, 1 Hamming
+  int k;
+  int32_t* ids;          // [nq][k]
+  float* dists;          // [nq][k] (may be null)
+};
+hipError_t launch_redo(const RedoArgs& a, hipStream_t s);
+
 // Device scratch of the no-allocation entry point (scratch.hip): a fixed
 // array of kScratchBytes per GPU, held until the process ends.  Returns its
 // device address on the current device (hipGetSymbolAddress on the first

@@ -388,6 +388,192 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(TopkMergeArgs a) {
   }
 }
 
+// ---- exhaustive redo of flagged queries ---------------------------------------
+//
+// When lists shorter than k fed the merge (k > T), a query whose full list's
+// last entry made its best k may have lost a member; the merge flags it.
+// This kernel redoes those queries on the device, so no flag travels to the
+// host: a persistent grid walks the flags, and for each flagged query a
+// workgroup scores every row (VALU dot products, or popcounts of XORed
+// words) in chunks of 4,096 and keeps the best k exactly as topk_merge does
+// (a lower bound from the chunk's wavefront maxima, candidates at or above
+// it in LDS, radix selection of the 64-bit ranks).  Flagged queries are
+// rare, so the rows are read per query.
+
+// Scores of one query against rows: score(j) and the row count.
+struct FloatScorer {
+  const void* base;
+  const void* query;
+  const float* bnorm;  // -|b|^2 / 2 (L2) or null
+  int ld, d, f16;
+  __device__ __forceinline__ float operator()(int64_t j) const {
+    float acc = 0.0f;
+    if (f16) {
+      const _Float16* b = (const _Float16*)base + j * ld;
+      const _Float16* qv = (const _Float16*)query;
+      for (int c = 0; c < d; ++c) acc += (float)qv[c] * (float)b[c];
+    } else {
+      const float* b = (const float*)base + j * ld;
+      const float* qv = (const float*)query;
+      for (int c = 0; c < d; ++c) acc += qv[c] * b[c];
+    }
+    // L2: 2 (q.b - |b|^2 / 2) = 2 q.b - |b|^2, reference src/knn.cpp:114-115
+    return bnorm ? 2.0f * (acc + bnorm[j]) : acc;
+  }
+};
+struct HammingScorer {
+  const uint32_t* base;
+  const uint32_t* query;
+  int ldw, w;
+  __device__ __forceinline__ float operator()(int64_t j) const {
+    const uint32_t* b = base + j * ldw;
+    uint32_t acc = 0;
+    for (int c = 0; c < w; ++c) acc += __popc(query[c] ^ b[c]);
+    return -(float)acc;
+  }
+};
+
+template <typename Scorer>
+__global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
+  constexpr int NT = 256, PER = 16, NW = NT / 64;
+  constexpr int64_t CHUNK = (int64_t)NT * PER;
+  __shared__ uint64_t buf[kCandCap];
+  __shared__ uint64_t tmp[kMaxK];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wbound[NW];
+  __shared__ PickState st;
+  __shared__ int s_cnt;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int k = a.k;
+  const int keff = (int)(a.n < k ? a.n : k);
+  for (int q = blockIdx.x; q < a.nq; q += gridDim.x) {
+    if (a.flags && !a.flags[q]) continue;  // uniform in the workgroup
+    if constexpr (std::is_same<Scorer, FloatScorer>::value)
+      sc.query = (const char*)a.queries + (int64_t)q * sc.ld * (sc.f16 ? 2 : 4);
+    else
+      sc.query = (const uint32_t*)a.queries + (int64_t)q * sc.ldw;
+    if (tid == 0) s_cnt = 0;
+    uint32_t L = 1;
+    int64_t seen = 0;
+    bool overflow = false;
+    __syncthreads();
+    for (int64_t c0 = 0; c0 < a.n; c0 += CHUNK) {
+      const int64_t valid = a.n - c0 < CHUNK ? a.n - c0 : CHUNK;
+      uint32_t key[PER];
+      uint32_t mx = 0;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int64_t c = (int64_t)e * NT + tid;
+        key[e] = c < valid ? key_nz(sc(c0 + c)) : 0u;
+        mx = max(mx, key[e]);
+      }
+      // the chunk's bound (see topk_merge_kernel)
+      const int j = (k + NW - 1) / NW;
+      const uint32_t lw = __shfl(wave_sort_desc(mx, lane), j - 1);
+      if (lane == 0) wbound[w] = lw;
+      __syncthreads();
+      const int cnt0 = s_cnt;
+      if (cnt0 > kCandCap) {
+        overflow = true;
+        break;
+      }
+      const int want0 = (int)(seen < k ? seen : k);
+      if (cnt0 > kCandCap / 2) {
+        auto visit = [&](auto f) {
+          for (int i = tid; i < cnt0; i += NT) f(buf[i]);
+        };
+        radix_pick<NT>(visit, want0, hist, st);
+        radix_gather(visit, st, tmp);
+        __syncthreads();
+        for (int i = tid; i < want0; i += NT) buf[i] = tmp[i];
+        if (tid == 0) s_cnt = want0;
+        if (want0 == k) L = max(L, (uint32_t)((st.prefix & st.mask) >> 32));
+        __syncthreads();
+      }
+      uint32_t lc = 0xffffffffu;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) lc = min(lc, wbound[i]);
+      L = max(L, max(lc, 1u));
+      seen += valid;
+      if (__builtin_amdgcn_ballot_w64(mx >= L) != 0) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const bool p = key[e] >= L;
+          const uint64_t b = __builtin_amdgcn_ballot_w64(p);
+          if (b == 0) continue;
+          const int leader = __builtin_ctzll(b);
+          uint32_t base = 0;
+          if (lane == leader) base = atomicAdd((uint32_t*)&s_cnt, (uint32_t)__builtin_popcountll(b));
+          base = __shfl(base, leader);
+          if (p) {
+            const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi(
+                                            (uint32_t)(b >> 32),
+                                            __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            const uint32_t id = (uint32_t)(c0 + (int64_t)e * NT + tid);
+            if (pos < (uint32_t)kCandCap) buf[pos] = ((uint64_t)key[e] << 32) | (uint32_t)(~id);
+          }
+        }
+      }
+      __syncthreads();  // the wbound words and the appends, before the next chunk
+    }
+    if (!overflow) overflow = s_cnt > kCandCap;
+    if (overflow) {
+      // many equal keys at the bound: every row again, selected directly
+      __syncthreads();
+      auto visit = [&](auto f) {
+        for (int64_t c = tid; c < a.n; c += NT)
+          f(((uint64_t)key_nz(sc(c)) << 32) | (uint32_t)(~(uint32_t)c));
+      };
+      radix_pick<NT>(visit, keff, hist, st);
+      radix_gather(visit, st, tmp);
+      __syncthreads();
+      for (int i = tid; i < keff; i += NT) buf[i] = tmp[i];
+      __syncthreads();
+    } else {
+      const int cnt = s_cnt;
+      if (cnt > keff) {
+        auto visit = [&](auto f) {
+          for (int i = tid; i < cnt; i += NT) f(buf[i]);
+        };
+        radix_pick<NT>(visit, keff, hist, st);
+        radix_gather(visit, st, tmp);
+        __syncthreads();
+        for (int i = tid; i < keff; i += NT) buf[i] = tmp[i];
+        __syncthreads();
+      }
+    }
+    // the output order, then distances (emit_topk's conventions)
+    const int P = pow2_at_least(keff > 1 ? keff : 1);
+    for (int i = keff + tid; i < P; i += NT) buf[i] = 0;
+    __syncthreads();
+    bitonic_desc<NT>(buf, P, OutputOrder{});
+    const bool l2 = a.metric == kL2;
+    const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
+    for (int i = tid; i < k; i += NT) {
+      const uint64_t r = i < keff ? buf[i] : 0ull;
+      const int64_t o = (int64_t)q * k + i;
+      if (r == 0) {
+        a.ids[o] = -1;
+        if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
+        continue;
+      }
+      a.ids[o] = id_of_rank(r);
+      const float sv = score_of_key((uint32_t)(r >> 32));
+      if (a.dists) {
+        if (a.dist_mode == 1) {
+          a.dists[o] = -sv;
+        } else if (l2) {
+          const float v = qn - sv;  // reference src/knn.cpp:126-129
+          a.dists[o] = v > 0.0f ? v : 0.0f;
+        } else {
+          a.dists[o] = sv;
+        }
+      }
+    }
+    __syncthreads();  // buf and s_cnt are reused by the next query
+  }
+}
+
 template <int NT, int PER>
 hipError_t topk_inst(TopkMergeArgs a, bool vec, hipStream_t s) {
   // rows per launch: the grid's work-items stay below 2^32
@@ -406,6 +592,21 @@ hipError_t topk_inst(TopkMergeArgs a, bool vec, hipStream_t s) {
 }
 
 }  // namespace
+
+hipError_t launch_redo(const RedoArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.n <= 0) return hipSuccess;
+  if (a.k < 1 || a.k > kMaxK) return hipErrorInvalidValue;
+  // a persistent grid: about four workgroups per CU walk the flags
+  const unsigned g = (unsigned)std::min<int64_t>(a.nq, 1024);
+  if (a.words) {
+    HammingScorer sc{(const uint32_t*)a.base, nullptr, a.ld, a.d};
+    hipLaunchKernelGGL((redo_kernel<HammingScorer>), dim3(g), dim3(256), 0, s, a, sc);
+  } else {
+    FloatScorer sc{a.base, nullptr, a.bnorm, a.ld, a.d, a.f16};
+    hipLaunchKernelGGL((redo_kernel<FloatScorer>), dim3(g), dim3(256), 0, s, a, sc);
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s) {
   if (a.nq <= 0) return hipSuccess;
