@@ -80,9 +80,9 @@ MLXVS_API void brute_force_knn_device(const Rows& base, const Rows& queries, int
  * fixed device array of 64 MiB per GPU that the library holds until the
  * process ends (no hipMalloc, hipFree or allocating call).  No counterpart
  * in the reference: for callers that cannot allocate (graph capture,
- * serving loops).  Sizes whose workspace exceeds the array, k > 16 and
- * shapes the fused kernels do not take are rejected with invalid_argument
- * before anything is enqueued.  Calls that overlap on one GPU share the
+ * serving loops).  Sizes whose workspace exceeds the array and shapes the
+ * fused kernels do not take are rejected with invalid_argument before
+ * anything is enqueued.  Calls that overlap on one GPU share the
  * array and race.
  */
 MLXVS_API void brute_force_knn_device_noalloc(const Rows& base, const Rows& queries, int k,

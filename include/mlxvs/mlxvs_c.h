@@ -236,9 +236,9 @@ MLXVS_C_API int mlxvs_brute_force_knn_device(
  * capture, serving loops, harnesses that forbid allocation).  Its
  * workspace (norms, per-lane lists, bounds, merge levels) is a fixed device
  * array of 64 MiB on each GPU the library runs on, held until the process
- * ends; the call itself allocates nothing.  Limits: k <= 16, a workspace of
- * at most 64 MiB (about 10,000 queries against 1,000,000 rows of 128 dims
- * at k = 10) and shapes the fused kernels take; anything else returns
+ * ends; the call itself allocates nothing.  Limits: a workspace of at most
+ * 64 MiB (about 10,000 queries against 1,000,000 rows of 128 dims at
+ * k = 10) and shapes the fused kernels take; anything else returns
  * MLXVS_ERROR_INVALID_ARGUMENT before any work is enqueued.  Enqueued on
  * stream, returns without waiting.  Calls that overlap on one GPU share the
  * array and race: order them (one stream, or events).
