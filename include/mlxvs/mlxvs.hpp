@@ -150,7 +150,9 @@ struct IvfFlatIndexView {
 MLXVS_API Neighbors ivf_flat_search(const IvfFlatIndexView& index, const Rows& queries, int k,
                                     int n_probes = 20, void* stream = nullptr);
 /** ivf_flat_search on device pointers (queries [nq, index.d] float32); writes
- * device ids / distances [nq, k] (distances may be null). */
+ * device ids / distances [nq, k] (distances may be null) and returns once
+ * the work is enqueued.  The offsets are read on the device only (not
+ * checked: they must run from 0 to n without decreasing). */
 MLXVS_API void ivf_flat_search_device(const IvfFlatIndexView& index, const float* queries,
                                       int64_t nq, int k, int n_probes, int32_t* ids,
                                       float* distances, void* stream = nullptr);

@@ -24,7 +24,11 @@
  * Device-pointer variants (suffix _device) take pointers to device memory
  * (hipMalloc'ed on the current HIP device) and a hipStream_t passed as
  * void* (NULL = the null stream).  They enqueue all work on that stream and
- * return without waiting, except where the text says that they synchronise.
+ * return without waiting for it: every step, including the exhaustive
+ * search of the queries a merge flags, is decided on the device.  Calls on
+ * one device plan their work one at a time (a per-device lock, held only
+ * while a call enqueues), and a call's work is ordered after the previous
+ * call's on that device, whatever the streams.
  */
 #ifndef MLXVS_C_H
 #define MLXVS_C_H
@@ -188,11 +192,9 @@ MLXVS_C_API int mlxvs_ivf_flat_search(
     float* distances);
 
 /** mlxvs_ivf_flat_search with every array in device memory, enqueued on
- * stream (a hipStream_t).  It reads the offsets back to the host first (a
- * copy and a wait); with k <= 16 the work items are then planned on the
- * device and the call returns once the work is enqueued, with k > 16 it also
- * reads the probes back to group them by list and returns once the results
- * are written. */
+ * stream (a hipStream_t); returns without waiting.  The work is planned on
+ * the device from the probes and the offsets, which are not read on the
+ * host and so not checked: they must run from 0 to n without decreasing. */
 MLXVS_C_API int mlxvs_ivf_flat_search_device(
     const float* centers,
     int64_t lists,
@@ -213,9 +215,8 @@ MLXVS_C_API int mlxvs_ivf_flat_search_device(
 /**
  * mlxvs_brute_force_knn on device memory: base [n, d] and queries [nq, d]
  * float32 (f16 == 0) or binary16 (f16 != 0), outputs ids / distances
- * [nq, k] in device memory (distances may be NULL).  Enqueued on stream.
- * Synchronises with stream only when k > 16 (the merge step then checks on
- * the host whether a query needs the exhaustive select).
+ * [nq, k] in device memory (distances may be NULL).  Enqueued on stream;
+ * returns without waiting.
  */
 MLXVS_C_API int mlxvs_brute_force_knn_device(
     const void* base,

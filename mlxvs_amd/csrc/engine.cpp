@@ -209,27 +209,52 @@ class Arena {
   const char* op_ = "";
 };
 
-std::mutex g_mutex;
-std::map<int, std::unique_ptr<Arena>> g_arenas;
+// One arena per device, with a lock of its own: a call holds it while it
+// plans and enqueues its work (and only then), so calls on other devices,
+// or calls that are waiting on the host for their results, do not wait.
+struct DeviceWorkspace {
+  std::mutex lock;
+  std::unique_ptr<Arena> arena;
+};
+std::mutex g_workspaces_lock;  // guards the map only
+std::map<int, std::unique_ptr<DeviceWorkspace>> g_workspaces;
 
-// Holds the device's arena for the duration of one call, or a caller's
-// fixed arena (no lock, no ordering with other calls, no allocation).
+DeviceWorkspace& device_workspace(int dev) {
+  std::lock_guard<std::mutex> g(g_workspaces_lock);
+  auto& w = g_workspaces[dev];
+  if (!w) w = std::make_unique<DeviceWorkspace>();
+  return *w;
+}
+
+// Holds the current device's arena while one call plans and enqueues its
+// work, or a caller's fixed arena (no lock, no ordering with other calls,
+// no allocation).  close() (or the end of the call) records the arena's
+// event after the work enqueued so far and releases the lock; the next call
+// on any stream is ordered after that work.
 class Session {
  public:
-  explicit Session(hipStream_t s) : lock_(g_mutex), stream_(s) {
-    int dev = current_device();
-    auto& slot = g_arenas[dev];
-    if (!slot) slot = std::make_unique<Arena>();
-    arena_ = slot.get();
+  explicit Session(hipStream_t s) : stream_(s) {
+    DeviceWorkspace& w = device_workspace(current_device());
+    lock_ = std::unique_lock<std::mutex>(w.lock);
+    if (!w.arena) w.arena = std::make_unique<Arena>();
+    arena_ = w.arena.get();
     arena_->begin(s);
   }
   Session(hipStream_t s, Arena& fixed) : stream_(s), arena_(&fixed) {}
   ~Session() {
-    if (arena_->fixed()) return;
+    if (closed_ || arena_->fixed()) return;
     try {
       arena_->end(stream_);
     } catch (...) {
     }
+  }
+  // The end of the arena's use: nothing enqueued after this may read or
+  // write arena memory (a host wait for results may follow).
+  void close() {
+    if (closed_ || arena_->fixed()) return;
+    closed_ = true;
+    std::unique_lock<std::mutex> held = std::move(lock_);
+    arena_->end(stream_);
   }
   Arena& arena() { return *arena_; }
   hipStream_t stream() const { return stream_; }
@@ -238,6 +263,7 @@ class Session {
   std::unique_lock<std::mutex> lock_;
   hipStream_t stream_;
   Arena* arena_ = nullptr;
+  bool closed_ = false;
 };
 
 // ---- planning ------------------------------------------------------------------
@@ -601,14 +627,10 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     const float *eb, *eq;
     fp32_rows(kbase, n, &eb);
     fp32_rows(kq, nq, &eq);
-    std::vector<int> all((size_t)nq);
-    for (int64_t i = 0; i < nq; ++i) all[(size_t)i] = (int)i;
     int* qsel = ar.take<int>((size_t)nq);
-    check_hip(hipMemcpyAsync(qsel, all.data(), sizeof(int) * nq, hipMemcpyHostToDevice, s),
-              "hipMemcpyAsync");
+    launch(s, "prep", [&] { return kern::launch_iota(qsel, nq, s); });
     exhaustive_float(ar, s, eb, eq, kld, bnorm, qnorm, n, d, metric, qsel, (int)nq, k, ids,
                      dists);
-    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // `all` is released next
     return;
   }
 
@@ -650,15 +672,13 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
 
 // ---- Hamming path --------------------------------------------------------------------
 
-// Exact select of the listed queries over all rows, from packed words with
-// row stride `wstride` (queries the fused path cannot finish, or all).
+// Exact select of every query over all rows, from packed words with row
+// stride `wstride` (the route when the fused scan cannot be planned).
 void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint32_t* qw,
-                        int wstride, int64_t n, const std::vector<int>& redo, int k,
-                        int32_t* ids, float* dists) {
-  int* qsel = ar.take<int>(redo.size());
-  check_hip(hipMemcpyAsync(qsel, redo.data(), sizeof(int) * redo.size(), hipMemcpyHostToDevice, s),
-            "hipMemcpyAsync");
-  const int64_t rcount = (int64_t)redo.size();
+                        int wstride, int64_t n, int64_t nq, int k, int32_t* ids, float* dists) {
+  int* qsel = ar.take<int>((size_t)nq);
+  launch(s, "prep", [&] { return kern::launch_iota(qsel, nq, s); });
+  const int64_t rcount = nq;
   const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rcount, (int64_t(1) << 28) / n));
   float* S = ar.take<float>((size_t)per_block * n);
   for (int64_t r0 = 0; r0 < rcount; r0 += per_block) {
@@ -668,7 +688,6 @@ void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint
     kern::SelectArgs se{S, n, cnt, k, qsel + r0, kern::kL2, nullptr, 1, ids, dists};
     launch(s, "select", [&] { return kern::launch_select(se, s); });
   }
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // `redo` is released next
 }
 
 
@@ -764,7 +783,6 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
   launch(s, "pack", [&] { return kern::launch_pack({rows, n, nbytes, bw, wstride}, s); });
   launch(s, "pack", [&] { return kern::launch_pack({queries, nq, nbytes, qw, wstride}, s); });
 
-  std::vector<int> redo;
   if (plan.ok) {
     uint64_t* part = ar.take<uint64_t>((size_t)nq * plan.nsplit * T);
     kern::HammingArgs ha{bw, qw, n, (int)nq, Wp, plan.rows_per_split, plan.nsplit, T, part};
@@ -778,11 +796,8 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
                       k, ids, dists};
     launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
     return;
-  } else {
-    redo.resize((size_t)nq);
-    for (int64_t i = 0; i < nq; ++i) redo[(size_t)i] = (int)i;
   }
-  hamming_exhaustive(ar, s, bw, qw, wstride, n, redo, k, ids, dists);
+  hamming_exhaustive(ar, s, bw, qw, wstride, n, nq, k, ids, dists);
 }
 
 // ---- IVF-Flat list scan ------------------------------------------------------------
@@ -843,9 +858,20 @@ V* to_device(Arena& ar, hipStream_t s, const std::vector<V>& v) {
   return p;
 }
 
-// One search on device pointers; `off` is the host copy of the offsets.
+// One search on device pointers.  `off` is the host copy of the offsets
+// when the caller has one (the host-array entry), else null: the work is
+// then planned from the device offsets alone, and the call enqueues it
+// without waiting.  The fused scan keeps per-lane lists of T = 16 for
+// k > 16 too, with the rows of a list cut into parts small enough that a
+// part rarely holds 16 of a query's best k; the merge flags the queries for
+// which it may have (its full list's last entry made the best k), and those
+// are searched again exhaustively on the device.  When the fused scan does
+// not apply (rows longer than 256 values, very long lists, many probes),
+// the host-array entry groups the probes on the host and scores candidate
+// buffers; the device entry searches every query exhaustively on the
+// device.
 void ivf_search(Session& ss, const float* centers, int64_t lists, const float* data, int64_t n,
-                const int32_t* indices, const int32_t* offsets, const std::vector<int32_t>& off,
+                const int32_t* indices, const int32_t* offsets, const std::vector<int32_t>* off,
                 int d, int metric, const float* queries, int64_t nq, int k, int P,
                 int32_t* ids, float* dists) {
   Arena& ar = ss.arena();
@@ -855,10 +881,12 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   // (query, probe) pairs are numbered in int32 by the plan and the kernels
   if (nq * P >= (int64_t(1) << 31))
     invalid("mlxvs::ivf_flat_search", "too many (query, probe) pairs: nq * n_probes must be below 2^31.");
-  // the longest list: a workgroup's rows must fit one 32-bit buffer range
-  int64_t maxlen = 0;
-  for (int64_t l = 0; l < lists; ++l)
-    maxlen = std::max<int64_t>(maxlen, off[(size_t)l + 1] - off[(size_t)l]);
+  // the longest list (at most n without the host offsets): a workgroup's
+  // rows must fit one 32-bit buffer range
+  int64_t maxlen = off ? 0 : n;
+  if (off)
+    for (int64_t l = 0; l < lists; ++l)
+      maxlen = std::max<int64_t>(maxlen, (*off)[(size_t)l + 1] - (*off)[(size_t)l]);
   // fp32 operands with a row length that is a multiple of 4 floats (zero
   // padded copies when d is not, or a pointer is not 16-byte aligned)
   const int ld = round_up(d, 4);
@@ -907,7 +935,6 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   const kern::Metric km = metric == kern::kCosine ? kern::kInnerProduct : (kern::Metric)metric;
 
   const int T = list_len_float(k);
-  std::vector<int> order;  // host arrays copied from live until the last wait
   // A small batch has few items (about one per list it probes): the lists'
   // rows are then cut into parts of about 128 rows or more, a workgroup
   // each, for about 4,096 workgroups.  Items expected: the lists that np
@@ -916,21 +943,25 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
   const int64_t avg_rows = n / std::max<int64_t>(1, lists);
   const double npairs = (double)nq * P;
   const double est = (double)lists * (1.0 - std::exp(-npairs / (double)lists)) + npairs / 128;
-  const int rs = plan::ivf_row_parts(
-      (int)std::clamp<int64_t>((int64_t)(4096.0 / std::max(1.0, est)), 1,
-                               std::clamp<int64_t>(avg_rows / 128, 1, 64)),
-      maxlen, ld);
-  if (k <= T && kern::fused_supported(ld, T, false) &&
+  int64_t want = std::clamp<int64_t>((int64_t)(4096.0 / std::max(1.0, est)), 1,
+                                     std::clamp<int64_t>(avg_rows / 128, 1, 64));
+  if (k > T) {
+    // k > 16: a part (two lane lists of 16) expects about k / (2 parts) of
+    // a query's best k when they all lie in one list, so k / 8 parts keep
+    // that near 4; lists of fewer rows need fewer parts (a lane list of at
+    // most 16 rows cannot drop one).  The segment lists stay below 4 GiB.
+    int64_t parts = std::min<int64_t>((k + 7) / 8, (avg_rows + 31) / 32);
+    const int64_t per_part = nq * 2 * P * T * (int64_t)sizeof(uint64_t);
+    parts = std::min<int64_t>(parts, std::max<int64_t>(1, (int64_t(4) << 30) / per_part));
+    want = std::max(want, std::clamp<int64_t>(parts, 1, 64));
+  }
+  const int rs = plan::ivf_row_parts((int)want, maxlen, ld);
+  const int64_t np = nq * P;
+  if (kern::fused_supported(ld, T, false) &&
       2 * (int64_t)P * T <= kern::kMaxMergeCandidates && rs > 0) {
     // fused: per-lane lists over every (query, probe) pair, then the merge.
-    // The work items are planned on the device from the probes (no copy to
-    // the host and no wait), the lists longest first.
-    order.resize((size_t)lists);
-    for (int64_t l = 0; l < lists; ++l) order[(size_t)l] = (int)l;
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
-      return off[(size_t)a + 1] - off[(size_t)a] > off[(size_t)b + 1] - off[(size_t)b];
-    });
-    const int64_t np = nq * P;
+    // The work items are planned on the device from the probes and offsets
+    // (no copy to the host and no wait), the lists longest first.
     const int64_t max_items = kern::ivf_plan_max_items(np, lists);
     if (max_items >= (int64_t(1) << 31) / 3) invalid("mlxvs::ivf_flat_search", "too many probes.");
     int* dslots = ar.take<int>((size_t)np);
@@ -942,7 +973,8 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     // a small batch reads few lists: only their rows' norms
     const int64_t nblk = (n + 255) / 256;
     int* need = (l2 && np < lists) ? ar.take<int>((size_t)std::max<int64_t>(nblk, 1)) : nullptr;
-    kern::IvfPlanArgs pa{probes, nq, P, offsets, to_device(ar, s, order), (int)lists, cnt, pos,
+    int* order = ar.take<int>((size_t)lists);
+    kern::IvfPlanArgs pa{probes, nq, P, offsets, order, (int)lists, cnt, pos,
                          dslots, ditems, dpairs, nitems, need, nblk};
     launch(s, "ivf_plan", [&] { return kern::launch_ivf_plan(pa, s); });
     base_norms(need);
@@ -959,11 +991,32 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
                        0, 0, ditems, dpairs, offsets, dslots, P, (int)max_items, nullptr, 0, 0,
                        nitems};
     launch(s, "ivf_scan", [&] { return kern::launch_ivf_select(fa, s); });
-    merge_lists(ar, s, part, nseg, T, k, nq, metric, qnorm, 0, ids, dists, nullptr);
+    int* flags = k > T ? ar.take<int>((size_t)nq) : nullptr;
+    merge_lists(ar, s, part, nseg, T, k, nq, metric, qnorm, 0, ids, dists, flags);
+    if (flags) {
+      // the flagged queries again, over their probed lists' rows (columns out)
+      kern::RedoArgs ra{kd, kq, l2 ? bnorm : nullptr, qnorm, flags, lists, (int)nq, ld, ld, 0, 0,
+                        metric, 0, k, ids, dists, probes, dslots, offsets, P};
+      launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
+    }
+    kern::IvfMapArgs mp{ids, dists, (int)nq, k, nullptr, 0, probes, dslots, offsets, indices, P,
+                        pad};
+    launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
+  } else if (!off) {
+    // device entry, no fused scan: every query over its probed lists' rows
+    base_norms(nullptr);
+    int* dslots = ar.take<int>((size_t)np);
+    kern::IvfPlanArgs pa{probes, nq, P, offsets, nullptr, (int)lists, nullptr, nullptr,
+                         dslots, nullptr, nullptr, nullptr, nullptr, 0};
+    launch(s, "ivf_plan", [&] { return kern::launch_ivf_slots(pa, s); });
+    kern::RedoArgs ra{kd, kq, l2 ? bnorm : nullptr, qnorm, nullptr, lists, (int)nq, ld, ld, 0, 0,
+                      metric, 0, k, ids, dists, probes, dslots, offsets, P};
+    launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
     kern::IvfMapArgs mp{ids, dists, (int)nq, k, nullptr, 0, probes, dslots, offsets, indices, P,
                         pad};
     launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
   } else {
+    const std::vector<int32_t>& hoff = *off;
     base_norms(nullptr);
     std::vector<int32_t> hp((size_t)nq * P);
     check_hip(hipMemcpyAsync(hp.data(), probes, sizeof(int32_t) * hp.size(), hipMemcpyDeviceToHost,
@@ -978,7 +1031,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
       for (int p = 0; p < P; ++p) {
         slots[(size_t)(q * P + p)] = (int32_t)c;
         const int l = hp[(size_t)(q * P + p)];
-        c += off[(size_t)l + 1] - off[(size_t)l];
+        c += hoff[(size_t)l + 1] - hoff[(size_t)l];
       }
       width = std::max(width, c);
     }
@@ -994,7 +1047,7 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
     for (int64_t q0 = 0; q0 < nq; q0 += block) {
       const int64_t q1 = std::min(nq, q0 + block);
       const int cnt = (int)(q1 - q0);
-      const IvfItems it = ivf_items(hp.data(), q0, q1, P, lists, off);
+      const IvfItems it = ivf_items(hp.data(), q0, q1, P, lists, hoff);
       int* ditems = to_device(ar, s, it.items);
       int* dpairs = to_device(ar, s, it.pairs);
       launch(s, "prep", [&] { return kern::launch_fill_f32(S, cnt * width, -INFINITY, s); });
@@ -1012,11 +1065,11 @@ void ivf_search(Session& ss, const float* centers, int64_t lists, const float* d
       kern::IvfMapArgs mp{ids, dists, cnt, k, qsel + q0, 0, probes, dslots, offsets, indices, P,
                           pad};
       launch(s, "ivf_map", [&] { return kern::launch_ivf_map(mp, s); });
-      // the host item lists are released at the end of the iteration
+      // the host item lists (and, last, the slots and query list) are
+      // released after the wait
       check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
     }
   }
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");  // host arrays released next
 }
 
 void ivf_args(const IvfFlatIndexView& ix, int64_t nq, int qd, int k, const char* op) {
@@ -1057,9 +1110,10 @@ const void* upload(Arena& ar, hipStream_t s, const Rows& r) {
   return p;
 }
 
-Neighbors download(Arena& ar, hipStream_t s, const int32_t* ids, const float* dists,
-                   int64_t nq, int k) {
-  (void)ar;
+// The results to the host: the copies are enqueued, the session closed
+// (the lock released), then the host waits for them.
+Neighbors download(Session& ss, const int32_t* ids, const float* dists, int64_t nq, int k) {
+  hipStream_t s = ss.stream();
   Neighbors out;
   out.nq = nq;
   out.k = k;
@@ -1071,6 +1125,7 @@ Neighbors download(Arena& ar, hipStream_t s, const int32_t* ids, const float* di
     check_hip(hipMemcpyAsync(out.distances.data(), dists, sizeof(float) * nq * k,
                              hipMemcpyDeviceToHost, s), "hipMemcpyAsync (distances)");
   }
+  ss.close();
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
   return out;
 }
@@ -1138,7 +1193,7 @@ Neighbors brute_force_knn(const Rows& base, const Rows& queries, int k, Metric m
   float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
   float_knn(ss, {db, dq, base.n, nq, base.d, base.dtype == Dtype::Float16}, k, (int)metric,
             ids, dists);
-  return download(ar, s, ids, dists, nq, k);
+  return download(ss, ids, dists, nq, k);
 }
 
 void brute_force_knn_device(const Rows& base, const Rows& queries, int k, Metric metric,
@@ -1229,6 +1284,7 @@ std::vector<int32_t> kmeans_predict(const Rows& x, const Rows& centroids, int m,
             dists);
   check_hip(hipMemcpyAsync(labels.data(), ids, sizeof(int32_t) * x.n * m, hipMemcpyDeviceToHost,
                            s), "hipMemcpyAsync (labels)");
+  ss.close();
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
   return labels;
 }
@@ -1261,9 +1317,9 @@ Neighbors ivf_flat_search(const IvfFlatIndexView& index, const Rows& queries, in
   int32_t* doff = to_device(ar, s, off);
   int32_t* ids = ar.take<int32_t>((size_t)nq * k);
   float* dists = ar.take<float>((size_t)nq * k);
-  ivf_search(ss, dc, index.lists, dd, index.n, di, doff, off, d, (int)index.metric, dq, nq, k, P,
+  ivf_search(ss, dc, index.lists, dd, index.n, di, doff, &off, d, (int)index.metric, dq, nq, k, P,
              ids, dists);
-  return download(ar, s, ids, dists, nq, k);
+  return download(ss, ids, dists, nq, k);
 }
 
 void ivf_flat_search_device(const IvfFlatIndexView& index, const float* queries, int64_t nq,
@@ -1272,17 +1328,13 @@ void ivf_flat_search_device(const IvfFlatIndexView& index, const float* queries,
   ivf_args(index, nq, index.d, k, op);
   if (nq > 0 && (queries == nullptr || ids == nullptr)) invalid(op, "queries and ids must not be NULL.");
   if (nq == 0) return;
+  // the offsets stay on the device (not checked here: the caller's index
+  // must hold offsets from 0 to n that do not decrease)
   Session ss((hipStream_t)stream);
-  hipStream_t s = ss.stream();
-  std::vector<int32_t> off((size_t)index.lists + 1);
-  check_hip(hipMemcpyAsync(off.data(), index.offsets, sizeof(int32_t) * off.size(),
-                           hipMemcpyDeviceToHost, s), "hipMemcpyAsync (offsets)");
-  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-  check_offsets(off, index.n, op);
   const int P = (int)std::clamp<int64_t>(n_probes, 1, index.lists);
   float* dists = distances ? distances : ss.arena().take<float>((size_t)nq * k);
   ivf_search(ss, index.centers, index.lists, index.data, index.n, index.indices, index.offsets,
-             off, index.d, (int)index.metric, queries, nq, k, P, ids, dists);
+             nullptr, index.d, (int)index.metric, queries, nq, k, P, ids, dists);
 }
 
 Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k, void* stream) {
@@ -1297,7 +1349,7 @@ Neighbors hamming_knn(const Rows& rows, const Rows& queries, int k, void* stream
   int32_t* ids = ar.take<int32_t>((size_t)std::max<int64_t>(1, nq * k));
   float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
   hamming(ss, (const uint8_t*)db, rows.n, (const uint8_t*)dq, nq, rows.d, k, ids, dists);
-  return download(ar, s, ids, dists, nq, k);
+  return download(ss, ids, dists, nq, k);
 }
 
 void hamming_knn_device(const Rows& rows, const Rows& queries, int k, int32_t* ids,
@@ -1323,7 +1375,7 @@ Neighbors knn_self_graph(const Rows& rows, int k, Metric metric, void* stream) {
   float* dists = ar.take<float>((size_t)rows.n * k);
   self_graph(ss, dr, rows.n, rows.d, rows.dtype == Dtype::Float16, k, (int)metric, ids,
              dists);
-  return download(ar, s, ids, dists, rows.n, k);
+  return download(ss, ids, dists, rows.n, k);
 }
 
 void knn_self_graph_device(const Rows& rows, int k, Metric metric, int32_t* ids,
@@ -1392,6 +1444,7 @@ std::pair<std::vector<int32_t>, std::vector<float>> topk_merge(const Rows& score
                            s), "hipMemcpyAsync (ids)");
   check_hip(hipMemcpyAsync(out.second.data(), os, sizeof(float) * nq * k, hipMemcpyDeviceToHost,
                            s), "hipMemcpyAsync (scores)");
+  ss.close();
   check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
   return out;
 }
@@ -1411,12 +1464,11 @@ void topk_merge_device(const float* scores, int64_t nq, int64_t t, const int32_t
 }
 
 void release_workspace() {
-  std::lock_guard<std::mutex> lock(g_mutex);
-  int dev = current_device();
-  auto it = g_arenas.find(dev);
-  if (it != g_arenas.end()) {
-    it->second->release();
-    g_arenas.erase(it);
+  DeviceWorkspace& w = device_workspace(current_device());
+  std::lock_guard<std::mutex> lock(w.lock);
+  if (w.arena) {
+    w.arena->release();
+    w.arena.reset();
   }
 }
 

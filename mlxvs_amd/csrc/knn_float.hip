@@ -1437,6 +1437,33 @@ __global__ __launch_bounds__(256) void ivf_slots_kernel(IvfPlanArgs a) {
   }
 }
 
+// Step 1c (one workgroup): the lists by descending bit length of their
+// sizes, empty lists last, into `order` (a counting sort over 33 classes).
+// Within a class the order is unspecified: it only decides which items
+// start first, and each pair writes its own segments.
+__global__ __launch_bounds__(1024) void ivf_order_kernel(IvfPlanArgs a) {
+  __shared__ int base[33];
+  const int tid = threadIdx.x;
+  if (tid < 33) base[tid] = 0;
+  __syncthreads();
+  auto cls = [&](int l) {
+    const int len = a.offsets[l + 1] - a.offsets[l];
+    return len > 0 ? 32 - __clz(len) : 0;  // 1 .. 31, or 0
+  };
+  for (int l = tid; l < a.lists; l += 1024) atomicAdd(&base[cls(l)], 1);
+  __syncthreads();
+  if (tid == 0) {  // exclusive sums, the longest class first
+    int run = 0;
+    for (int c = 32; c >= 0; --c) {
+      const int v = base[c];
+      base[c] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int l = tid; l < a.lists; l += 1024) a.order[atomicAdd(&base[cls(l)], 1)] = l;
+}
+
 // Pairs per workgroup of the LDS-binned count and fill: a list's global
 // counter then takes one atomic per workgroup (same-address atomics from
 // every workgroup serialise; binning cuts them 8,192-fold).
@@ -1913,8 +1940,26 @@ hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s) {
   const bool binned = a.lists <= kPlanLdsLists;
   const dim3 chunks((unsigned)((np + kPlanChunk - 1) / kPlanChunk));
   hipLaunchKernelGGL(ivf_count_kernel, chunks, dim3(256), binned ? 4 * a.lists : 0, s, a);
+  hipLaunchKernelGGL(ivf_order_kernel, dim3(1), dim3(1024), 0, s, a);
   hipLaunchKernelGGL(ivf_scan_kernel, dim3(1), dim3(1024), 0, s, a);
   hipLaunchKernelGGL(ivf_fill_kernel, chunks, dim3(256), binned ? 8 * a.lists : 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_ivf_slots(const IvfPlanArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.P <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ivf_slots_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+__global__ void iota_kernel(int* p, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = (int)i;
+}
+
+hipError_t launch_iota(int* p, int64_t count, hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, p, count);
   return hipGetLastError();
 }
 

@@ -164,9 +164,10 @@ struct IvfMapArgs {
 };
 hipError_t launch_ivf_map(const IvfMapArgs& a, hipStream_t s);
 
-// The IVF-Flat work items on the device, from the probes (the host bucketing
-// without a round trip): pairs q * P + p grouped by list, the lists in
-// `order` (longest first), each list's pairs cut into items of up to 128;
+// The IVF-Flat work items on the device, from the probes and the offsets
+// (no round trip to the host): pairs q * P + p grouped by list, the lists
+// longest first (by the bit length of their sizes; the plan writes that
+// order to `order`), each list's pairs cut into items of up to 128;
 // slots[q * P + p] = the buffer column of the probe's first row (the sizes
 // of the query's earlier probes).  Items land in [0, *n_items) of an array
 // of ivf_plan_max_items(nq * P, lists) rows; the pairs' order within a list
@@ -176,7 +177,7 @@ struct IvfPlanArgs {
   int64_t nq;
   int P;
   const int* offsets;    // [lists + 1]
-  const int* order;      // [lists] list ids, longest first
+  int* order;            // [lists] scratch: list ids, longest first
   int lists;
   int* cnt;              // [lists] scratch
   int* pos;              // [lists] scratch
@@ -190,9 +191,13 @@ struct IvfPlanArgs {
 };
 int64_t ivf_plan_max_items(int64_t pairs, int64_t lists);
 hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t s);
+// Only the slots (probes, nq, P, offsets, lists, slots are read).
+hipError_t launch_ivf_slots(const IvfPlanArgs& a, hipStream_t s);
 
 // Fill a float array (candidate buffers start at -inf).
 hipError_t launch_fill_f32(float* p, int64_t count, float v, hipStream_t s);
+// p[i] = i for i < count (the query list of a search over every query).
+hipError_t launch_iota(int* p, int64_t count, hipStream_t s);
 
 // Exact merge of the per-segment lists into the final sorted k best.
 //   grid nq; workgroup 256 threads.
@@ -360,14 +365,16 @@ hipError_t launch_topk_merge(const TopkMergeArgs& a, hipStream_t s);
 // would.  Float rows: scores q.b, or 2 (q.b + bnorm) for L2, over the first
 // d of ld values (binary16 when f16); words: Hamming over packed uint32
 // words (d words of row stride ld), score -popcount, distances with
-// dist_mode 1.
+// dist_mode 1.  IVF-Flat (probes set): a query's rows are the rows of its
+// probed lists, numbered by their column in the query's candidate buffer
+// (probe p's rows from slots[q * P + p]), and the ids written are columns.
 struct RedoArgs {
   const void* base;      // [n][ld] rows
   const void* queries;   // [nq][ld]
   const float* bnorm;    // [n] -|b|^2 / 2 (L2 float) else null
   const float* qnorm;    // [nq] |q|^2 (L2 float, dist_mode 0) else null
   const int* flags;      // [nq] or null
-  int64_t n;
+  int64_t n;             // rows (IVF: lists)
   int nq;
   int ld;
   int d;
@@ -378,6 +385,10 @@ struct RedoArgs {
   int k;
   int32_t* ids;          // [nq][k]
   float* dists;          // [nq][k] (may be null)
+  const int* probes;     // IVF: [nq][P] probed lists, else null
+  const int* slots;      // IVF: [nq][P] first column of each probe
+  const int* offsets;    // IVF: [lists + 1]
+  int P;
 };
 hipError_t launch_redo(const RedoArgs& a, hipStream_t s);
 

@@ -398,14 +398,21 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(TopkMergeArgs a) {
 // words) in chunks of 4,096 and keeps the best k exactly as topk_merge does
 // (a lower bound from the chunk's wavefront maxima, candidates at or above
 // it in LDS, radix selection of the 64-bit ranks).  Flagged queries are
-// rare, so the rows are read per query.
+// rare, so the rows are read per query.  For IVF-Flat a query's rows are
+// those of its probed lists; with no flags (rows too long for the fused
+// scan, device entry) every query is searched this way.
 
-// Scores of one query against rows: score(j) and the row count.
+// Scores of one query against its rows: begin(a, q) points the scorer at
+// query q and returns the query's row count, score(j) the score of row j.
 struct FloatScorer {
   const void* base;
   const void* query;
   const float* bnorm;  // -|b|^2 / 2 (L2) or null
   int ld, d, f16;
+  __device__ __forceinline__ int64_t begin(const RedoArgs& a, int q) {
+    query = (const char*)a.queries + (int64_t)q * ld * (f16 ? 2 : 4);
+    return a.n;
+  }
   __device__ __forceinline__ float operator()(int64_t j) const {
     float acc = 0.0f;
     if (f16) {
@@ -425,11 +432,67 @@ struct HammingScorer {
   const uint32_t* base;
   const uint32_t* query;
   int ldw, w;
+  __device__ __forceinline__ int64_t begin(const RedoArgs& a, int q) {
+    query = (const uint32_t*)a.queries + (int64_t)q * ldw;
+    return a.n;
+  }
   __device__ __forceinline__ float operator()(int64_t j) const {
     const uint32_t* b = base + j * ldw;
     uint32_t acc = 0;
     for (int c = 0; c < w; ++c) acc += __popc(query[c] ^ b[c]);
     return -(float)acc;
+  }
+};
+// IVF-Flat: the query's candidate columns, probe by probe (probe p's rows
+// from column slots[p]); fp32 rows of a multiple of 4 values, with the
+// arithmetic of the IVF VALU scan (four partial sums, then pairs), so both
+// routes give the same scores.  A thread's columns mostly increase, so it
+// keeps its place in the probes and restarts only when a column lies behind.
+struct IvfScorer {
+  const float* data;
+  const float* query;
+  const float* bnorm;  // -|b|^2 / 2 (L2) or null
+  int ld, lists;
+  const int* probes;   // the query's P probes
+  const int* slots;    // their first columns
+  const int* offsets;
+  int P;
+  int p;               // the walk: probe p, columns [c0, c1) from row r0
+  int64_t c0, c1, r0;
+  __device__ __forceinline__ int64_t len_of(int l) const {
+    return (l >= 0 && l < lists) ? offsets[l + 1] - offsets[l] : 0;
+  }
+  __device__ __forceinline__ int64_t begin(const RedoArgs& a, int q) {
+    query = (const float*)a.queries + (int64_t)q * ld;
+    probes = a.probes + (int64_t)q * P;
+    slots = a.slots + (int64_t)q * P;
+    p = -1;
+    c0 = c1 = 0;
+    return slots[P - 1] + len_of(probes[P - 1]);
+  }
+  __device__ __forceinline__ float operator()(int64_t c) {
+    if (c < c0) {
+      p = -1;
+      c0 = c1 = 0;
+    }
+    // c is below the query's column count, so the walk ends at p < P
+    while (c >= c1) {
+      ++p;
+      const int l = probes[p];
+      c0 = slots[p];
+      c1 = c0 + len_of(l);
+      r0 = c1 > c0 ? offsets[l] : 0;
+    }
+    const int64_t row = r0 + (c - c0);
+    const float* b = data + row * ld;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < ld; j += 4) {
+      const floatx4 x = *(const floatx4*)(query + j), y = *(const floatx4*)(b + j);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = __builtin_fmaf(x[u], y[u], acc[u]);
+    }
+    const float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    return bnorm ? 2.0f * (dot + bnorm[row]) : dot;
   }
 };
 
@@ -445,20 +508,17 @@ __global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
   __shared__ int s_cnt;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int k = a.k;
-  const int keff = (int)(a.n < k ? a.n : k);
   for (int q = blockIdx.x; q < a.nq; q += gridDim.x) {
     if (a.flags && !a.flags[q]) continue;  // uniform in the workgroup
-    if constexpr (std::is_same<Scorer, FloatScorer>::value)
-      sc.query = (const char*)a.queries + (int64_t)q * sc.ld * (sc.f16 ? 2 : 4);
-    else
-      sc.query = (const uint32_t*)a.queries + (int64_t)q * sc.ldw;
+    const int64_t n = sc.begin(a, q);      // the query's rows
+    const int keff = (int)(n < k ? n : k);
     if (tid == 0) s_cnt = 0;
     uint32_t L = 1;
     int64_t seen = 0;
     bool overflow = false;
     __syncthreads();
-    for (int64_t c0 = 0; c0 < a.n; c0 += CHUNK) {
-      const int64_t valid = a.n - c0 < CHUNK ? a.n - c0 : CHUNK;
+    for (int64_t c0 = 0; c0 < n; c0 += CHUNK) {
+      const int64_t valid = n - c0 < CHUNK ? n - c0 : CHUNK;
       uint32_t key[PER];
       uint32_t mx = 0;
 #pragma unroll
@@ -521,7 +581,7 @@ __global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
       // many equal keys at the bound: every row again, selected directly
       __syncthreads();
       auto visit = [&](auto f) {
-        for (int64_t c = tid; c < a.n; c += NT)
+        for (int64_t c = tid; c < n; c += NT)
           f(((uint64_t)key_nz(sc(c)) << 32) | (uint32_t)(~(uint32_t)c));
       };
       radix_pick<NT>(visit, keff, hist, st);
@@ -598,7 +658,12 @@ hipError_t launch_redo(const RedoArgs& a, hipStream_t s) {
   if (a.k < 1 || a.k > kMaxK) return hipErrorInvalidValue;
   // a persistent grid: about four workgroups per CU walk the flags
   const unsigned g = (unsigned)std::min<int64_t>(a.nq, 1024);
-  if (a.words) {
+  if (a.probes) {
+    if (a.P < 1 || a.ld % 4 != 0 || !a.slots || !a.offsets) return hipErrorInvalidValue;
+    IvfScorer sc{(const float*)a.base, nullptr, a.bnorm, a.ld, (int)a.n, nullptr, nullptr,
+                 a.offsets, a.P, -1, 0, 0, 0};
+    hipLaunchKernelGGL((redo_kernel<IvfScorer>), dim3(g), dim3(256), 0, s, a, sc);
+  } else if (a.words) {
     HammingScorer sc{(const uint32_t*)a.base, nullptr, a.ld, a.d};
     hipLaunchKernelGGL((redo_kernel<HammingScorer>), dim3(g), dim3(256), 0, s, a, sc);
   } else {

@@ -118,6 +118,36 @@ def test_ivf_device_api_matches_host_api():
     assert np.array_equal(dd.download((150, 10), np.float32), dist)
 
 
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("d,n_probes,k", [
+    (32, 4, 10),     # fused scan, k <= 16
+    (32, 6, 40),     # fused scan, k > 16: flagged queries searched again on the device
+    (32, 3, 256),    # k > 16 with short lists: padding
+    (300, 4, 10),    # rows longer than the fused scan takes: the exhaustive device route
+    (300, 5, 64),
+    (16, 200, 20),   # more probes than the fused merge holds: the exhaustive device route
+])
+def test_ivf_device_entry_routes(oracle, metric, d, n_probes, k):
+    # the device entry plans from the device offsets alone (no host copy of
+    # offsets or probes); every route matches the restatement bit for bit on
+    # integer rows, and the host-array entry
+    x = int_rows(6000, d, 21)
+    q = int_rows(257, d, 22)
+    c, data, ind, off = ivf_index(x, 250 if n_probes > 64 else 48)
+    lists = c.shape[0]
+    wi, wd = oracle.ivf_flat(c, data, ind, off, q, k, n_probes, metric)
+    bufs = [_hip.DeviceBuffer.from_array(a) for a in (c, data, ind, off, q)]
+    di, dd = _hip.DeviceBuffer(257 * k * 4), _hip.DeviceBuffer(257 * k * 4)
+    mlxvs_amd.ivf_flat_search_device(bufs[0].value, lists, bufs[1].value, 6000, bufs[2].value,
+                                     bufs[3].value, d, metric, bufs[4].value, 257, k, di.value,
+                                     dd.value, n_probes=n_probes)
+    _hip.synchronize()
+    ids, dist = di.download((257, k), np.int32), dd.download((257, k), np.float32)
+    assert np.array_equal(ids, wi) and np.array_equal(dist, wd)
+    hi, hd = mlxvs_amd.ivf_flat_search(c, data, ind, off, metric, q, k, n_probes=n_probes)
+    assert np.array_equal(hi, ids) and np.array_equal(hd, dist)
+
+
 def test_ivf_argument_errors():
     x = int_rows(100, 4, 8)
     c, data, ind, off = ivf_index(x, 4)
