@@ -337,6 +337,12 @@ def main() -> int:
         flops = 2.0 * d * cands / (cnt / args.steps)
         roof = {"bound": "mfma", "achieved": round(flops / per / 1e12, 2),
                 "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s", "candidates_per_query": round(cands / nq, 1)}
+    elif w["kind"] == "hamming" and kname == "scan_bits":
+        # a few queries: the codes read once (the queries of a split share
+        # the rows in L2)
+        row_bytes = float(n) * d / (cnt / args.steps)
+        roof = {"bound": "hbm", "achieved": round(row_bytes / per / 1e9, 1), "peak": PEAK_HBM,
+                "unit": "GB/s"}
     elif w["kind"] == "hamming" and kname in ("hamming_mfma", "stream_bits"):
         # the FP4 MFMA route: 2 ops (multiply, add) per code bit and pair
         ops = 2.0 * nq * n * 8 * d / (cnt / args.steps)  # per launch

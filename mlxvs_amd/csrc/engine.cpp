@@ -690,6 +690,46 @@ void hamming_exhaustive(Arena& ar, hipStream_t s, const uint32_t* bw, const uint
   }
 }
 
+// A few queries (at most kScanQueries): the search is HBM-bound, and the
+// MFMA routes would leave all but a few of their query lanes idle.  Each
+// workgroup scores one split of the rows against one query with VALU
+// popcounts and selects the split's best k exactly; one workgroup per query
+// then selects the best k of the splits' lists.  About one workgroup per
+// CU in all, each split at least 256 rows.  Returns false when the route
+// does not apply.
+constexpr int64_t kScanQueries = 4;
+bool hamming_scan(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
+                  int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int ldb = kern::bits_row_bytes(nbytes);
+  const int nv = ldb / 16;
+  if (nq > kScanQueries || (nv != 2 && nv != 4 && nv != 8)) return false;
+  // whole chunks of 4,096 rows a split where there are enough of them
+  const int64_t want = std::max<int64_t>(8, device_slots(1) / nq);
+  int64_t rps = std::max<int64_t>(256, (n + want - 1) / want);
+  if (rps > 2048) rps = (rps + 4095) / 4096 * 4096;
+  const int64_t nsplit = ((n + rps - 1) / rps + 7) / 8 * 8;
+  if ((rps + 4096) * ldb >= (int64_t(1) << 31)) return false;
+  const int ldw = ldb / 4;
+  auto packed = [&](const uint8_t* x, int64_t rows_) -> const uint32_t* {
+    if (nbytes == ldb && (uintptr_t)x % 16 == 0) return (const uint32_t*)x;
+    uint32_t* w = ar.take<uint32_t>((size_t)rows_ * ldw);
+    launch(s, "pack", [&] { return kern::launch_pack({x, rows_, nbytes, w, ldw}, s); });
+    return w;
+  };
+  const uint32_t* bw = packed(rows, n);
+  const uint32_t* qw = packed(queries, nq);
+  uint64_t* part = ar.take<uint64_t>((size_t)(nq * nsplit * k));
+  kern::ScanBitsArgs sa{bw, qw, n, (int)nq, nv, rps, (int)nsplit, k, part};
+  launch(s, "scan_bits", [&] { return kern::launch_scan_bits(sa, s); });
+  // each list holds its split's exact best k: one exact select per query
+  // over them
+  const int64_t m = nsplit * k;
+  uint64_t* lev = ar.take<uint64_t>((size_t)std::max<int64_t>(1, kern::merge_ranks_scratch(nq, m, k)));
+  launch(s, "merge", [&] { return kern::launch_merge_ranks(part, nq, m, k, lev, ids, dists, s); });
+  return true;
+}
 
 // FP4 MFMA route: the bits kernel reads packed codes and unpacks them to
 // {0, 1} e2m1 values, whose squared L2 distance is the Hamming distance
@@ -769,6 +809,7 @@ void hamming(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries
     launch(s, "fill", [&] { return kern::launch_fill(ids, dists, nq * k, INFINITY, s); });
     return;
   }
+  if (hamming_scan(ss, rows, n, queries, nq, nbytes, k, ids, dists)) return;
   if (hamming_bits(ss, rows, n, queries, nq, nbytes, k, ids, dists)) return;
   const int W = (nbytes + 3) / 4;
   const int T = list_len_hamming(k);

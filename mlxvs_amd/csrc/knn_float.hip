@@ -947,7 +947,7 @@ __global__ __launch_bounds__(256) void select_group_kernel(MergeGroupArgs a) {
       const uint64_t pre = s_prefix, msk = s_mask;
       for (int i = threadIdx.x; i < C; i += 256) {
         const uint64_t v = buf[i];
-        if ((v & msk) == pre) atomicAdd(&hist[(uint32_t)(v >> (8 * d)) & 255u], 1u);
+        wave_hist_add(hist, (uint32_t)(v >> (8 * d)) & 255u, (v & msk) == pre);
       }
       __syncthreads();
       if (threadIdx.x < 64) {
@@ -995,19 +995,15 @@ __global__ __launch_bounds__(256) void select_group_kernel(MergeGroupArgs a) {
     const uint64_t pre = s_prefix, msk = s_mask;
     for (int i = threadIdx.x; i < C; i += 256) {
       const uint64_t v = buf[i];
-      const bool take = (v & msk) > pre || (v & msk) == pre;
-      if (take && v != 0) {
-        const int o = atomicAdd(&s_out, 1);
-        a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
-      }
+      const bool take = ((v & msk) > pre || (v & msk) == pre) && v != 0;
+      const int o = wave_take(&s_out, take);
+      if (take) a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
     }
   } else {
     for (int i = threadIdx.x; i < C; i += 256) {
       const uint64_t v = buf[i];
-      if (v != 0) {
-        const int o = atomicAdd(&s_out, 1);
-        a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
-      }
+      const int o = wave_take(&s_out, v != 0);
+      if (v != 0) a.out[((int64_t)q * a.ngroups + g) * a.keep + o] = v;
     }
   }
   __syncthreads();
@@ -1314,7 +1310,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     __syncthreads();
     for (int64_t j = threadIdx.x; j < a.n; j += 256) {
       const uint64_t r = rank_of(sr[j], (uint32_t)j);
-      if ((r & mask) == prefix) atomicAdd(&hist[(r >> shift) & 255u], 1u);
+      wave_hist_add(hist, (uint32_t)(r >> shift) & 255u, (r & mask) == prefix);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1341,10 +1337,8 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   if (a.n > 0) {
     for (int64_t j = threadIdx.x; j < a.n; j += 256) {
       const uint64_t r = rank_of(sr[j], (uint32_t)j);
-      if (r >= prefix) {
-        const int slot = atomicAdd(&s_cnt, 1);
-        if (slot < kMaxK) sel[slot] = r;
-      }
+      const int slot = wave_take(&s_cnt, r >= prefix);
+      if (r >= prefix && slot < kMaxK) sel[slot] = r;
     }
   }
   __syncthreads();

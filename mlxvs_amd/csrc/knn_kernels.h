@@ -392,6 +392,35 @@ struct RedoArgs {
 };
 hipError_t launch_redo(const RedoArgs& a, hipStream_t s);
 
+// Exact Hamming k-NN of a few queries, HBM-bound: workgroup (split, query)
+// scores its split's rows against the query with VALU popcounts (a row per
+// thread, 16-byte loads) and selects their best k exactly (chunk bounds,
+// candidates in LDS, radix select); the ranks (key of -distance, then
+// lowest row) go to part[q][split][k], zero past the split's rows, for
+// merge_lists (segment lists of length k, Hamming distances).  The nq
+// workgroups of a split run on one XCD and share its L2, so the rows cross
+// HBM about once.  nsplit is a multiple of 8.
+struct ScanBitsArgs {
+  const uint32_t* rows;     // [n][4 nv] packed words
+  const uint32_t* queries;  // [nq][4 nv]
+  int64_t n;
+  int nq;
+  int nv;                   // 16-byte vectors per row: 2, 4 or 8
+  int64_t rows_per_split;
+  int nsplit;
+  int k;
+  uint64_t* part;           // [nq][nsplit][k] out
+};
+hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s);
+// The best k of each query's m ranks part[q][0, m) (0: none), as Hamming
+// results: ids, distances -score.  Groups of 4,096 ranks are reduced to
+// their best k on a workgroup each, level by level, into `scratch`
+// (merge_ranks_scratch(nq, m, k) ranks), until one workgroup per query
+// finishes.
+int64_t merge_ranks_scratch(int64_t nq, int64_t m, int k);
+hipError_t launch_merge_ranks(const uint64_t* part, int64_t nq, int64_t m, int k, uint64_t* scratch,
+                              int32_t* ids, float* dists, hipStream_t s);
+
 // Device scratch of the no-allocation entry point (scratch.hip): a fixed
 // array of kScratchBytes per GPU, held until the process ends.  Returns its
 // device address on the current device (hipGetSymbolAddress on the first

@@ -14,6 +14,40 @@
 
 namespace mlxvs::kern {
 
+// One count per lane with `on` into the LDS histogram hist[dig].  The
+// digits of a radix select pass are often concentrated (the high bytes of
+// near scores, the low bytes of integer scores), and same-address LDS
+// atomics serialise: the digits of the wavefront's first two leading lanes
+// take one atomic each for all their lanes, the rest one per lane.
+__device__ __forceinline__ void wave_hist_add(uint32_t* hist, uint32_t dig, bool on) {
+  uint64_t act = __builtin_amdgcn_ballot_w64(on);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    if (act == 0) return;
+    const int lead = __builtin_ctzll(act);
+    const uint32_t d0 = __builtin_amdgcn_readlane(dig, lead);
+    const uint64_t same = __builtin_amdgcn_ballot_w64(on && dig == d0);
+    if ((int)(threadIdx.x & 63) == lead) atomicAdd(&hist[d0], (uint32_t)__builtin_popcountll(same));
+    act &= ~same;
+    on = on && dig != d0;
+  }
+  if (on) atomicAdd(&hist[dig], 1u);
+}
+
+// A slot for each lane with `on` from the LDS counter *ctr: one atomic per
+// wavefront (same-address atomics serialise), the lanes' places by mbcnt.
+// Returns the lane's slot (unspecified when !on).
+__device__ __forceinline__ int wave_take(int* ctr, bool on) {
+  const uint64_t b = __builtin_amdgcn_ballot_w64(on);
+  if (b == 0) return 0;
+  const int leader = __builtin_ctzll(b);
+  int base = 0;
+  if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(ctr, __builtin_popcountll(b));
+  base = __shfl(base, leader);
+  return base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                               __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+}
+
 // Larger float, larger key (reference src/kernels.h:16-19).
 __device__ __forceinline__ uint32_t key_of(float v) {
   uint32_t u = __float_as_uint(v);

@@ -85,7 +85,7 @@ __device__ void radix_pick(Visit visit, int want, uint32_t* hist, PickState& st)
     const uint64_t pre = st.prefix, msk = st.mask;
     const int sh = 8 * dg;
     visit([&](uint64_t r) {
-      if ((r & msk) == pre) atomicAdd(&hist[(uint32_t)(r >> sh) & 255u], 1u);
+      wave_hist_add(hist, (uint32_t)(r >> sh) & 255u, (r & msk) == pre);
     });
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -139,8 +139,16 @@ __device__ void radix_gather(Visit visit, PickState& st, uint64_t* out) {
   visit([&](uint64_t r) {
     const uint64_t m = r & msk;
     bool take = m > pre;
-    if (!take && m == pre) take = done || atomicAdd(&st.tie, 1) < need;
-    if (take) out[atomicAdd(&st.taken, 1)] = r;
+    const bool tied = m == pre;
+    if (done) {
+      take = take || tied;
+    } else {
+      // of the ranks equal to the prefix, the first `need` to arrive
+      const int t = wave_take(&st.tie, tied);
+      take = take || (tied && t < need);
+    }
+    const int o = wave_take(&st.taken, take);
+    if (take) out[o] = r;
   });
 }
 
@@ -405,6 +413,9 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(TopkMergeArgs a) {
 // Scores of one query against its rows: begin(a, q) points the scorer at
 // query q and returns the query's row count, score(j) the score of row j.
 struct FloatScorer {
+  static constexpr bool kAnyRow = false;  // rows past the end must not be read
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = false;
   const void* base;
   const void* query;
   const float* bnorm;  // -|b|^2 / 2 (L2) or null
@@ -429,6 +440,9 @@ struct FloatScorer {
   }
 };
 struct HammingScorer {
+  static constexpr bool kAnyRow = false;  // rows past the end must not be read
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = false;
   const uint32_t* base;
   const uint32_t* query;
   int ldw, w;
@@ -449,6 +463,9 @@ struct HammingScorer {
 // routes give the same scores.  A thread's columns mostly increase, so it
 // keeps its place in the probes and restarts only when a column lies behind.
 struct IvfScorer {
+  static constexpr bool kAnyRow = false;  // rows past the end must not be read
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = false;
   const float* data;
   const float* query;
   const float* bnorm;  // -|b|^2 / 2 (L2) or null
@@ -496,121 +513,180 @@ struct IvfScorer {
   }
 };
 
+// LDS of one exact select over scored rows.
+struct RowSelect {
+  uint64_t buf[kCandCap];
+  uint64_t tmp[kMaxK];
+  uint32_t hist[256];
+  uint32_t wbound[4];
+  PickState st;
+  int cnt;
+};
+
+// The best keff = min(k, c1 - c0) ranks (key of the score, then lowest
+// row) of the rows [c0, c1) that sc scores (or, for a rank source, of the
+// ranks it holds, 0 for none), in sm.buf[0, keff): in the output order and
+// sm.buf[keff, pow2) zero when `sorted`, else in no order.  Rows in chunks of 4,096, 16 a
+// thread: the chunk's lower bound is the least over the wavefronts of
+// their j-th largest thread maximum (j = ceil(k / 4)), which at least k
+// scores of the rows seen so far reach; candidates at or above it go to LDS,
+// and a radix select trims them to the best k when they pass half the
+// buffer (its k-th best then bounds the next chunks).  Too many equal keys
+// at the bound to hold: every row again, selected directly.  All threads
+// call it; it ends with a barrier.
 template <typename Scorer>
-__global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
+__device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelect& sm,
+                           bool sorted = true) {
   constexpr int NT = 256, PER = 16, NW = NT / 64;
   constexpr int64_t CHUNK = (int64_t)NT * PER;
-  __shared__ uint64_t buf[kCandCap];
-  __shared__ uint64_t tmp[kMaxK];
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t wbound[NW];
-  __shared__ PickState st;
-  __shared__ int s_cnt;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t n = c1r - c0r;
+  const int keff = (int)(n < k ? n : k);
+  if (tid == 0) sm.cnt = 0;
+  uint32_t L = 1;
+  int64_t seen = 0;
+  bool overflow = false;
+  __syncthreads();
+  for (int64_t c0 = c0r; c0 < c1r; c0 += CHUNK) {
+    const int64_t valid = c1r - c0 < CHUNK ? c1r - c0 : CHUNK;
+    constexpr bool RANKS = Scorer::kRanks || Scorer::kChunk;
+    uint32_t key[PER];
+    uint32_t low[RANKS ? PER : 1];  // rank sources: the low words
+    uint32_t mx = 0;
+    if constexpr (Scorer::kChunk) {
+      // the scorer lays the chunk's rows out over the threads itself
+      sc.chunk(c0, valid, key, low);
+    } else {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int64_t c = (int64_t)e * NT + tid;
+        // kAnyRow: reads past the range return zeros, so every element is
+        // fetched unconditionally and all PER loads can be in flight at once
+        if constexpr (Scorer::kRanks) {
+          uint64_t r;
+          if constexpr (Scorer::kAnyRow)
+            r = sc.rank(c0 + c);
+          else
+            r = c < valid ? sc.rank(c0 + c) : 0ull;
+          if (c >= valid) r = 0;
+          key[e] = (uint32_t)(r >> 32);
+          low[e] = (uint32_t)r;
+        } else if constexpr (Scorer::kAnyRow) {
+          const uint32_t kk = key_nz(sc(c0 + c));
+          key[e] = c < valid ? kk : 0u;
+        } else {
+          key[e] = c < valid ? key_nz(sc(c0 + c)) : 0u;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) mx = max(mx, key[e]);
+    // the chunk's bound (see topk_merge_kernel)
+    const int j = (k + NW - 1) / NW;
+    const uint32_t lw = __shfl(wave_sort_desc(mx, lane), j - 1);
+    if (lane == 0) sm.wbound[w] = lw;
+    __syncthreads();
+    const int cnt0 = sm.cnt;
+    if (cnt0 > kCandCap) {
+      overflow = true;
+      break;
+    }
+    const int want0 = (int)(seen < k ? seen : k);
+    if (cnt0 > kCandCap / 2) {
+      auto visit = [&](auto f) {
+        for (int i = tid; i < cnt0; i += NT) f(sm.buf[i]);
+      };
+      radix_pick<NT>(visit, want0, sm.hist, sm.st);
+      radix_gather(visit, sm.st, sm.tmp);
+      __syncthreads();
+      for (int i = tid; i < want0; i += NT) sm.buf[i] = sm.tmp[i];
+      if (tid == 0) sm.cnt = want0;
+      if (want0 == k) L = max(L, (uint32_t)((sm.st.prefix & sm.st.mask) >> 32));
+      __syncthreads();
+    }
+    uint32_t lc = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) lc = min(lc, sm.wbound[i]);
+    L = max(L, max(lc, 1u));
+    seen += valid;
+    if (__builtin_amdgcn_ballot_w64(mx >= L) != 0) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const bool p = key[e] >= L;
+        const uint64_t b = __builtin_amdgcn_ballot_w64(p);
+        if (b == 0) continue;
+        const int leader = __builtin_ctzll(b);
+        uint32_t base = 0;
+        if (lane == leader) base = atomicAdd((uint32_t*)&sm.cnt, (uint32_t)__builtin_popcountll(b));
+        base = __shfl(base, leader);
+        if (p) {
+          const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi(
+                                          (uint32_t)(b >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+          uint32_t lo;
+          if constexpr (RANKS)
+            lo = low[e];
+          else
+            lo = ~(uint32_t)(c0 + (int64_t)e * NT + tid);
+          if (pos < (uint32_t)kCandCap) sm.buf[pos] = ((uint64_t)key[e] << 32) | lo;
+        }
+      }
+    }
+    __syncthreads();  // the wbound words and the appends, before the next chunk
+  }
+  if (!overflow) overflow = sm.cnt > kCandCap;
+  if (overflow) {
+    __syncthreads();
+    auto visit = [&](auto f) {
+      for (int64_t c = c0r + tid; c < c1r; c += NT) {
+        if constexpr (Scorer::kRanks || Scorer::kChunk)
+          f(sc.rank(c));
+        else
+          f(((uint64_t)key_nz(sc(c)) << 32) | (uint32_t)(~(uint32_t)c));
+      }
+    };
+    radix_pick<NT>(visit, keff, sm.hist, sm.st);
+    radix_gather(visit, sm.st, sm.tmp);
+    __syncthreads();
+    for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
+    __syncthreads();
+  } else {
+    const int cnt = sm.cnt;
+    if (cnt > keff) {
+      auto visit = [&](auto f) {
+        for (int i = tid; i < cnt; i += NT) f(sm.buf[i]);
+      };
+      radix_pick<NT>(visit, keff, sm.hist, sm.st);
+      radix_gather(visit, sm.st, sm.tmp);
+      __syncthreads();
+      for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
+      __syncthreads();
+    }
+  }
+  // the output order (unless the caller takes the set unordered)
+  if (!sorted) return keff;
+  const int P = pow2_at_least(keff > 1 ? keff : 1);
+  for (int i = keff + tid; i < P; i += NT) sm.buf[i] = 0;
+  __syncthreads();
+  bitonic_desc<NT>(sm.buf, P, OutputOrder{});
+  return keff;
+}
+
+template <typename Scorer>
+__global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  const int tid = threadIdx.x;
   const int k = a.k;
   for (int q = blockIdx.x; q < a.nq; q += gridDim.x) {
     if (a.flags && !a.flags[q]) continue;  // uniform in the workgroup
     const int64_t n = sc.begin(a, q);      // the query's rows
-    const int keff = (int)(n < k ? n : k);
-    if (tid == 0) s_cnt = 0;
-    uint32_t L = 1;
-    int64_t seen = 0;
-    bool overflow = false;
-    __syncthreads();
-    for (int64_t c0 = 0; c0 < n; c0 += CHUNK) {
-      const int64_t valid = n - c0 < CHUNK ? n - c0 : CHUNK;
-      uint32_t key[PER];
-      uint32_t mx = 0;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int64_t c = (int64_t)e * NT + tid;
-        key[e] = c < valid ? key_nz(sc(c0 + c)) : 0u;
-        mx = max(mx, key[e]);
-      }
-      // the chunk's bound (see topk_merge_kernel)
-      const int j = (k + NW - 1) / NW;
-      const uint32_t lw = __shfl(wave_sort_desc(mx, lane), j - 1);
-      if (lane == 0) wbound[w] = lw;
-      __syncthreads();
-      const int cnt0 = s_cnt;
-      if (cnt0 > kCandCap) {
-        overflow = true;
-        break;
-      }
-      const int want0 = (int)(seen < k ? seen : k);
-      if (cnt0 > kCandCap / 2) {
-        auto visit = [&](auto f) {
-          for (int i = tid; i < cnt0; i += NT) f(buf[i]);
-        };
-        radix_pick<NT>(visit, want0, hist, st);
-        radix_gather(visit, st, tmp);
-        __syncthreads();
-        for (int i = tid; i < want0; i += NT) buf[i] = tmp[i];
-        if (tid == 0) s_cnt = want0;
-        if (want0 == k) L = max(L, (uint32_t)((st.prefix & st.mask) >> 32));
-        __syncthreads();
-      }
-      uint32_t lc = 0xffffffffu;
-#pragma unroll
-      for (int i = 0; i < NW; ++i) lc = min(lc, wbound[i]);
-      L = max(L, max(lc, 1u));
-      seen += valid;
-      if (__builtin_amdgcn_ballot_w64(mx >= L) != 0) {
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-          const bool p = key[e] >= L;
-          const uint64_t b = __builtin_amdgcn_ballot_w64(p);
-          if (b == 0) continue;
-          const int leader = __builtin_ctzll(b);
-          uint32_t base = 0;
-          if (lane == leader) base = atomicAdd((uint32_t*)&s_cnt, (uint32_t)__builtin_popcountll(b));
-          base = __shfl(base, leader);
-          if (p) {
-            const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi(
-                                            (uint32_t)(b >> 32),
-                                            __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-            const uint32_t id = (uint32_t)(c0 + (int64_t)e * NT + tid);
-            if (pos < (uint32_t)kCandCap) buf[pos] = ((uint64_t)key[e] << 32) | (uint32_t)(~id);
-          }
-        }
-      }
-      __syncthreads();  // the wbound words and the appends, before the next chunk
-    }
-    if (!overflow) overflow = s_cnt > kCandCap;
-    if (overflow) {
-      // many equal keys at the bound: every row again, selected directly
-      __syncthreads();
-      auto visit = [&](auto f) {
-        for (int64_t c = tid; c < n; c += NT)
-          f(((uint64_t)key_nz(sc(c)) << 32) | (uint32_t)(~(uint32_t)c));
-      };
-      radix_pick<NT>(visit, keff, hist, st);
-      radix_gather(visit, st, tmp);
-      __syncthreads();
-      for (int i = tid; i < keff; i += NT) buf[i] = tmp[i];
-      __syncthreads();
-    } else {
-      const int cnt = s_cnt;
-      if (cnt > keff) {
-        auto visit = [&](auto f) {
-          for (int i = tid; i < cnt; i += NT) f(buf[i]);
-        };
-        radix_pick<NT>(visit, keff, hist, st);
-        radix_gather(visit, st, tmp);
-        __syncthreads();
-        for (int i = tid; i < keff; i += NT) buf[i] = tmp[i];
-        __syncthreads();
-      }
-    }
-    // the output order, then distances (emit_topk's conventions)
-    const int P = pow2_at_least(keff > 1 ? keff : 1);
-    for (int i = keff + tid; i < P; i += NT) buf[i] = 0;
-    __syncthreads();
-    bitonic_desc<NT>(buf, P, OutputOrder{});
+    const int keff = select_rows(sc, 0, n, k, sm);
+    // distances (emit_topk's conventions)
     const bool l2 = a.metric == kL2;
     const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
     for (int i = tid; i < k; i += NT) {
-      const uint64_t r = i < keff ? buf[i] : 0ull;
+      const uint64_t r = i < keff ? sm.buf[i] : 0ull;
       const int64_t o = (int64_t)q * k + i;
       if (r == 0) {
         a.ids[o] = -1;
@@ -630,7 +706,150 @@ __global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
         }
       }
     }
-    __syncthreads();  // buf and s_cnt are reused by the next query
+    __syncthreads();  // sm is reused by the next query
+  }
+}
+
+// ---- exact Hamming scan of a few queries ------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// -popcount(query ^ row) over NV 16-byte vectors (the query's words are
+// uniform: scalar registers).
+// Hamming ranks of packed rows r0 .. (NV 16-byte vectors a row) against
+// one query, through a buffer resource over the split's rows (rows past it
+// read zeros).  chunk(): NV lanes read a row together, one vector each, so
+// a load instruction covers 64 / NV whole rows (coalesced); the lanes' XOR
+// popcounts are summed over the group by lane shuffles, and lane l keeps
+// the row of instructions i with i % NV == l % NV: sixteen rows a lane.
+// Instruction i of wavefront w reads rows R (4 i + w) .. + R - 1 of the
+// chunk, so a partial chunk's rows spread over all wavefronts (each then
+// bounds the chunk).  rank(r): one row, for the rare pass over every row.
+template <int NV>
+struct BitsChunkScorer {
+  static constexpr bool kAnyRow = true;
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = true;
+  static constexpr int R = 64 / NV;  // rows per load instruction
+  __amdgpu_buffer_rsrc_t rs;
+  int64_t r0;
+  const u32x4* query;  // NV vectors
+  u32x4 qv;            // the query's vector lane % NV
+  __device__ __forceinline__ uint64_t rank_of_dist(uint32_t d, int64_t r) const {
+    return ((uint64_t)key_nz(-(float)d) << 32) | (uint32_t)(~(uint32_t)r);
+  }
+  __device__ __forceinline__ void chunk(int64_t c0, int64_t valid, uint32_t (&key)[16],
+                                        uint32_t (&low)[16]) const {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = lane % NV, g = lane / NV;
+    // lane's row of instruction i: c0 + R (4 i + w) + g
+    const uint32_t base = (uint32_t)(c0 - r0 + R * w + g) * (16u * NV) + 16u * j;
+    // a ring of S loads in flight: instruction i + S is issued once i's
+    // vector is consumed (16 KiB a wavefront in flight)
+    constexpr int NI = 16 * NV, S = 16;
+    u32x4 x[S];
+    auto issue = [&](int i) {
+      x[i % S] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + (uint32_t)(4 * R * i) * (16u * NV), 0, 0));
+    };
+#pragma unroll
+    for (int i = 0; i < S; ++i) issue(i);
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const u32x4 v = x[i % S];
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + S < NI) issue(i + S);
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t d = __popc(v[0] ^ qv[0]) + __popc(v[1] ^ qv[1]) + __popc(v[2] ^ qv[2]) +
+                   __popc(v[3] ^ qv[3]);
+#pragma unroll
+      for (int o = 1; o < NV; o <<= 1) d += __shfl_xor(d, o);
+      const int e = i / NV, jj = i % NV;
+      mine = j == jj ? d : mine;
+      if (jj == NV - 1) {
+        const int64_t c = (int64_t)R * (4 * (e * NV + j) + w) + g;  // the lane's row in the chunk
+        const uint64_t r = rank_of_dist(mine, c0 + c);
+        key[e] = c < valid ? (uint32_t)(r >> 32) : 0u;
+        low[e] = (uint32_t)r;
+      }
+    }
+  }
+  __device__ __forceinline__ uint64_t rank(int64_t r) const {
+    const uint32_t off = (uint32_t)(r - r0) * (16u * NV);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 16 * v, 0));
+      const u32x4 q = query[v];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc += __popc(x[e] ^ q[e]);
+    }
+    return rank_of_dist(acc, r);
+  }
+};
+
+template <int NV>
+__global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  // (split, query): XCD id % 8 takes splits xcd, xcd + 8, ..., each with
+  // its nq queries in a row
+  const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+  const int split = (local / a.nq) * 8 + xcd, q = local % a.nq;
+  const int64_t r0 = min(a.n, (int64_t)split * a.rows_per_split);
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  BitsChunkScorer<NV> sc;
+  sc.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.rows + r0 * 4 * NV), (short)0,
+                                           (int)((r1 - r0) * 16 * NV), 0x00020000);
+  sc.r0 = r0;
+  sc.query = (const u32x4*)a.queries + (int64_t)q * NV;
+  sc.qv = sc.query[(threadIdx.x & 63) % NV];
+  // the merge takes each list as a set: no sort
+  const int keff = select_rows(sc, r0, r1, a.k, sm, false);
+  uint64_t* dst = a.part + ((int64_t)q * a.nsplit + split) * a.k;
+  for (int i = threadIdx.x; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+}
+
+// The per-split lists of one query as a rank source (through a buffer
+// resource: reads past the m ranks return 0, no rank).
+struct RankSource {
+  static constexpr bool kAnyRow = true;
+  static constexpr bool kRanks = true;
+  static constexpr bool kChunk = false;
+  __amdgpu_buffer_rsrc_t rs;
+  __device__ __forceinline__ uint64_t rank(int64_t c) const {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)c * 8u, 0, 0));
+    return ((uint64_t)v[1] << 32) | v[0];
+  }
+};
+
+// The best k of each query's m ranks (the splits' lists of scan_bits).
+// Workgroup (q, g) takes ranks [g w, g w + w) of query q: with `out` set it
+// writes their best k (unordered, 0 past them) to out[q][g][k] for another
+// level; else (one group) the query's results as Hamming distances (ids;
+// distances = -score; -1 / +inf past the ranks there are).
+__global__ __launch_bounds__(256) void merge_ranks_kernel(const uint64_t* part, int64_t m,
+                                                          int64_t w, int k, uint64_t* out,
+                                                          int32_t* ids, float* dists) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  const int q = blockIdx.x, g = blockIdx.y;
+  const int64_t c0 = (int64_t)g * w, c1 = min(m, c0 + w);
+  RankSource src{__builtin_amdgcn_make_buffer_rsrc((void*)(part + (int64_t)q * m), (short)0,
+                                                   (int)(m * 8), 0x00020000)};
+  const int keff = select_rows(src, c0, c1, k, sm, out == nullptr);
+  if (out) {
+    uint64_t* dst = out + ((int64_t)q * gridDim.y + g) * k;
+    for (int i = threadIdx.x; i < k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+    return;
+  }
+  for (int i = threadIdx.x; i < k; i += NT) {
+    const uint64_t r = i < keff ? sm.buf[i] : 0ull;
+    const int64_t o = (int64_t)q * k + i;
+    ids[o] = r ? id_of_rank(r) : -1;
+    if (dists) dists[o] = r ? -score_of_key((uint32_t)(r >> 32)) : INFINITY;
   }
 }
 
@@ -670,6 +889,56 @@ hipError_t launch_redo(const RedoArgs& a, hipStream_t s) {
     FloatScorer sc{a.base, nullptr, a.bnorm, a.ld, a.d, a.f16};
     hipLaunchKernelGGL((redo_kernel<FloatScorer>), dim3(g), dim3(256), 0, s, a, sc);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.nsplit <= 0) return hipSuccess;
+  if (a.nsplit % 8 != 0 || a.k < 1 || a.k > kMaxK || a.rows_per_split <= 0 ||
+      (int64_t)a.nsplit * a.rows_per_split < a.n || (int64_t)a.nsplit * a.nq >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  // a split's rows, and the offsets of the chunk past them, in 32 bits
+  if ((a.rows_per_split + 4096) * 16 * a.nv >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(a.nsplit * a.nq));
+  switch (a.nv) {
+    case 2: hipLaunchKernelGGL(scan_bits_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(scan_bits_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(scan_bits_kernel<8>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int64_t merge_ranks_scratch(int64_t nq, int64_t m, int k) {
+  int64_t total = 0;
+  while (m > 4096) {
+    const int64_t groups = (m + 4095) / 4096;
+    total += nq * groups * k;
+    m = groups * k;
+  }
+  return total;
+}
+
+hipError_t launch_merge_ranks(const uint64_t* part, int64_t nq, int64_t m, int k, uint64_t* scratch,
+                              int32_t* ids, float* dists, hipStream_t s) {
+  if (nq <= 0) return hipSuccess;
+  // byte offsets of the ranks (and of the last chunk past them) in 32 bits
+  if (k < 1 || k > kMaxK || m < 0 || (m + 4096) * 8 >= (int64_t(1) << 31) ||
+      nq >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  // levels of chunk-sized groups (one workgroup each) until one chunk is left
+  while (m > 4096) {
+    const int64_t groups = (m + 4095) / 4096;
+    hipLaunchKernelGGL(merge_ranks_kernel, dim3((unsigned)nq, (unsigned)groups), dim3(256), 0, s,
+                       part, m, (int64_t)4096, k, scratch, nullptr, nullptr);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    part = scratch;
+    scratch += nq * groups * k;
+    m = groups * k;
+  }
+  hipLaunchKernelGGL(merge_ranks_kernel, dim3((unsigned)nq, 1), dim3(256), 0, s, part, m, m, k,
+                     nullptr, ids, dists);
   return hipGetLastError();
 }
 

@@ -164,3 +164,22 @@ def test_unaligned_rows_are_packed(engine, oracle):
         _hip.synchronize()
         assert np.array_equal(di.download((50, 12), np.int32), oid)
         assert np.array_equal(dd.download((50, 12), np.float32), odist)
+
+
+@pytest.mark.parametrize("nq", [1, 2, 3, 4])
+@pytest.mark.parametrize("nbytes,n", [(32, 300_000), (64, 70_000), (128, 1_000), (20, 9_000)])
+@pytest.mark.parametrize("k", [1, 37, 256])
+def test_few_queries_scan(engine, oracle, nq, nbytes, n, k):
+    # at most four queries: one workgroup per (split, query) scores its rows
+    # with VALU popcounts, and the splits' lists of k merge (row widths of
+    # 2, 4 and 8 vectors; 20-byte codes are packed to 32; 1,000 rows: some
+    # splits are empty)
+    rng = np.random.default_rng(nq * 1000 + nbytes + k)
+    x = rng.integers(0, 256, (n, nbytes), dtype=np.uint8)
+    # a few exact copies and near copies of the queries: ties at distance 0
+    q = rng.integers(0, 256, (nq, nbytes), dtype=np.uint8)
+    x[rng.choice(n, 5, replace=False)] = q[0]
+    ids, dist = engine.hamming_knn(x, q, k)
+    oid, odist = oracle.hamming(x, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    assert not np.signbit(dist).any()
