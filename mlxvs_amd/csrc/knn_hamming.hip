@@ -179,6 +179,12 @@ __device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
 template <int NCT, int T>
 __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   constexpr bool QREG = NCT <= 8;
+  // lists of 16 (k > 10: many lanes pass): the tile's four blocks drain in
+  // pairs into a per-lane candidate buffer of CB ranks in LDS, merged into
+  // the list when a lane's buffer fills (select_pair_buf)
+  constexpr bool BUF = T == 16;
+  constexpr int CB = 6;
+  __shared__ uint64_t cbuf[BUF ? CB * 256 : 1];
   __shared__ __align__(16) uint32_t tA[2][kBitsRows * kBitsStride];
   __shared__ __align__(16) uint32_t tQ[2][QREG ? 4 : kQueriesPerBlock * kBitsStride];
   __shared__ __align__(16) float tnorm[2][kBitsRows];
@@ -262,8 +268,10 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 #pragma unroll
   for (int i = 0; i < T; ++i) K[i] = I[i] = 0;
   // (+inf for a lane without a query: nothing passes, so it never
-  // lengthens the wavefront's drain)
-  float thr = qvalid ? score_of_key(0u) : INFINITY;
+  // lengthens the wavefront's drain; the buffered drain needs a number or
+  // -inf)
+  float thr = qvalid ? (BUF ? -INFINITY : score_of_key(0u)) : INFINITY;
+  CandBuf<CB, 256> cb(&cbuf[BUF ? tid : 0]);
   // 16 slots: the bound is read once per 128-row tile of whole codes, so
   // its reads cost little and the finer slots bound tighter (m ~ k / 3)
   constexpr int S = kBitsBoundSlots;
@@ -336,33 +344,51 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       }
       fetch(j);
       if (j == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
-      if (c == NCT - 1) {
-        if (wave_on) {
-          if (share) thr = fmaxf(thr, filter_of<true>(score_of_key(seen.bound())));
-          if (share1) thr = fmaxf(thr, filter_of<true>(score_of_key(pend)));
-          const int lim0 = nrows - t * kBitsRows;
-          const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kBitsRows);
-          bool inserted = false;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            // half scores (all integers / 2 below 2^23: exact)
-            float sc[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sc[i] = acc[r][i];
-            inserted |= select_block<T, true>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
-          }
-          if (share && qvalid && inserted) {
-            const uint32_t kp = list_key(K, a.pubj);
-            if (kp > seen.slot(myslot))
-              pend = __hip_atomic_fetch_max(gk + myslot, kp, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
       par ^= 1;
       __syncthreads();
     }
+    // the tile's scores, selected after the barrier (the next tile's
+    // fetches and unpacks are in flight; the selection reads registers and
+    // the candidate buffer only)
+    if (wave_on) {
+      if (share) thr = fmaxf(thr, filter_of<true>(score_of_key(seen.bound())));
+      if (share1) thr = fmaxf(thr, filter_of<true>(score_of_key(pend)));
+      const int lim0 = nrows - t * kBitsRows;
+      const uint32_t id0 = (uint32_t)(r0 + (int64_t)t * kBitsRows);
+      bool inserted = false;
+      if constexpr (BUF) {
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          // half scores (all integers / 2 below 2^23: exact)
+          float sc0[16], sc1[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            sc0[i] = acc[r][i];
+            sc1[i] = acc[r + 1][i];
+          }
+          inserted |= select_pair_buf<T, true, CB, 256>(K, I, thr, sc0, sc1, h, id0 + 32 * r,
+                                                        lim0 - 32 * r, cb);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float sc[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[i] = acc[r][i];
+          inserted |= select_block<T, true>(K, I, thr, sc, h, id0 + 32 * r, lim0 - 32 * r);
+        }
+      }
+      if (share && qvalid && inserted) {
+        const uint32_t kp = list_key(K, a.pubj);
+        if (kp > seen.slot(myslot))
+          pend = __hip_atomic_fetch_max(gk + myslot, kp, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
+
+  // what is left in the candidate buffer (a wavefront-uniform loop)
+  if constexpr (BUF) flush_buf<T, true, CB, 256>(K, I, thr, cb);
 
   if (qvalid) {
     uint64_t* dst = a.part + ((int64_t)q * (2 * a.nsplit) + 2 * split + h) * T;
