@@ -732,10 +732,11 @@ bool hamming_scan(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
 }
 
 // FP4 MFMA route: the bits kernel reads packed codes and unpacks them to
-// {0, 1} e2m1 values, whose squared L2 distance is the Hamming distance
-// (bnorm = -popcounts / 2), then the float merge finishes (L2 finalise:
-// qpop - s = the distance, exact).  Returns false when the route does not
-// apply.
+// e2m1 values, {0, 1} for rows and +-1/2 for queries, so that its MFMAs sum
+// the half L2 score q.b - pop(b) / 2 of the {0, 1} vectors (whose squared
+// L2 distance is the Hamming distance); the float merge finishes (L2
+// finalise: qpop - s = the distance, exact).  Returns false when the route
+// does not apply.
 bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* queries,
                   int64_t nq, int nbytes, int k, int32_t* ids, float* dists) {
   Arena& ar = ss.arena();
@@ -768,12 +769,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   };
   const uint32_t* bw = packed(rows, n);
   const uint32_t* qw = packed(queries, nq);
-  // row popcounts (the streamed scan sums its own)
-  float* bpop = nullptr;
-  if (!use_stream) {
-    bpop = ar.take<float>((size_t)n);
-    launch(s, "pack", [&] { return kern::launch_popcount_rows(bw, n, ldw, bpop, -0.5f, s); });
-  }
+  // the queries' popcounts finish the distances
   float* qpop = ar.take<float>((size_t)nq);
   launch(s, "pack", [&] { return kern::launch_popcount_rows(qw, nq, ldw, qpop, 1.0f, s); });
 
@@ -783,7 +779,7 @@ bool hamming_bits(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   const BoundPlan bp = shared_bound(k, T, slots, nseg);
   uint32_t* gkey = ar.take<uint32_t>((size_t)nq * slots);
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });
-  kern::FusedArgs fa{bw, qw, bpop, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,
+  kern::FusedArgs fa{bw, qw, nullptr, n, (int)nq, ldb, kern::kL2, plan.rows_per_split,
                      plan.nsplit, T, k, part, gkey, bp.m, bp.pubj, (int)qblocks,
                      plan.xcd ? 1 : 0};
   if (use_stream)

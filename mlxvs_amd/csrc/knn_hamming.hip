@@ -117,9 +117,12 @@ __global__ void pack_kernel(PackArgs a) {
 // For {0, 1} vectors the squared L2 distance is the Hamming distance and
 // sum b_i^2 is popcount(b), so the k-NN is the L2 one: s = 2 q.b - pop(b)
 // selected largest first, distance pop(q) - s.  The dot products run on the
-// FP4 MFMA, v_mfma_scale_f32_32x32x64_f8f6f4 with e2m1 operands (a code bit
-// becomes the value 0 or 1.0, scale 1.0; products of 1.0s summed in fp32 are
-// exact up to 2^24): per 128-bit chunk of the codes a row is 128 nibbles,
+// FP4 MFMA, v_mfma_scale_f32_32x32x64_f8f6f4 with e2m1 operands, scale 1.0:
+// a row bit becomes 0 or 1.0 and a query bit +0.5 (set) or -0.5 (clear), so
+// the MFMA sums b_i (q_i - 1/2) = q.b - pop(b) / 2 = s / 2 directly, with no
+// row popcounts and no epilogue (products and sums are multiples of 0.5
+// below 2^23: exact; zero padding bits of a row add nothing).  Per 128-bit
+// chunk of the codes a row is 128 nibbles,
 // two MFMA steps of 64 (lane half h supplies dwords 8 v + 4 h .. + 3 of step
 // v; any split of K works as long as rows and queries use the same).  An
 // earlier form ran v_mfma_i32_32x32x32_i8 on {0, 1} bytes: twice the
@@ -163,10 +166,19 @@ __device__ __forceinline__ void unpack_pair(uint32_t* dst, u32x2 x) {
   *(u32x4*)(dst + 4) = unpack_word(x[1]);
 }
 
-// A 128-bit chunk (four words) at dwords 0 .. 15 of dst: word w at 4 w.
+// A query word in the same order: nibble code 0x1 (+0.5) for a set bit,
+// 0x9 (-0.5) for a clear one.
+__device__ __forceinline__ u32x4 unpack_qword(uint32_t v) {
+  constexpr uint32_t m = 0x88888888u, c = 0x99999999u;
+  return u32x4{c ^ ((v << 3) & m), c ^ ((v << 2) & m), c ^ ((v << 1) & m), c ^ (v & m)};
+}
+
+// A 128-bit chunk (four words) at dwords 0 .. 15 of dst: word w at 4 w
+// (Q: query nibbles).
+template <bool Q = false>
 __device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) *(u32x4*)(dst + 4 * w) = unpack_word(x[w]);
+  for (int w = 0; w < 4; ++w) *(u32x4*)(dst + 4 * w) = Q ? unpack_qword(x[w]) : unpack_word(x[w]);
 }
 
 // QREG (codes of up to 128 bytes): each lane holds its query's B fragments
@@ -187,7 +199,6 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   __shared__ uint64_t cbuf[BUF ? CB * 256 : 1];
   __shared__ __align__(16) uint32_t tA[2][kBitsRows * kBitsStride];
   __shared__ __align__(16) uint32_t tQ[2][QREG ? 4 : kQueriesPerBlock * kBitsStride];
-  __shared__ __align__(16) float tnorm[2][kBitsRows];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -213,8 +224,6 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const int qrows = min(kQueriesPerBlock, a.nq - qb0);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const char*)a.queries + (int64_t)qb0 * ldb), (short)0, qrows * ldb, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.bnorm + r0), (short)0, nrows * 4, 0x00020000);
 
   // QREG: MFMA step v of chunk c takes, in lane half h, code word 4 c + 2 v + h
   u32x4 qf[QREG ? NCT : 1][2];
@@ -223,29 +232,24 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
-      for (int v = 0; v < 2; ++v) qf[c][v] = unpack_word(qvalid ? qr[4 * c + 2 * v + h] : 0u);
+      for (int v = 0; v < 2; ++v) qf[c][v] = unpack_qword(qvalid ? qr[4 * c + 2 * v + h] : 0u);
   }
 
   // The thread's fetch: QREG, words 2 p .. 2 p + 1 of each chunk of row
   // idx; otherwise the whole row idx (wavefronts 0-1) or query idx (2-3).
-  // Out-of-range rows read zero.  Every thread also fetches the norm of row
-  // idx (only row threads store it), so the wait counts are the same on
-  // every path.
+  // Out-of-range rows read zero.
   const int idx = tid & 127;
   const bool row_role = QREG || __builtin_amdgcn_readfirstlane(wave) < 2;
-  const bool stores_norm = QREG ? tid < 128 : row_role;
   const int part = QREG ? tid >> 7 : 0;
   uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 8 * part]
                              : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
   constexpr int kBuf = kBitsRows * kBitsStride;  // dwords per LDS buffer
   typedef typename std::conditional<QREG, u32x2, u32x4>::type frag_t;
   frag_t pk[NCT];
-  uint32_t pn = 0;
   const __amdgpu_buffer_rsrc_t rf = row_role ? rb : rq;
   // offset of the thread's fetch in the tile being fetched
   uint32_t roff = (uint32_t)(idx * ldb + 8 * part);
   const uint32_t rstep = row_role ? (uint32_t)(kBitsRows * ldb) : 0u;
-  uint32_t noff = (uint32_t)(idx * 4);
   auto fetch = [&](int c) {
     if constexpr (QREG)
       pk[c] = __builtin_amdgcn_raw_buffer_load_b64(rf, roff + 16 * c, 0, 0);
@@ -255,14 +259,14 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   auto unpack = [&](uint32_t* dst, frag_t x) {
     if constexpr (QREG)
       unpack_pair(dst, x);
+    else if (row_role)
+      unpack_chunk<false>(dst, x);
     else
-      unpack_chunk(dst, x);
+      unpack_chunk<true>(dst, x);
   };
 #pragma unroll
   for (int c = 0; c < NCT; ++c) fetch(c);
-  pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   roff += rstep;
-  noff += kBitsRows * 4;
 
   uint32_t K[T], I[T];
 #pragma unroll
@@ -283,9 +287,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 
   // chunk 0 of tile 0, then the refetch of chunk 0 for tile 1
   unpack(my0, pk[0]);
-  if (stores_norm) tnorm[0][idx] = __uint_as_float(pn);
   fetch(0);
-  pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   __syncthreads();
 
   floatx16 acc[4];
@@ -298,19 +300,6 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
     for (int c = 0; c < NCT; ++c) {
       if (c == 0 && share) seen.load(gk, a.mslots);
       const int buf = (NCT % 2 == 0) ? (c & 1) : par;
-      if (c == 0 && wave_on) {
-        // the accumulators start at the tile's -popcount / 2 (the norms
-        // array holds them) and end at the half score q.b - |b|^2 / 2 of
-        // the {0, 1} vectors: acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * r + 8 * jj + 4 * h];
-#pragma unroll
-            for (int w = 0; w < 4; ++w) acc[r][4 * jj + w] = hn[w];
-          }
-      }
       if (wave_on) {
         const uint32_t* arow = &tA[buf][col * kBitsStride + 4 * h];
 #pragma unroll
@@ -326,9 +315,13 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
             const i32x4 a4 = *(const i32x4*)(arow + r * 32 * kBitsStride + 8 * v);
             const i32x8 av = {a4[0], a4[1], a4[2], a4[3], 0, 0, 0, 0};
             // formats 4, 4: e2m1 A and B (only the first 4 registers are
-            // read); scales 0x7f: 2^0
+            // read); scales 0x7f: 2^0.  The tile's first step starts from
+            // zero (an inline constant), and the accumulators end at the
+            // half score q.b - pop(b) / 2 (the query's +-0.5 nibbles):
+            // acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
+            const floatx16 c0 = {};
             acc[r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                av, bq, acc[r], 4, 4, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+                av, bq, (c == 0 && v == 0) ? c0 : acc[r], 4, 4, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
           }
         }
       }
@@ -337,13 +330,8 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       const int j = (c + 1) % NCT;
       const int nb = buf ^ 1;
       unpack(my0 + nb * kBuf, pk[j]);
-      if (c == NCT - 1 && stores_norm) tnorm[(t + 1) & 1][idx] = __uint_as_float(pn);
-      if (j == 0) {
-        roff += rstep;
-        noff += kBitsRows * 4;
-      }
+      if (j == 0) roff += rstep;
       fetch(j);
-      if (j == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
       par ^= 1;
       __syncthreads();
     }
@@ -404,12 +392,10 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 // independent wavefronts per workgroup, no LDS and no barrier, as the fp32
 // stream kernel.  Lane (h, col) owns words [h NW / 2, (h + 1) NW / 2) of its
 // row and of query col: the query's words are unpacked to e2m1 nibbles once
-// (4 registers per word, one MFMA step per word), the row's packed words
+// (4 registers per word, one MFMA step per word; +-0.5 nibbles, so the
+// MFMA sums the half score q.b - pop(b) / 2), the row's packed words
 // arrive straight from HBM two tiles ahead and are unpacked at their step.
-// The row popcounts are summed from the same registers (each lane its
-// words, then the pair) and read as scalars for the score layout, so no
-// popcount pass over the base runs.  Segments: eight per workgroup,
-// 8 split + 2 w + h.
+// Segments: eight per workgroup, 8 split + 2 w + h.
 template <int NW, int T>
 __global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
   constexpr int HW = NW / 2;       // words per lane (one MFMA step each)
@@ -440,11 +426,7 @@ __global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (qvalid) w = qr[v];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t x = w[e];
-        qn[4 * v + e] = i32x4{(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u),
-                              (int)((x >> 1) & 0x22222222u), (int)((x >> 2) & 0x22222222u)};
-      }
+      for (int e = 0; e < 4; ++e) qn[4 * v + e] = __builtin_bit_cast(i32x4, unpack_qword(w[e]));
     }
   }
 
@@ -466,13 +448,11 @@ __global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
     floatx16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    uint32_t pc = 0;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t x = A[slot][v][e];
-        pc += __popc(x);
         const i32x8 av = {(int)((x << 1) & 0x22222222u), (int)(x & 0x22222222u),
                           (int)((x >> 1) & 0x22222222u), (int)((x >> 2) & 0x22222222u), 0, 0, 0, 0};
         const i32x4 b4 = qn[4 * v + e];
@@ -481,18 +461,10 @@ __global__ __launch_bounds__(256, 2) void stream_bits_kernel(FusedArgs a) {
                                                               0, 0x7f7f7f7f);
       }
     }
-    // row col's popcount (the pair's sums), then row 8 j + 4 h + u's at score
-    // slot 4 j + u, read from lane 8 j + 4 h + u as a scalar
-    const int pop = (int)pc + __shfl_xor((int)pc, 32);
+    // the score 2 q.b - pop(b) of row 8 j + 4 h + u at slot 4 j + u
     float sc[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int p0 = __builtin_amdgcn_readlane(pop, 8 * j + u);
-        const int p1 = __builtin_amdgcn_readlane(pop, 8 * j + 4 + u);
-        sc[4 * j + u] = __builtin_fmaf(2.0f, acc[4 * j + u], -(float)(h ? p1 : p0));
-      }
+    for (int i = 0; i < 16; ++i) sc[i] = 2.0f * acc[i];
     // the slot is consumed: refill it with the tile two ahead (out of range
     // past the end: zeros)
     issue(slot, i + 2);
