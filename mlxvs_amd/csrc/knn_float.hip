@@ -570,61 +570,62 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const int ntiles = (nrows + kDeepRows - 1) / kDeepRows;
   const int nsteps = ntiles * NC;
 
-  // buffer ranges: the split's rows, the block's queries, the split's norms;
-  // reads past them return zero
+  // The split's rows, the block's queries and the split's norms go through
+  // buffer resources built per chunk in scalar registers (base at the
+  // chunk, range = the bytes left), so a lane's offsets stay fixed and reads
+  // past the rows return zero: for a row r of the tile and chunk c the lane
+  // offset is r ld esize + 16 v (< 128), the range (rows left) ld esize - 128 c.
   const char* sbase = (const char*)a.base + r0 * ld * esize;
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)sbase, (short)0, nrows * ld * esize, 0x00020000);
+  const int srows_bytes = nrows * ld * esize;
   const int qrows = min(kQueriesPerBlock, a.nq - qb0);
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const char*)a.queries + (int64_t)qb0 * ld * esize), (short)0,
-      qrows * ld * esize, 0x00020000);
+  const char* qbase = (const char*)a.queries + (int64_t)qb0 * ld * esize;
+  const int qrows_bytes = qrows * ld * esize;
   const float* snorm = L2 ? a.bnorm + r0 : (const float*)a.base;
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
       (void*)snorm, (short)0, L2 ? nrows * 4 : 0, 0x00020000);
 
   // Lane l of load instruction j of wavefront w fills LDS vector p = 64 (w
   // NV + j) + l of a chunk buffer: row p / 8, slot p % 8, so it fetches
-  // vector (p % 8) ^ (row & 7) of that row, for the base rows and the queries
-  // alike.  Offsets of the next chunk to fetch are carried: +128 bytes per
-  // chunk, and at a tile end the row offsets move on by one tile while the
-  // query offsets return to chunk 0.
+  // vector (p % 8) ^ swz(row) of that row, for the base rows and the queries
+  // alike.  swz(r) = (r & 7) ^ (r >> 3 & 1): the sixteen rows whose 16-byte
+  // reads the LDS serves together (rows 128 bytes apart) then cover all 64
+  // banks.
   constexpr int NV = kDeepRows * (kDeepChunkBytes / 16) / 256;  // 4
-  uint32_t aoff[NV], qoff[NV];
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t voff[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int p = 64 * (wave * NV + j) + lane;
-    const int r = p >> 3, cv = (p & 7) ^ (r & 7);
-    const uint32_t o = (uint32_t)(r * ld * esize + 16 * cv);
-    aoff[j] = o;
-    qoff[j] = o;
+    const int r = p >> 3, cv = (p & 7) ^ ((r & 7) ^ ((r >> 3) & 1));
+    voff[j] = (uint32_t)(r * ld * esize + 16 * cv);
   }
   uint32_t noff = tid < kDeepRows ? tid * 4u : 0x80000000u;
-  const uint32_t row_wrap = (uint32_t)(kDeepRows * ld * esize) - (uint32_t)(NC * kDeepChunkBytes);
-  const uint32_t q_wrap = (uint32_t)(NC * kDeepChunkBytes);
 
   uint32_t pn = 0;
-  int pc = 0;  // chunk index of the next fetch
+  int pc = 0, pt = 0;  // chunk and tile of the next fetch
   auto issue_loads = [&](uint32_t* dA, uint32_t* dQ) {
+    // (signed max: a saturating unsigned subtract has no scalar form, and a
+    // resource computed in vector registers would need a loop per load;
+    // every byte count here is below 2^31)
+    const int cdone = pc * kDeepChunkBytes;
+    const int tc = pt * (kDeepRows * ld * esize) + cdone;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(sbase + tc), (short)0, max(srows_bytes - tc, 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(qbase + cdone), (short)0, max(qrows_bytes - cdone, 0), 0x00020000);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      load16_to_lds(rb, dA + 256 * (wave * NV + j), aoff[j]);
-      load16_to_lds(rq, dQ + 256 * (wave * NV + j), qoff[j]);
+      load16_to_lds(ra, dA + 256 * (wv * NV + j), voff[j]);
+      load16_to_lds(rq, dQ + 256 * (wv * NV + j), voff[j]);
     }
     if (L2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   };
-  // stores the fetched chunk's norms (at chunk 0 of a tile) and advances the
-  // offsets
+  // stores the fetched chunk's norms (at chunk 0 of a tile) and moves on
   auto store_chunk = [&](int tpar) {
     if (L2 && pc == 0 && tid < kDeepRows) tnorm[tpar][tid] = __uint_as_float(pn);
-    const bool wrap = ++pc == NC;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      aoff[j] += wrap ? row_wrap + kDeepChunkBytes : kDeepChunkBytes;
-      qoff[j] += wrap ? kDeepChunkBytes - q_wrap : kDeepChunkBytes;
-    }
-    if (wrap) {
+    if (++pc == NC) {
       pc = 0;
+      ++pt;
       noff += kDeepRows * 4;
     }
   };
@@ -659,9 +660,12 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   // step s: chunk c of tile t from (cA, cQ); the next chunk into (nA, nQ)
   auto step = [&](const uint32_t* cA, const uint32_t* cQ, uint32_t* nA, uint32_t* nQ) {
     // the bound is used at the tile's last chunk: read it in that step only
+    const bool last = c + 1 == NC;
     SharedBound<S> seen;
-    seen.clear();
-    if (share && c + 1 == NC) seen.load(gk, a.mslots);
+    if (last) {
+      seen.clear();
+      if (share) seen.load(gk, a.mslots);
+    }
     // the fetched tile's parity, read before store_chunk advances pc
     const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
     issue_loads(nA, nQ);
@@ -671,7 +675,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
       // 32 r share the swizzle of col)
       const uint32_t* qrow = cQ + (qw + col) * kDeepChunkDwords;
       const uint32_t* arow = cA + (32 * rb0 + col) * kDeepChunkDwords;
-      const int sw = col & 7;
+      const int sw = (col & 7) ^ ((col >> 3) & 1);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if constexpr (F16) {
@@ -697,7 +701,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
         }
       }
     }
-    if (c + 1 == NC) {
+    if (last) {
       __builtin_amdgcn_sched_barrier(0);
       if (wave_on) {
         if (share) thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
