@@ -24,8 +24,11 @@ The same JSON line carries:
   cpu_baseline  the CPU restatement of the reference path (oracle/, a port:
                 the reference itself runs only on Apple GPUs) timed on this
                 host's cores over a bounded query sample;
-  check         the last step's answers for the first 64 queries against the
-                float64 golden fixture (bit-exact, integer-valued data).
+  check         the last step's answers against the CPU restatement for the
+                queries it answered (bit-exact on integer-valued data; float
+                data: distances within the tests' tolerance and the share of
+                equal ids) and, where a fixture exists, the first queries
+                against the float64 golden fixture.
 
 Other workloads (c1, c2h, c3, c3cos, c3h, c4, c5, ivf, topk) are for measurement runs; the
 driver's line is the default.  --workload copy times a 1 GiB device copy, the
@@ -394,7 +397,7 @@ def main() -> int:
     # the whole GPU answer for the queries the CPU restatement answered
     # (bit-exact on integer-valued data; float data: ids and distances to
     # the tolerances the tests use)
-    if cpu_out is not None and w["kind"] in ("float", "hamming", "topk") and not args.nq:
+    if cpu_out is not None and not args.nq:
         oi, od = cpu_out
         m = oi.shape[0]
         if w["kind"] == "topk":
@@ -407,6 +410,20 @@ def main() -> int:
         if same is not None:
             full = f"{m} of {nq} rows vs the CPU restatement: {'bit-exact' if same else 'MISMATCH'}"
             check = full if check is None else f"{full}; {check}"
+        elif w["kind"] in ("float", "self", "ivf"):
+            # float data: the distances within the tests' tolerance, and the
+            # share of equal ids (near-equal scores may swap places)
+            if w["kind"] == "self":
+                # the restatement's k + 1 include the row itself: drop it
+                keep = oi != np.arange(m)[:, None]
+                keep[keep.sum(1) > w["k"], -1] = False
+                oi = oi[keep].reshape(m, w["k"])
+                od = od[keep].reshape(m, w["k"])
+            tol = 2e-3 if base.dtype == np.float16 else 1e-4
+            close = np.allclose(dist[:m], od, rtol=tol, atol=tol)
+            share = float((ids[:m] == oi).mean())
+            check = (f"{m} of {nq} rows vs the CPU restatement: distances within {tol:g} "
+                     f"{'yes' if close else 'NO'}, ids equal {100 * share:.2f}%")
     e2e = host_api_ms(w) if args.e2e else None
 
     line = {
