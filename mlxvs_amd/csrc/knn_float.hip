@@ -368,16 +368,19 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  // the shared bound, read every 4th tile (a stale bound is still a bound,
-  // and the reads of a query's bound words are what sharing costs)
+  // the shared bound, read at each of the first 8 tiles (while the lists
+  // fill, most candidates pass and a fresh bound stops the most) and every
+  // 4th tile after (a stale bound is still a bound, and the reads of a
+  // query's bound words are what sharing costs)
   SharedBound<S> seen;
   seen.clear();
+  auto bound_tile = [](int t) { return (t & 3) == 0 || t < 8; };
   // tile t from (cur, ncur); tile t + 1 into (nxt, nnxt)
   auto step = [&](const E* cur, const float* ncur, E* nxt, float* nnxt, int t) {
     // read before the tile prefetch, so that waiting for it (in the
     // epilogue) does not wait for the prefetch
     if constexpr (MODE != 2)
-      if (share && (t & 3) == 0) seen.load(gk, a.mslots);
+      if (share && bound_tile(t)) seen.load(gk, a.mslots);
     // the next tile into the other buffer (read in the previous tile, which
     // every wavefront has left: the barrier below); unconditional (past the
     // last tile the range is empty and the loads write zeros)
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       }
       __builtin_amdgcn_sched_barrier(0);
       // the bound changes only where it was read
-      if (MODE != 2 && share && (t & 3) == 0)
+      if (MODE != 2 && share && bound_tile(t))
         thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
       bool inserted = false;
       // lists of 16 (k > 10, often k > 16: many lanes pass): the two blocks
