@@ -112,7 +112,10 @@ __device__ __forceinline__ uint32_t key_nz(float v) {
 // is false before that slot and true from it on, and
 //   K'[j] = median(K[j-1], kc, K[j])      (K[-1] = all ones)
 //   I'[j] = g_j ? (g_{j-1} ? I[j-1] : ic) : I[j]
-// One median, one compare and two selects per slot.
+// One median, one compare and two selects per slot.  The slots are updated
+// from the last to the first, so slot j's old entry is last read (by slot j
+// + 1 and by itself) before its new one is written: the list is updated in
+// place, with no copies in a loop that inserts over and over.
 __device__ __forceinline__ uint32_t median3(uint32_t a, uint32_t b, uint32_t c) {
   return max(min(a, b), min(max(a, b), c));
 }
@@ -120,18 +123,16 @@ __device__ __forceinline__ uint32_t median3(uint32_t a, uint32_t b, uint32_t c) 
 template <int T>
 __device__ __forceinline__ void stream_insert(uint32_t (&K)[T], uint32_t (&I)[T], uint32_t kc,
                                               uint32_t ic) {
-  uint32_t kp = 0xffffffffu, ip = 0;
-  bool gp = false;
+  bool g = kc > K[T - 1];
 #pragma unroll
-  for (int j = 0; j < T; ++j) {
-    const uint32_t kj = K[j], ij = I[j];
-    const bool g = kc > kj;
-    K[j] = median3(kp, kc, kj);
-    I[j] = g ? (gp ? ip : ic) : ij;
-    kp = kj;
-    ip = ij;
-    gp = g;
+  for (int j = T - 1; j > 0; --j) {
+    const bool gp = kc > K[j - 1];
+    K[j] = median3(K[j - 1], kc, K[j]);
+    I[j] = g ? (gp ? I[j - 1] : ic) : I[j];
+    g = gp;
   }
+  K[0] = max(kc, K[0]);
+  I[0] = g ? ic : I[0];
 }
 
 // sc[i] for a per-lane i in [0, 16): a select tree on the bits of i.
@@ -197,12 +198,16 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
   for (int i = 0; i < 16; ++i) pm |= !(sc[i] < thr) ? (1u << i) : 0u;
   if (lim < 32) pm &= real_rows(h, lim);
   const bool any = pm != 0;
-  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
-    const int i = pm ? __builtin_ctz(pm) : 0;
-    const float x = HALF ? 2.0f * pick16(sc, i) : pick16(sc, i);
-    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-    stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
-    pm &= pm - 1u;
+  // (a guarded do-while: the list's registers then carry straight round
+  // the loop, where a while loop copies them at every iteration)
+  if (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+    do {
+      const int i = pm ? __builtin_ctz(pm) : 0;
+      const float x = HALF ? 2.0f * pick16(sc, i) : pick16(sc, i);
+      const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+      stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
+      pm &= pm - 1u;
+    } while (__builtin_amdgcn_ballot_w64(pm != 0) != 0);
   }
   // Own filter: a later candidate needs a strictly larger key than the
   // list's last (an equal key has a larger id and would not enter), so the
@@ -239,17 +244,19 @@ __device__ __forceinline__ bool select_pair(uint32_t (&K)[T], uint32_t (&I)[T], 
   }
   if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
   const bool any = pm != 0;
-  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
-    const int i = pm ? __builtin_ctz(pm) : 0;
-    const bool b = i & 16;
-    float s[16];
+  if (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+    do {
+      const int i = pm ? __builtin_ctz(pm) : 0;
+      const bool b = i & 16;
+      float s[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = b ? sc1[e] : sc0[e];
-    const int j = i & 15;
-    const float x = HALF ? 2.0f * pick16(s, j) : pick16(s, j);
-    const int m = (b ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
-    stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
-    pm &= pm - 1u;
+      for (int e = 0; e < 16; ++e) s[e] = b ? sc1[e] : sc0[e];
+      const int j = i & 15;
+      const float x = HALF ? 2.0f * pick16(s, j) : pick16(s, j);
+      const int m = (b ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
+      stream_insert<T>(K, I, pm ? key_nz(x) : 0u, id0 + m);
+      pm &= pm - 1u;
+    } while (__builtin_amdgcn_ballot_w64(pm != 0) != 0);
   }
   thr = fmaxf(thr, filter_of<HALF>(score_of_key(K[T - 1] + 1u)));
   return any;
@@ -321,7 +328,9 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
   uint32_t pm = ~fm;
   if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
   bool flushed = false;
-  while (__builtin_amdgcn_ballot_w64(pm != 0) != 0) {
+  if (__builtin_amdgcn_ballot_w64(pm != 0) == 0) return false;
+  // (a guarded do-while, as in select_block)
+  do {
     if (__builtin_amdgcn_ballot_w64(cb.cnt == B) != 0) {
       flush_buf<T, HALF, B, S>(K, I, thr, cb);
       flushed = true;
@@ -335,7 +344,7 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
       ++cb.cnt;
       pm &= pm - 1u;
     }
-  }
+  } while (__builtin_amdgcn_ballot_w64(pm != 0) != 0);
   return flushed;
 }
 
