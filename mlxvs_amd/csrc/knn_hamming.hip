@@ -197,7 +197,13 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   constexpr bool BUF = T == 16;
   constexpr int CB = 6;
   __shared__ uint64_t cbuf[BUF ? CB * 256 : 1];
-  __shared__ __align__(16) uint32_t tA[2][kBitsRows * kBitsStride];
+  // chunks unpacked per stage (one barrier each): two where the queries sit
+  // in registers (the stage buffers then take 40 KB), so a wavefront runs 16
+  // MFMAs between barriers instead of 8
+  constexpr int CPS = (QREG && NCT % 2 == 0) ? 2 : 1;
+  constexpr int NST = NCT / CPS;                   // stages per tile
+  constexpr int kChunk = kBitsRows * kBitsStride;  // dwords per unpacked chunk
+  __shared__ __align__(16) uint32_t tA[2][CPS * kChunk];
   __shared__ __align__(16) uint32_t tQ[2][QREG ? 4 : kQueriesPerBlock * kBitsStride];
 
   const int tid = threadIdx.x;
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const int part = QREG ? tid >> 7 : 0;
   uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 8 * part]
                              : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
-  constexpr int kBuf = kBitsRows * kBitsStride;  // dwords per LDS buffer
+  constexpr int kBuf = CPS * kChunk;  // dwords per LDS buffer
   typedef typename std::conditional<QREG, u32x2, u32x4>::type frag_t;
   frag_t pk[NCT];
   const __amdgpu_buffer_rsrc_t rf = row_role ? rb : rq;
@@ -285,9 +291,11 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const int myslot = share ? (2 * split + h) % a.mslots : 0;
   uint32_t pend = 0;  // slot value returned by the last publish (used a tile later)
 
-  // chunk 0 of tile 0, then the refetch of chunk 0 for tile 1
-  unpack(my0, pk[0]);
-  fetch(0);
+  // stage 0 of tile 0, then the refetch of its chunks for tile 1
+#pragma unroll
+  for (int u = 0; u < CPS; ++u) unpack(my0 + u * kChunk, pk[u]);
+#pragma unroll
+  for (int u = 0; u < CPS; ++u) fetch(u);
   __syncthreads();
 
   floatx16 acc[4];
@@ -297,11 +305,14 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
     SharedBound<S> seen;
     seen.clear();
 #pragma unroll
-    for (int c = 0; c < NCT; ++c) {
-      if (c == 0 && share) seen.load(gk, a.mslots);
-      const int buf = (NCT % 2 == 0) ? (c & 1) : par;
+    for (int st = 0; st < NST; ++st) {
+      if (st == 0 && share) seen.load(gk, a.mslots);
+      const int buf = (NST % 2 == 0) ? (st & 1) : par;
+#pragma unroll
+      for (int u = 0; u < CPS; ++u) {
+      const int c = st * CPS + u;
       if (wave_on) {
-        const uint32_t* arow = &tA[buf][col * kBitsStride + 4 * h];
+        const uint32_t* arow = &tA[buf][u * kChunk + col * kBitsStride + 4 * h];
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
           i32x4 bq4;
@@ -325,13 +336,16 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
           }
         }
       }
-      // the next chunk (j of this tile, or chunk 0 of the next) into the
-      // other buffer, then the refetch of chunk j one tile further
-      const int j = (c + 1) % NCT;
+      }
+      // the next stage's chunks (of this tile, or stage 0 of the next) into
+      // the other buffer, then their refetch one tile further
+      const int j = ((st + 1) % NST) * CPS;
       const int nb = buf ^ 1;
-      unpack(my0 + nb * kBuf, pk[j]);
+#pragma unroll
+      for (int u = 0; u < CPS; ++u) unpack(my0 + nb * kBuf + u * kChunk, pk[j + u]);
       if (j == 0) roff += rstep;
-      fetch(j);
+#pragma unroll
+      for (int u = 0; u < CPS; ++u) fetch(j + u);
       par ^= 1;
       __syncthreads();
     }
