@@ -444,6 +444,8 @@ int max_merge_segments(int k, int T) {
 // wavefront; a small batch's thousands of lists thus merge on many CUs in a
 // few short steps instead of one workgroup's sort.  flags (T < k) as
 // merge_kernel, from the sentinels the levels pass on.
+// The part lists are stream lists, sorted best first (the merge's sort
+// starts from the sorted runs).
 void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T, int k,
                  int64_t nq, int metric, const float* qnorm, int dist_mode, int32_t* ids,
                  float* dists, int* flags) {
@@ -464,7 +466,7 @@ void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T
     uint64_t* out = ar.take<uint64_t>((size_t)nq * ngroups * g.keep);
     uint64_t* sent = flags ? ar.take<uint64_t>((size_t)nq * ngroups) : nullptr;
     kern::MergeGroupArgs mg{mpart, mseg, mT, (int)nq, gs, ngroups, g.keep, out, sent,
-                            first ? nullptr : sentinel};
+                            first ? nullptr : sentinel, first ? 1 : 0};
     launch(s, "merge", [&] { return kern::launch_merge_group(mg, s); });
     mpart = out;
     mseg = ngroups;
@@ -473,7 +475,7 @@ void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T
     first = false;
   }
   kern::MergeArgs ma{mpart, mseg, mT, k, (int)nq, metric, qnorm, dist_mode, ids, dists, flags,
-                     sentinel};
+                     sentinel, first ? 1 : 0};
   launch(s, "merge", [&] { return kern::launch_merge(ma, s); });
 }
 

@@ -1027,10 +1027,14 @@ __global__ __launch_bounds__(256) void select_group_kernel(MergeGroupArgs a) {
 // best by rank, the overflow flags, the reference's output order (the rank
 // order except that -0 and +0 scores tie and fall back to the id: when a -0
 // key is among the k, the k are sorted again by that order), distances.
+// first > 2: the blocks of first / 2 are already sorted, descending and
+// ascending in turn (what the network's earlier phases would leave), so the
+// sort starts at the merge of blocks of that size.
 template <int E>
-__device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, bool out_order) {
+__device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, bool out_order,
+                                             int first = 2) {
   auto ord = [&](uint64_t r) { return out_order ? output_order(r) : r; };
-  for (int size = 2; size <= P; size <<= 1) {
+  for (int size = first; size <= P; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       if (stride >= E) {
         const int lm = stride / E;  // partner lane distance
@@ -1062,6 +1066,21 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, 
   }
 }
 
+// Candidate i of a merge's input in the order wave_bitonic starts from:
+// when the input is lists of T ranks each sorted best first (sorted) and T
+// is a power of two, the odd lists are read back to front, so that the blocks of T
+// alternate descending and ascending and the sort can skip its first
+// log2(T) phases (see run_start).
+__device__ __forceinline__ bool runs_of(int T, int sorted) {
+  return sorted && T >= 2 && (T & (T - 1)) == 0;
+}
+__device__ __forceinline__ int run_index(int i, int T, int sorted) {
+  return runs_of(T, sorted) && ((i / T) & 1) ? (i ^ (T - 1)) : i;
+}
+__device__ __forceinline__ int run_start(int T, int sorted, int P) {
+  return (runs_of(T, sorted) && 2 * T <= P) ? 2 * T : 2;
+}
+
 // The largest of the wavefront's values.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t m) {
 #pragma unroll
@@ -1084,7 +1103,7 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
   uint64_t x[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int i = lane * E + e;
+    const int i = run_index(lane * E + e, a.T, a.sorted);
     x[e] = i < C ? src[i] : 0;
   }
   const bool l2 = a.metric == kL2;
@@ -1147,7 +1166,7 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
     if (lane < a.k) emit(slot, best);
     return;
   }
-  wave_bitonic<E>(x, lane, P, false);
+  wave_bitonic<E>(x, lane, P, false, run_start(a.T, a.sorted, P));
   // the k-th best rank (element k - 1), broadcast
   const int kl = (a.k - 1) / E, ke = (a.k - 1) % E;
   uint64_t mine = 0;
@@ -1197,7 +1216,7 @@ __global__ __launch_bounds__(256) void merge_group_wave_kernel(MergeGroupArgs a)
   uint64_t x[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int i = lane * E + e;
+    const int i = run_index(lane * E + e, a.T, a.sorted);
     x[e] = i < C ? src[i] : 0;
   }
   if (a.sentinel) {
@@ -1210,7 +1229,7 @@ __global__ __launch_bounds__(256) void merge_group_wave_kernel(MergeGroupArgs a)
     m = wave_max_u64(m);
     if (lane == 0) a.sentinel[(int64_t)q * a.ngroups + g] = m;
   }
-  wave_bitonic<E>(x, lane, 64 * E, false);
+  wave_bitonic<E>(x, lane, 64 * E, false, run_start(a.T, a.sorted, 64 * E));
   uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.keep;
 #pragma unroll
   for (int e = 0; e < E; ++e) {

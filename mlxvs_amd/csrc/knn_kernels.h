@@ -217,6 +217,7 @@ struct MergeArgs {
   // the worst entries of the group's full segment lists (0: none); the
   // per-list check then uses these instead of the lists' last entries
   const uint64_t* sentinel;
+  int sorted;            // 1: each list of T is sorted best first (stream lists)
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
@@ -241,6 +242,7 @@ struct MergeGroupArgs {
   // pass on (the largest of the group's); null: lists of T from the kernels,
   // sentinel = the largest last entry of the group's full lists
   const uint64_t* in_sentinel;
+  int sorted;            // 1: each list of T is sorted best first (stream lists)
 };
 hipError_t launch_merge_group(const MergeGroupArgs& a, hipStream_t s);
 
