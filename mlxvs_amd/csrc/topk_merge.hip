@@ -661,6 +661,11 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
       __syncthreads();
       for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
       __syncthreads();
+    } else if (cnt < keff) {
+      // a rank source with fewer than keff ranks (its zeros are no
+      // element): the rest of the k are empty
+      for (int i = cnt + tid; i < keff; i += NT) sm.buf[i] = 0;
+      __syncthreads();
     }
   }
   // the output order (unless the caller takes the set unordered)

@@ -183,3 +183,18 @@ def test_few_queries_scan(engine, oracle, nq, nbytes, n, k):
     oid, odist = oracle.hamming(x, q, k)
     assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
     assert not np.signbit(dist).any()
+
+
+@pytest.mark.parametrize("n", [1, 21, 255])
+@pytest.mark.parametrize("k", [44, 256])
+def test_few_queries_scan_under_k_rows(engine, oracle, n, k):
+    # fewer rows than k at four queries (the scan path): the splits' lists
+    # hold n ranks between them, and the rest of the k slots come out empty
+    # (-1 / +inf), not as whatever the merge's buffer held before
+    rng = np.random.default_rng(n + k)
+    x = rng.integers(0, 256, (n, 71), dtype=np.uint8)
+    q = rng.integers(0, 256, (4, 71), dtype=np.uint8)
+    ids, dist = engine.hamming_knn(x, q, k)
+    oid, odist = oracle.hamming(x, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    assert (ids[:, n:] == -1).all() and (dist[:, n:] == np.inf).all()
