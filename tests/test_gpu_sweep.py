@@ -1,5 +1,6 @@
 """A seeded sweep over shapes, list lengths and metrics: the HIP engine
-against the CPU restatement, bit for bit.
+against the CPU restatement, bit for bit (exact k-NN over fp32 and fp16
+rows, Hamming codes, IVF-Flat, the self k-NN graph and topk_merge).
 
 Every case draws its sizes from a fixed generator (log-uniform row and
 query counts, dimensions, code widths and k up to 256), so the sweep
@@ -63,3 +64,72 @@ def test_hamming_sweep(engine, oracle, seed):
     case = f"n={n} nq={nq} bytes={nbytes} k={k}"
     assert np.array_equal(ids, oid), case
     assert np.array_equal(dist, odist), case
+
+
+def ivf_index(x, lists):
+    c = x[:: max(1, x.shape[0] // lists)][:lists].astype(np.float32)
+    d2 = ((x[:, None, :].astype(np.float64) - c[None].astype(np.float64)) ** 2).sum(-1)
+    lab = d2.argmin(1)
+    order = np.argsort(lab, kind="stable")
+    off = np.concatenate([[0], np.cumsum(np.bincount(lab, minlength=c.shape[0]))]).astype(np.int32)
+    return c, x[order].astype(np.float32), order.astype(np.int32), off
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_ivf_sweep(oracle, seed):
+    import mlxvs_amd
+
+    rng = np.random.default_rng(3000 + seed)
+    n = log_int(rng, 1, 20_000)
+    d = log_int(rng, 1, 300)
+    lists = max(1, min(n, log_int(rng, 1, 256)))
+    nq = log_int(rng, 1, 500)
+    n_probes = max(1, min(lists, log_int(rng, 1, 64)))
+    k = log_int(rng, 1, 256)
+    metric = "l2" if seed % 2 == 0 else "inner_product"
+    x = rng.integers(-4, 5, (n, d)).astype(np.float32)
+    q = rng.integers(-4, 5, (nq, d)).astype(np.float32)
+    c, data, ind, off = ivf_index(x, lists)
+    ids, dist = mlxvs_amd.ivf_flat_search(c, data, ind, off, metric, q, k, n_probes=n_probes)
+    wi, wd = oracle.ivf_flat(c, data, ind, off, q, k, n_probes, metric)
+    case = f"n={n} d={d} lists={c.shape[0]} nq={nq} probes={n_probes} k={k} {metric}"
+    assert np.array_equal(ids, wi), case
+    assert np.array_equal(dist, wd), case
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_self_graph_sweep(engine, oracle, seed):
+    rng = np.random.default_rng(4000 + seed)
+    f16 = seed % 3 == 2
+    n = max(2, log_int(rng, 1, 20_000))  # the route needs two rows
+    d = log_int(rng, 1, 256)
+    k = log_int(rng, 1, 128)
+    metric = "l2" if seed % 2 == 0 else "inner_product"
+    x = rng.integers(-4, 5, (n, d)).astype(np.float16 if f16 else np.float32)
+    ids, dist = engine.all_neighbors(x, k, metric)
+    oid, odist = oracle.self_graph(oracle.f16_to_f32(x) if f16 else x, k, metric)
+    case = f"n={n} d={d} k={k} {metric} {'fp16' if f16 else 'fp32'}"
+    assert np.array_equal(ids, oid), case
+    assert np.array_equal(dist, odist), case
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_topk_merge_sweep(engine, oracle, seed):
+    rng = np.random.default_rng(5000 + seed)
+    nq = log_int(rng, 1, 300)
+    t = log_int(rng, 1, 70_000)
+    k = log_int(rng, 1, 256)
+    first = seed % 3 != 0
+    off = int(rng.integers(-(1 << 20), 1 << 20))
+    s = rng.integers(-30, 30, (nq, t)).astype(np.float32)
+    if first:
+        pi = pb = None
+    else:
+        pb = np.sort(rng.integers(-30, 30, (nq, k)).astype(np.float32), axis=1)[:, ::-1].copy()
+        pi = rng.integers(0, 1 << 20, (nq, k)).astype(np.int32)
+    gi, gs = engine.topk_merge(s, pi, pb, off, first, k)
+    oi, os_ = oracle.topk_merge(s, pi, pb, off, first, k)
+    case = f"nq={nq} t={t} k={k} first={first} off={off}"
+    assert np.array_equal(gi, oi), case
+    assert np.array_equal(np.asarray(gs, np.float32).view(np.uint32),
+                          np.asarray(os_, np.float32).view(np.uint32)), case
