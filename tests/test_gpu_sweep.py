@@ -133,3 +133,61 @@ def test_topk_merge_sweep(engine, oracle, seed):
     assert np.array_equal(gi, oi), case
     assert np.array_equal(np.asarray(gs, np.float32).view(np.uint32),
                           np.asarray(os_, np.float32).view(np.uint32)), case
+
+
+def test_device_calls_queued_on_two_streams(engine, oracle):
+    # 24 device calls of mixed shapes and routes (float fp32 / fp16, Hamming,
+    # self graph) queued back to back on two streams with no wait between
+    # them: each call's workspace is reused by the next, so every result must
+    # still equal the restatement's once both streams drain
+    from mlxvs_amd import _hip
+
+    streams = [_hip.Stream(), _hip.Stream()]
+    keep, checks = [], []
+    rng = np.random.default_rng(6000)
+    for i in range(24):
+        st = streams[i % 2].handle.value
+        kind = ("float", "f16", "hamming", "self")[i % 4]
+        n, k = log_int(rng, 2, 30_000), log_int(rng, 1, 200)
+        if kind == "hamming":
+            nbytes, nq = log_int(rng, 1, 128), log_int(rng, 1, 300)
+            x = rng.integers(0, 256, (n, nbytes), dtype=np.uint8)
+            q = rng.integers(0, 256, (nq, nbytes), dtype=np.uint8)
+            dx, dq = _hip.DeviceBuffer.from_array(x), _hip.DeviceBuffer.from_array(q)
+            di, dd = _hip.DeviceBuffer(nq * k * 4), _hip.DeviceBuffer(nq * k * 4)
+            engine.hamming_knn_device(dx.value, n, dq.value, nq, nbytes, k, di.value, dd.value,
+                                      stream=st)
+            want = lambda x=x, q=q, k=k: oracle.hamming(x, q, k)
+        elif kind == "self":
+            d = log_int(rng, 1, 128)
+            x = rng.integers(-4, 5, (n, d)).astype(np.float32)
+            nq = n
+            dx = _hip.DeviceBuffer.from_array(x)
+            dq = None
+            di, dd = _hip.DeviceBuffer(n * k * 4), _hip.DeviceBuffer(n * k * 4)
+            engine.knn_self_graph_device(dx.value, n, d, k, "l2", di.value, dd.value, stream=st)
+            want = lambda x=x, k=k: oracle.self_graph(x, k, "l2")
+        else:
+            f16 = kind == "f16"
+            d, nq = log_int(rng, 1, 256), log_int(rng, 1, 500)
+            metric = "l2" if i % 3 else "inner_product"
+            dt = np.float16 if f16 else np.float32
+            x = rng.integers(-4, 5, (n, d)).astype(dt)
+            q = rng.integers(-4, 5, (nq, d)).astype(dt)
+            dx, dq = _hip.DeviceBuffer.from_array(x), _hip.DeviceBuffer.from_array(q)
+            di, dd = _hip.DeviceBuffer(nq * k * 4), _hip.DeviceBuffer(nq * k * 4)
+            engine.brute_force_knn_device(dx.value, n, dq.value, nq, d, k, metric, di.value,
+                                          dd.value, f16=f16, stream=st)
+            ox = oracle.f16_to_f32(x) if f16 else x
+            oq = oracle.f16_to_f32(q) if f16 else q
+            want = lambda ox=ox, oq=oq, k=k, metric=metric: oracle.knn(ox, oq, k, metric)
+        keep.append((dx, dq, di, dd))
+        checks.append((f"call {i} {kind} n={n} nq={nq} k={k}", di, dd, nq, k, want))
+    for s in streams:
+        s.synchronize()
+    for case, di, dd, nq, k, want in checks:
+        ids = di.download((nq, k), np.int32)
+        dist = dd.download((nq, k), np.float32)
+        oid, odist = want()
+        assert np.array_equal(ids, oid), case
+        assert np.array_equal(dist, odist), case
