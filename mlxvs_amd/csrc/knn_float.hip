@@ -180,6 +180,16 @@ __device__ __forceinline__ void load4_to_lds(__amdgpu_buffer_rsrc_t r, void* lds
 #endif
 }
 
+// A workgroup barrier after this wavefront's outstanding vector-memory
+// operations -- its LDS-direct loads among them -- have completed: an LDS
+// buffer that every wavefront fills with LDS-direct loads is whole once all
+// have passed it.  (The barrier's own workgroup-scope fence does not wait
+// for loads, so the wait is explicit.)
+__device__ __forceinline__ void dma_barrier() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), no other counter
+  __syncthreads();
+}
+
 // 32-row MFMA blocks per streamed tile: two where the registers allow, which
 // halves the barriers and per-tile overhead per row.  One where the query
 // fragments take 128 VGPRs (fp32, 256 dims): the second accumulator and
@@ -362,6 +372,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const int myslot = share ? (2 * seg + h) % a.mslots : 0;
 
   if (ntiles > 0) issue_loads(tile0, tnorm0, 0);
+  // LATE (the buffered select): the select of tile t runs after the
+  // barrier that ends its MFMAs, and tile t + 2 is fetched into tile t's
+  // buffers after it, so two tiles are fetched ahead here
+  constexpr bool LATE = BUF;
+  if (LATE && ntiles > 0) issue_loads(tile1, tnorm1, 1);
   // nothing may be outstanding at the loop head: the query fragments are
   // read in every iteration, and a pending prologue load would otherwise
   // make each iteration wait for its own tile prefetch as well
@@ -375,8 +390,9 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   SharedBound<S> seen;
   seen.clear();
   auto bound_tile = [](int t) { return (t & 3) == 0 || t < 8; };
-  // tile t from (cur, ncur); tile t + 1 into (nxt, nnxt)
-  auto step = [&](const E* cur, const float* ncur, E* nxt, float* nnxt, int t) {
+  // tile t from (cur, ncur); tile t + 1 into (nxt, nnxt) (LATE: tile t + 2
+  // into (cur, ncur), after the select)
+  auto step = [&](E* cur, float* ncur, E* nxt, float* nnxt, int t) {
     // read before the tile prefetch, so that waiting for it (in the
     // epilogue) does not wait for the prefetch
     if constexpr (MODE != 2)
@@ -384,13 +400,13 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     // the next tile into the other buffer (read in the previous tile, which
     // every wavefront has left: the barrier below); unconditional (past the
     // last tile the range is empty and the loads write zeros)
-    issue_loads(nxt, nnxt, t + 1);
+    if constexpr (!LATE) issue_loads(nxt, nnxt, t + 1);
     __builtin_amdgcn_sched_barrier(0);
+    // L2: the accumulators start at the rows' -|b|^2 / 2 (the norms array
+    // holds them), so they end at the half score q.b - |b|^2 / 2 with no
+    // epilogue arithmetic: acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
+    floatx16 acc[RB];
     if (wave_on) {
-      // L2: the accumulators start at the rows' -|b|^2 / 2 (the norms array
-      // holds them), so they end at the half score q.b - |b|^2 / 2 with no
-      // epilogue arithmetic: acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
-      floatx16 acc[RB];
 #pragma unroll
       for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -431,7 +447,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
                                                             0, 0);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // LATE: tile t + 1 has landed and every wavefront is done with cur
+    if constexpr (LATE) dma_barrier();
+    if (wave_on) {
       // the bound changes only where it was read
       if (MODE != 2 && share && bound_tile(t))
         thr = fmaxf(thr, filter_of<L2>(score_of_key(seen.bound())));
@@ -481,14 +501,20 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // this wavefront's LDS-direct loads have landed (the barrier's fence
-    // waits for them), and every wavefront is done with cur
-    __syncthreads();
+    if constexpr (LATE) {
+      issue_loads(cur, ncur, t + 2);
+    } else {
+      // every wavefront's LDS-direct loads of tile t + 1 have landed, and
+      // every wavefront is done with cur
+      dma_barrier();
+    }
   };
   for (int t = 0; t < ntiles; t += 2) {
     step(tile0, tnorm0, tile1, tnorm1, t);
     if (t + 1 < ntiles) step(tile1, tnorm1, tile0, tnorm0, t + 1);
   }
+  // LATE: the fetches past the last tile land before the workgroup ends
+  if constexpr (LATE) __builtin_amdgcn_s_waitcnt(0);
   // what is left in the candidate buffer (a wavefront-uniform loop)
   if constexpr (BUF) flush_buf<T, L2, CB, 256>(K, I, thr, cb);
 
@@ -743,9 +769,9 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
     store_chunk(ftpar);
-    // this wavefront's loads of the next chunk have landed (the barrier's
-    // fence waits for them), and every wavefront is done with this one
-    __syncthreads();
+    // every wavefront's loads of the next chunk have landed, and every
+    // wavefront is done with this one
+    dma_barrier();
     if (++c == NC) {
       c = 0;
       ++t;
