@@ -190,6 +190,20 @@ __device__ __forceinline__ void dma_barrier() {
   __syncthreads();
 }
 
+// Wait states between a barrier and the first read of MFMA results issued
+// before it.  The compiler's MFMA-to-VALU dependency count includes the
+// barrier and the wait in front of it, which need not take a cycle (a
+// wavefront that arrives last passes both at once): reading the last
+// accumulator registers first, at the count it derived, gave stale values
+// now and then (lists that lost a candidate, measured on the GPU: gone with
+// 8 more wait states, not with 1).  Sixteen that the compiler does not
+// count (inline), fenced so that nothing is scheduled across them.
+__device__ __forceinline__ void mfma_settle() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // 32-row MFMA blocks per streamed tile: two where the registers allow, which
 // halves the barriers and per-tile overhead per row.  One where the query
 // fragments take 128 VGPRs (fp32, 256 dims): the second accumulator and
@@ -450,7 +464,10 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     }
     __builtin_amdgcn_sched_barrier(0);
     // LATE: tile t + 1 has landed and every wavefront is done with cur
-    if constexpr (LATE) dma_barrier();
+    if constexpr (LATE) {
+      dma_barrier();
+      mfma_settle();
+    }
     if (wave_on) {
       // the bound changes only where it was read
       if (MODE != 2 && share && bound_tile(t))

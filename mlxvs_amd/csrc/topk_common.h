@@ -272,7 +272,8 @@ __device__ __forceinline__ float pick32(const float (&sc0)[16], const float (&sc
 
 // A lane's candidate buffer: B entries in LDS at stride S (entry e of the
 // lane at slot[S e]; the workgroup's S lanes side by side), each the
-// candidate's key (high word) and id.  Candidates that pass the lane's
+// candidate's score (high word, as selected: its key is made at the flush)
+// and id.  Candidates that pass the lane's
 // threshold are appended (about 45 instructions an iteration) instead of
 // being inserted into the sorted list (a T-slot insertion each); the buffer
 // is merged into the list when some lane of the wavefront has B entries, or
@@ -294,8 +295,9 @@ __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], fl
 #pragma unroll
   for (int e = 0; e < B; ++e) {
     if (__builtin_amdgcn_ballot_w64(e < cb.cnt) == 0) break;
-    const uint64_t v = e < cb.cnt ? cb.slot[S * e] : 0ull;
-    stream_insert<T>(K, I, (uint32_t)(v >> 32), (uint32_t)v);
+    const uint64_t v = cb.slot[S * e];
+    const float x = __uint_as_float((uint32_t)(v >> 32));
+    stream_insert<T>(K, I, e < cb.cnt ? key_nz(HALF ? 2.0f * x : x) : 0u, (uint32_t)v);
   }
   cb.cnt = 0;
   thr = fmaxf(thr, filter_of<HALF>(score_of_key(K[T - 1] + 1u)));
@@ -308,14 +310,8 @@ template <int T, bool HALF, int B, int S>
 __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                                 const float (&sc0)[16], const float (&sc1)[16],
                                                 int h, uint32_t id0, int lim, CandBuf<B, S>& cb) {
-  float mx0 = fmaxf(fmaxf(sc0[0], sc0[1]), sc0[2]), mx1 = fmaxf(fmaxf(sc1[0], sc1[1]), sc1[2]);
-#pragma unroll
-  for (int i = 3; i < 15; i += 2) {
-    mx0 = fmaxf(fmaxf(mx0, sc0[i]), sc0[i + 1]);
-    mx1 = fmaxf(fmaxf(mx1, sc1[i]), sc1[i + 1]);
-  }
-  const float mx = fmaxf(fmaxf(mx0, sc0[15]), fmaxf(mx1, sc1[15]));
-  if (__builtin_amdgcn_ballot_w64(!(mx < thr)) == 0) return false;
+  // (no max tree and vote first: some lane passes in almost every pair of
+  // blocks of a list of 16, so the mask is built anyway)
   // the failing positions: the sign of x - thr (x >= thr gives +0 or more),
   // shifted in one per funnel shift, position i ending at bit i.  thr must
   // be a number or -inf here (no NaN): -inf passes everything, and inf - inf
@@ -337,10 +333,10 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
     }
     if (pm) {
       const int i = __builtin_ctz(pm);
-      const float x = HALF ? 2.0f * pick32(sc0, sc1, i) : pick32(sc0, sc1, i);
+      const float x = pick32(sc0, sc1, i);
       const int j = i & 15;
       const int m = (i & 16 ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
-      cb.slot[S * cb.cnt] = ((uint64_t)key_nz(x) << 32) | (uint32_t)(id0 + m);
+      cb.slot[S * cb.cnt] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(id0 + m);
       ++cb.cnt;
       pm &= pm - 1u;
     }

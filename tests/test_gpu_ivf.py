@@ -210,3 +210,21 @@ def test_ivf_extend_and_save_load(tmp_path):
     assert np.array_equal(a, b) and loaded.metric == "l2"
     with pytest.raises(ValueError):
         index.extend(x[:5, :10])
+
+
+def test_lists_of_16_repeated_calls(oracle):
+    # k > 16 through lists of 16 with the rows of long lists cut into parts:
+    # items of fewer than 128 pairs leave wavefronts without queries, so the
+    # scanning wavefronts often reach the tile barrier last and read their
+    # accumulators right after it.  Read too soon after the last MFMA, the
+    # last accumulator registers held stale values now and then (a list lost
+    # a candidate); every call of several must be exact.
+    x = int_rows(6000, 16, 1)
+    q = int_rows(333, 16, 2)
+    c, data, ind, off = ivf_index(x, 64)
+    for k in (17, 24, 40, 64):
+        wi, wd = oracle.ivf_flat(c, data, ind, off, q, k, 12, "l2")
+        for rep in range(4):
+            ids, dist = mlxvs_amd.ivf_flat_search(c, data, ind, off, "l2", q, k, n_probes=12)
+            assert np.array_equal(ids, wi), (k, rep)
+            assert np.array_equal(dist, wd), (k, rep)
