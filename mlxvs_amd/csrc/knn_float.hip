@@ -722,28 +722,34 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
       const uint32_t* qrow = cQ + (qw + col) * kDeepChunkDwords;
       const uint32_t* arow = cA + (32 * rb0 + col) * kDeepChunkDwords;
       const int sw = (col & 7) ^ ((col >> 3) & 1);
+      // the fragments of vector step v + 1 are read before the MFMAs of
+      // step v (a scheduling barrier keeps them there), so each step's
+      // MFMAs find their operands read and the pipe does not drain while
+      // the LDS answers; only step 0 waits, right after the barrier
+      typedef typename std::conditional<F16, halfx8, floatx4>::type fragv;
+      fragv bq[2], av[2][NB];
+      auto fetch = [&](int v, int b) {
+        const int slot = F16 ? 4 * ((2 * v + h) ^ sw) : 4 * ((4 * h + v) ^ sw);
+        bq[b] = *(const fragv*)(qrow + slot);
+#pragma unroll
+        for (int r = 0; r < NB; ++r) av[b][r] = *(const fragv*)(arow + r * 32 * kDeepChunkDwords + slot);
+      };
+      fetch(0, 0);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
+        if (v + 1 < 4) fetch(v + 1, (v + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (F16) {
-          const int slot = 4 * ((2 * v + h) ^ sw);
-          const halfx8 bq = *(const halfx8*)(qrow + slot);
-#pragma unroll
-          for (int r = 0; r < NB; ++r) {
-            const halfx8 av = *(const halfx8*)(arow + r * 32 * kDeepChunkDwords + slot);
-            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq, acc[r], 0, 0, 0);
-          }
-        } else {
-          const int slot = 4 * ((4 * h + v) ^ sw);
-          const floatx4 bq = *(const floatx4*)(qrow + slot);
-          floatx4 av[NB];
 #pragma unroll
           for (int r = 0; r < NB; ++r)
-            av[r] = *(const floatx4*)(arow + r * 32 * kDeepChunkDwords + slot);
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[v & 1][r], bq[v & 1], acc[r], 0, 0, 0);
+        } else {
 #pragma unroll
           for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int r = 0; r < NB; ++r)
-              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[r][u], bq[u], acc[r], 0, 0, 0);
+              acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[v & 1][r][u], bq[v & 1][u], acc[r],
+                                                            0, 0, 0);
         }
       }
     }
