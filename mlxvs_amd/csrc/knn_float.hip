@@ -196,11 +196,12 @@ __device__ __forceinline__ void dma_barrier() {
 // wavefront that arrives last passes both at once): reading the last
 // accumulator registers first, at the count it derived, gave stale values
 // now and then (lists that lost a candidate, measured on the GPU: gone with
-// 8 more wait states, not with 1).  Sixteen that the compiler does not
-// count (inline), fenced so that nothing is scheduled across them.
+// 8 more wait states, not with 1).  Twenty-four, fenced so that nothing is
+// scheduled across them: more than the longest MFMA here needs (16 passes
+// + 2) whether or not the compiler counts them towards its own.
 __device__ __forceinline__ void mfma_settle() {
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_nop 7\n\ts_nop 7");
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
   __builtin_amdgcn_sched_barrier(0);
 }
 
