@@ -1080,11 +1080,19 @@ __global__ __launch_bounds__(256) void select_group_kernel(MergeGroupArgs a) {
 // first > 2: the blocks of first / 2 are already sorted, descending and
 // ascending in turn (what the network's earlier phases would leave), so the
 // sort starts at the merge of blocks of that size.
-template <int E>
+template <int E, int FIRST = 0>
 __device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, bool out_order,
                                              int first = 2) {
   auto ord = [&](uint64_t r) { return out_order ? output_order(r) : r; };
+  // FIRST > 0: the start and the length are known here (P = 64 E), so the
+  // network unrolls into straight-line code
+  if constexpr (FIRST > 0) {
+    first = FIRST;
+    P = 64 * E;
+  }
+#pragma unroll
   for (int size = first; size <= P; size <<= 1) {
+#pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       if (stride >= E) {
         const int lm = stride / E;  // partner lane distance
@@ -1129,6 +1137,18 @@ __device__ __forceinline__ int run_index(int i, int T, int sorted) {
 }
 __device__ __forceinline__ int run_start(int T, int sorted, int P) {
   return (runs_of(T, sorted) && 2 * T <= P) ? 2 * T : 2;
+}
+
+// wave_bitonic from run_start's first phase, unrolled for the starts that
+// sorted stream lists of 4, 8 or 16 give.
+template <int E>
+__device__ __forceinline__ void wave_sort_runs(uint64_t (&x)[E], int lane, int first) {
+  switch (first) {
+    case 8: wave_bitonic<E, 8>(x, lane, 64 * E, false); break;
+    case 16: wave_bitonic<E, 16>(x, lane, 64 * E, false); break;
+    case 32: wave_bitonic<E, 32>(x, lane, 64 * E, false); break;
+    default: wave_bitonic<E>(x, lane, 64 * E, false, first); break;
+  }
 }
 
 // The largest of the wavefront's values.
@@ -1216,7 +1236,7 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(MergeArgs a) {
     if (lane < a.k) emit(slot, best);
     return;
   }
-  wave_bitonic<E>(x, lane, P, false, run_start(a.T, a.sorted, P));
+  wave_sort_runs<E>(x, lane, run_start(a.T, a.sorted, P));
   // the k-th best rank (element k - 1), broadcast
   const int kl = (a.k - 1) / E, ke = (a.k - 1) % E;
   uint64_t mine = 0;
@@ -1279,7 +1299,7 @@ __global__ __launch_bounds__(256) void merge_group_wave_kernel(MergeGroupArgs a)
     m = wave_max_u64(m);
     if (lane == 0) a.sentinel[(int64_t)q * a.ngroups + g] = m;
   }
-  wave_bitonic<E>(x, lane, 64 * E, false, run_start(a.T, a.sorted, 64 * E));
+  wave_sort_runs<E>(x, lane, run_start(a.T, a.sorted, 64 * E));
   uint64_t* dst = a.out + ((int64_t)q * a.ngroups + g) * a.keep;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
