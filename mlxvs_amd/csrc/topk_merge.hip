@@ -681,37 +681,54 @@ template <typename Scorer>
 __global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
   constexpr int NT = 256;
   __shared__ RowSelect sm;
+  // the workgroup's queries are blockIdx.x + i gridDim.x; their flags are
+  // read NT at a time (a thread each, so the walk over the flags is not a
+  // chain of dependent loads) into a list of the flagged ones; without
+  // flags every query is redone
+  __shared__ int flagged[NT];
+  __shared__ int nflagged;
   const int tid = threadIdx.x;
   const int k = a.k;
-  for (int q = blockIdx.x; q < a.nq; q += gridDim.x) {
-    if (a.flags && !a.flags[q]) continue;  // uniform in the workgroup
-    const int64_t n = sc.begin(a, q);      // the query's rows
-    const int keff = select_rows(sc, 0, n, k, sm);
-    // distances (emit_topk's conventions)
-    const bool l2 = a.metric == kL2;
-    const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
-    for (int i = tid; i < k; i += NT) {
-      const uint64_t r = i < keff ? sm.buf[i] : 0ull;
-      const int64_t o = (int64_t)q * k + i;
-      if (r == 0) {
-        a.ids[o] = -1;
-        if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
-        continue;
-      }
-      a.ids[o] = id_of_rank(r);
-      const float sv = score_of_key((uint32_t)(r >> 32));
-      if (a.dists) {
-        if (a.dist_mode == 1) {
-          a.dists[o] = -sv;
-        } else if (l2) {
-          const float v = qn - sv;  // reference src/knn.cpp:126-129
-          a.dists[o] = v > 0.0f ? v : 0.0f;
-        } else {
-          a.dists[o] = sv;
+  for (int64_t i0 = 0; blockIdx.x + i0 * gridDim.x < a.nq; i0 += NT) {
+    if (tid == 0) nflagged = 0;
+    __syncthreads();
+    {
+      const int64_t q = blockIdx.x + (i0 + tid) * gridDim.x;
+      if (q < a.nq && (!a.flags || a.flags[q])) flagged[atomicAdd(&nflagged, 1)] = (int)q;
+    }
+    __syncthreads();
+    const int nf = nflagged;
+    for (int f = 0; f < nf; ++f) {
+      const int q = flagged[f];
+      const int64_t n = sc.begin(a, q);      // the query's rows
+      const int keff = select_rows(sc, 0, n, k, sm);
+      // distances (emit_topk's conventions)
+      const bool l2 = a.metric == kL2;
+      const float qn = (l2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
+      for (int i = tid; i < k; i += NT) {
+        const uint64_t r = i < keff ? sm.buf[i] : 0ull;
+        const int64_t o = (int64_t)q * k + i;
+        if (r == 0) {
+          a.ids[o] = -1;
+          if (a.dists) a.dists[o] = (a.dist_mode == 1 || l2) ? INFINITY : -INFINITY;
+          continue;
+        }
+        a.ids[o] = id_of_rank(r);
+        const float sv = score_of_key((uint32_t)(r >> 32));
+        if (a.dists) {
+          if (a.dist_mode == 1) {
+            a.dists[o] = -sv;
+          } else if (l2) {
+            const float v = qn - sv;  // reference src/knn.cpp:126-129
+            a.dists[o] = v > 0.0f ? v : 0.0f;
+          } else {
+            a.dists[o] = sv;
+          }
         }
       }
+      __syncthreads();  // sm is reused by the next query
     }
-    __syncthreads();  // sm is reused by the next query
+    __syncthreads();  // flagged and nflagged are rewritten for the next block
   }
 }
 
