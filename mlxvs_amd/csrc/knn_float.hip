@@ -1100,8 +1100,24 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, 
         const bool desc = ((lane * E) & size) == 0;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-          const uint32_t plo = __shfl_xor((uint32_t)x[e], lm);
-          const uint32_t phi = __shfl_xor((uint32_t)(x[e] >> 32), lm);
+          uint32_t plo, phi;
+          if (FIRST > 0 && lm == 1) {
+            // (unrolled: lm is a constant) partners within a quad or a row
+            // of 16: DPP moves (quad_perm 1, 0, 3, 2), no LDS round trip
+            plo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0xB1, 0xF, 0xF, true);
+            phi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x[e] >> 32), 0xB1, 0xF, 0xF, true);
+          } else if (FIRST > 0 && lm == 2) {
+            // quad_perm 2, 3, 0, 1
+            plo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0x4E, 0xF, 0xF, true);
+            phi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x[e] >> 32), 0x4E, 0xF, 0xF, true);
+          } else if (FIRST > 0 && lm == 8) {
+            // row_ror 8: lane i of a 16-lane row reads lane (i + 8) mod 16
+            plo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0x128, 0xF, 0xF, true);
+            phi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x[e] >> 32), 0x128, 0xF, 0xF, true);
+          } else {
+            plo = __shfl_xor((uint32_t)x[e], lm);
+            phi = __shfl_xor((uint32_t)(x[e] >> 32), lm);
+          }
           const uint64_t y = ((uint64_t)phi << 32) | plo;
           const bool keep_big = lo == desc;
           const bool xb = ord(x[e]) > ord(y);
