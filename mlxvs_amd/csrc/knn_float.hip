@@ -1110,6 +1110,13 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&x)[E], int lane, int P, 
             // quad_perm 2, 3, 0, 1
             plo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0x4E, 0xF, 0xF, true);
             phi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x[e] >> 32), 0x4E, 0xF, 0xF, true);
+          } else if (FIRST > 0 && lm == 4) {
+            // row_half_mirror (lane j reads j ^ 7 within 8), then quad_perm
+            // 3, 2, 1, 0 (j ^ 3): lane i reads i ^ 4
+            const int tlo = __builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0x141, 0xF, 0xF, true);
+            const int thi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(x[e] >> 32), 0x141, 0xF, 0xF, true);
+            plo = (uint32_t)__builtin_amdgcn_mov_dpp(tlo, 0x1B, 0xF, 0xF, true);
+            phi = (uint32_t)__builtin_amdgcn_mov_dpp(thi, 0x1B, 0xF, 0xF, true);
           } else if (FIRST > 0 && lm == 8) {
             // row_ror 8: lane i of a 16-lane row reads lane (i + 8) mod 16
             plo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x[e], 0x128, 0xF, 0xF, true);
