@@ -1715,38 +1715,42 @@ __global__ void gather_kernel(const float* in, const int* sel, int rows, int d,
 
 // Self graph: drop the row's own id and -1 entries from its k+1 list, keep
 // k, order by nearness with lowest id first among equal distances
-// (reference src/all_neighbors.cpp:56-95).  A workgroup takes R rows
-// (R max(kin, k) <= 4096): their lists are staged through LDS with coalesced loads
-// and stores, and one thread per row does the work there.  The input is
-// ordered by score and the distance is monotone in the score, so the
-// insertion sort only reorders runs of equal distance.  dists is required.
+// (reference src/all_neighbors.cpp:56-95).  A workgroup is one wavefront and
+// takes R rows (R max(kin, k) <= 4096, R <= 64): their lists are staged
+// through LDS with coalesced loads and stores, max(kin, k) slots a row, and
+// one lane per row does the work there, in place (the kept entries fill the
+// row's first slots, never past the input entry being read).  32 KB of LDS a workgroup, so
+// several run on a CU.  The input is ordered by score and the distance is
+// monotone in the score, so the insertion sort only reorders runs of equal
+// distance.  dists is required.
 constexpr int kSelfDropEntries = 4096;
-__global__ __launch_bounds__(256) void self_drop_kernel(SelfDropArgs a, int R) {
+constexpr int kSelfDropThreads = 64;
+__global__ __launch_bounds__(kSelfDropThreads) void self_drop_kernel(SelfDropArgs a, int R) {
   __shared__ int32_t si[kSelfDropEntries];
   __shared__ float sd[kSelfDropEntries];
-  __shared__ int32_t oi[kSelfDropEntries];
-  __shared__ float od[kSelfDropEntries];
   const int64_t r0 = (int64_t)blockIdx.x * R;
   const int rows = (int)min((int64_t)R, a.n - r0);
   const int kin = a.kin, k = a.k;
-  for (int e = threadIdx.x; e < rows * kin; e += 256) {
-    si[e] = a.ids_in[r0 * kin + e];
-    sd[e] = a.dists_in[r0 * kin + e];
+  const int W = max(kin, k);  // a row's slots: its input, then its output in place
+  // (unrolled, so that a lane has several loads in flight, not one)
+#pragma unroll 16
+  for (int e = threadIdx.x; e < rows * kin; e += kSelfDropThreads) {
+    const int row = e / kin;
+    si[e + row * (W - kin)] = a.ids_in[r0 * kin + e];
+    sd[e + row * (W - kin)] = a.dists_in[r0 * kin + e];
   }
   __syncthreads();
   const int t = threadIdx.x;
   if (t < rows) {
     const int64_t r = r0 + t;
-    const int32_t* iin = si + t * kin;
-    const float* din = sd + t * kin;
-    int32_t* io = oi + t * k;
-    float* dout = od + t * k;
+    int32_t* io = si + t * W;  // input at j, output at m <= j
+    float* dout = sd + t * W;
     const bool l2 = a.metric == kL2;
     int m = 0;
     for (int j = 0; j < kin && m < k; ++j) {
-      const int32_t id = iin[j];
+      const int32_t id = io[j];
       if (id < 0 || id == (int32_t)r) continue;
-      const float v = din[j];
+      const float v = dout[j];
       const float key = l2 ? v : -v;  // smaller is nearer
       int p = m;
       while (p > 0) {
@@ -1767,9 +1771,11 @@ __global__ __launch_bounds__(256) void self_drop_kernel(SelfDropArgs a, int R) {
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < rows * k; e += 256) {
-    a.ids[r0 * k + e] = oi[e];
-    a.dists[r0 * k + e] = od[e];
+#pragma unroll 16
+  for (int e = threadIdx.x; e < rows * k; e += kSelfDropThreads) {
+    const int row = e / k, i = e - row * k;
+    a.ids[r0 * k + e] = si[row * W + i];
+    a.dists[r0 * k + e] = sd[row * W + i];
   }
 }
 
@@ -2186,11 +2192,12 @@ hipError_t launch_gather_f32(const float* in, const int* sel, int rows, int d,
 hipError_t launch_self_drop(const SelfDropArgs& a, hipStream_t s) {
   if (a.n <= 0) return hipSuccess;
   // R rows of kin inputs and k outputs each fit the staging arrays
+  // (in place: the k kept entries of a row fill its first slots)
   const int w = std::max(a.kin, a.k);
   if (w > kSelfDropEntries) return hipErrorInvalidValue;
-  const int R = std::min(256, kSelfDropEntries / w);
-  hipLaunchKernelGGL(self_drop_kernel, dim3((unsigned)((a.n + R - 1) / R)), dim3(256), 0, s, a,
-                     R);
+  const int R = std::min(kSelfDropThreads, kSelfDropEntries / w);
+  hipLaunchKernelGGL(self_drop_kernel, dim3((unsigned)((a.n + R - 1) / R)),
+                     dim3(kSelfDropThreads), 0, s, a, R);
   return hipGetLastError();
 }
 
