@@ -62,34 +62,45 @@ __global__ __launch_bounds__(256) void row_norms_kernel(PrepArgs a) {
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * 256;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // VEC: the next slab's vectors are loaded into registers before the
+  // current slab is summed, so its memory latency overlaps that work
+  constexpr int EPV = F16 ? 8 : 4;  // elements per 16-byte vector
+  constexpr int VPR = 32 / EPV;     // vectors per row slab
+  float pv[VEC ? VPR : 1][EPV];
+  auto load_slab = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < VPR; ++j) {
+      const int e = tid + 256 * j;
+      const int r = e / VPR, c = (e % VPR) * EPV;
+      const int64_t row = row0 + r;
+      if (row < a.n && c0 + c < a.d) {
+        if constexpr (F16) {
+          const halfx8 h = *(const halfx8*)((const _Float16*)a.x + row * a.ld + c0 + c);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) pv[j][u] = (float)h[u];
+        } else {
+          const floatx4 f = *(const floatx4*)((const float*)a.x + row * a.ld + c0 + c);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) pv[j][u] = f[u];
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < EPV; ++u) pv[j][u] = 0.0f;
+      }
+    }
+  };
+  if constexpr (VEC) load_slab(0);
   for (int c0 = 0; c0 < a.d; c0 += 32) {
     if constexpr (VEC) {
-      constexpr int EPV = F16 ? 8 : 4;         // elements per 16-byte vector
-      constexpr int VPR = 32 / EPV;            // vectors per row slab
 #pragma unroll
       for (int j = 0; j < VPR; ++j) {
         const int e = tid + 256 * j;
         const int r = e / VPR, c = (e % VPR) * EPV;
-        const int64_t row = row0 + r;
-        float v[EPV];
-        if (row < a.n && c0 + c < a.d) {
-          if constexpr (F16) {
-            const halfx8 h = *(const halfx8*)((const _Float16*)a.x + row * a.ld + c0 + c);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = (float)h[u];
-          } else {
-            const floatx4 f = *(const floatx4*)((const float*)a.x + row * a.ld + c0 + c);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = f[u];
-          }
-        } else {
-#pragma unroll
-          for (int u = 0; u < EPV; ++u) v[u] = 0.0f;
-        }
 #pragma unroll
         for (int u = 0; u < EPV; u += 4)
-          *(floatx4*)&sh[r * SS + c + u] = floatx4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+          *(floatx4*)&sh[r * SS + c + u] = floatx4{pv[j][u], pv[j][u + 1], pv[j][u + 2], pv[j][u + 3]};
       }
+      if (c0 + 32 < a.d) load_slab(c0 + 32);
     } else {
       for (int e = tid; e < 256 * 32; e += 256) {
         const int r = e >> 5, j = e & 31;
