@@ -324,6 +324,65 @@ MLXVS_C_API int mlxvs_topk_merge_device(
     float* out_scores,
     void* stream);
 
+/*
+ * Host-array entries on a caller's stream.  The same as the entries without
+ * the suffix, except that the copies in, the kernels and the copies out are
+ * enqueued on stream (a hipStream_t; NULL: the null stream) and the call
+ * waits for that stream, not the device, before it returns with the results
+ * in the caller's buffers.  Extension: the reference's Python binding takes
+ * a stream for brute_force_knn and kmeans_predict (python/bindings.cpp:55,
+ * 125) and runs on it (src/utils.h:31-38 gpu_stream); hamming_knn takes one
+ * in the C++ entry (include/mlxvs/mlxvs.h:775-784).  f16 != 0: binary16
+ * rows, as mlxvs_brute_force_knn_f16.
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_on_stream(
+    const void* base,
+    int64_t n,
+    const void* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+MLXVS_C_API int mlxvs_hamming_knn_on_stream(
+    const uint8_t* rows,
+    int64_t n,
+    const uint8_t* queries,
+    int64_t nq,
+    int32_t bytes,
+    int32_t k,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+MLXVS_C_API int mlxvs_kmeans_predict_on_stream(
+    const void* x,
+    int64_t n,
+    const void* centroids,
+    int64_t c,
+    int32_t d,
+    int32_t f16,
+    int32_t m,
+    int32_t* labels,
+    void* stream);
+
+MLXVS_C_API int mlxvs_topk_merge_on_stream(
+    const float* scores,
+    int64_t nq,
+    int64_t t,
+    const int32_t* ids,
+    const float* best,
+    int32_t id_offset,
+    int32_t first,
+    int32_t k,
+    int32_t* out_ids,
+    float* out_scores,
+    void* stream);
+
 /**
  * Releases the workspace the library keeps on the current device between
  * calls (it is grown on demand and reused).  Safe to call at any time when

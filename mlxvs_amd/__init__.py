@@ -76,6 +76,11 @@ def _load():
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_topk_merge": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp],
         "mlxvs_topk_merge_device": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp, vp],
+        "mlxvs_brute_force_knn_on_stream": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp,
+                                            vp, vp],
+        "mlxvs_hamming_knn_on_stream": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
+        "mlxvs_kmeans_predict_on_stream": [vp, i64, vp, i64, i32, i32, i32, vp, vp],
+        "mlxvs_topk_merge_on_stream": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp, vp],
         "mlxvs_release_workspace": [],
         "mlxvs_profile": [ctypes.c_int],
         "mlxvs_profile_report": [ctypes.c_char_p, i64],
@@ -141,12 +146,26 @@ def _rows(x, name: str, op: str) -> np.ndarray:
     return a
 
 
-def _host_stream(stream, op: str, device_fn: str) -> None:
-    """Host-array calls run on the null stream; a caller's stream is refused
-    rather than ignored (the *_device entry points take one)."""
-    if stream not in (None, 0):
-        raise ValueError(f"[{op}] host arrays are copied on the null stream; use {device_fn} "
-                         "to run on a stream")
+def _host_stream(stream, op: str):
+    """The hipStream_t a host-array call runs on (None: the null stream).
+
+    Takes what the reference's ``stream=`` takes the place of here: a
+    hipStream_t handle as an int or ``ctypes.c_void_p``, or an object that
+    carries one (``.cuda_stream``, as torch.cuda.Stream, or ``.handle``).
+    The call enqueues its copies and kernels on that stream and waits for
+    it before returning (reference python/bindings.cpp:55, 125)."""
+    if stream is None:
+        return None
+    h = stream
+    for attr in ("cuda_stream", "handle"):
+        if hasattr(h, attr):
+            h = getattr(h, attr)
+            break
+    if isinstance(h, ctypes.c_void_p):
+        h = h.value or 0
+    if isinstance(h, bool) or not isinstance(h, int) or h < 0:
+        raise ValueError(f"[{op}] stream must be a hipStream_t handle (int), or None.")
+    return h or None
 
 
 def _ptr(a: np.ndarray):
@@ -163,12 +182,12 @@ def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stre
     ``(ids int32 [nq, k], distances float32 [nq, k])``, nearest first:
     squared L2 ascending, otherwise similarity descending; -1 / +-inf where
     fewer than k rows exist.  ``tile_rows`` is accepted for compatibility
-    (the result does not depend on it).  ``stream`` must be None or 0: the
-    host arrays go through the null stream (``brute_force_knn_device`` runs
-    on a given hipStream_t).
+    (the result does not depend on it).  ``stream``: a hipStream_t handle
+    (int, or an object with ``.cuda_stream``) the copies and kernels run on;
+    the call waits for that stream before returning.
     """
     op = "mlxvs::brute_force_knn"
-    _host_stream(stream, op, "brute_force_knn_device")
+    st = _host_stream(stream, op)
     b = _rows(base, "base", op)
     q = _rows(queries, "queries", op)
     if b.shape[1] != q.shape[1]:
@@ -176,7 +195,8 @@ def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stre
     m = _metric(metric)
     k = int(k)
     nq = q.shape[0]
-    if b.dtype == np.float16 and q.dtype == np.float16:
+    f16 = b.dtype == np.float16 and q.dtype == np.float16
+    if f16:
         b = np.ascontiguousarray(b)
         q = np.ascontiguousarray(q)
         fn = _L().mlxvs_brute_force_knn_f16
@@ -186,7 +206,13 @@ def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stre
         fn = _L().mlxvs_brute_force_knn
     ids = np.empty((nq, max(k, 0)), dtype=np.int32)
     dist = np.empty((nq, max(k, 0)), dtype=np.float32)
-    _check(fn(_ptr(b), b.shape[0], _ptr(q), nq, b.shape[1], k, int(m), _ptr(ids), _ptr(dist)))
+    if st is None:
+        _check(fn(_ptr(b), b.shape[0], _ptr(q), nq, b.shape[1], k, int(m), _ptr(ids),
+                  _ptr(dist)))
+    else:
+        _check(_L().mlxvs_brute_force_knn_on_stream(_ptr(b), b.shape[0], _ptr(q), nq,
+                                                    b.shape[1], int(f16), k, int(m), _ptr(ids),
+                                                    _ptr(dist), st))
     return ids, dist
 
 
@@ -197,10 +223,10 @@ def hamming_knn(rows, queries, k, *, stream=None):
     ``rows`` uint8 [n, bytes] (as numpy.packbits), ``queries`` uint8
     [nq, bytes], k <= 256.  Returns ``(ids int32, distances float32)``
     [nq, k], nearest first, lowest id first among equal distances.
-    ``stream`` must be None or 0 (``hamming_knn_device`` takes a stream).
+    ``stream``: as for brute_force_knn.
     """
     op = "mlxvs::hamming_knn"
-    _host_stream(stream, op, "hamming_knn_device")
+    st = _host_stream(stream, op)
     r = np.asarray(rows)
     q = np.asarray(queries)
     if r.ndim != 2 or r.dtype != np.uint8 or q.ndim != 2 or q.dtype != np.uint8:
@@ -213,8 +239,12 @@ def hamming_knn(rows, queries, k, *, stream=None):
     nq = q.shape[0]
     ids = np.empty((nq, max(k, 0)), dtype=np.int32)
     dist = np.empty((nq, max(k, 0)), dtype=np.float32)
-    _check(_L().mlxvs_hamming_knn(_ptr(r), r.shape[0], _ptr(q), nq, r.shape[1], k,
-                                  _ptr(ids), _ptr(dist)))
+    if st is None:
+        _check(_L().mlxvs_hamming_knn(_ptr(r), r.shape[0], _ptr(q), nq, r.shape[1], k,
+                                      _ptr(ids), _ptr(dist)))
+    else:
+        _check(_L().mlxvs_hamming_knn_on_stream(_ptr(r), r.shape[0], _ptr(q), nq, r.shape[1],
+                                                k, _ptr(ids), _ptr(dist), st))
     return ids, dist
 
 
@@ -255,10 +285,10 @@ def kmeans_predict(x, centroids, m=1, *, tile_rows=65536, stream=None):
     both are, else float32), ``1 <= m <= clusters`` (at most 256 here).
     Squared L2 with the lowest centroid index first among equal distances
     (the reference's argmin for m = 1).  Returns int32 ``[n, m]``.
-    ``stream`` must be None or 0 (host arrays, the null stream).
+    ``stream``: as for brute_force_knn.
     """
     op = "mlxvs::kmeans_predict"
-    _host_stream(stream, op, "brute_force_knn_device")
+    st = _host_stream(stream, op)
     xa = _rows(x, "x", op)
     ca = _rows(centroids, "centroids", op)
     if xa.shape[1] != ca.shape[1]:
@@ -271,8 +301,12 @@ def kmeans_predict(x, centroids, m=1, *, tile_rows=65536, stream=None):
         ca = np.ascontiguousarray(ca, dtype=np.float32)
         f16 = 0
     labels = np.empty((xa.shape[0], max(m, 0)), dtype=np.int32)
-    _check(_L().mlxvs_kmeans_predict(_ptr(xa), xa.shape[0], _ptr(ca), ca.shape[0], xa.shape[1],
-                                     f16, m, _ptr(labels)))
+    if st is None:
+        _check(_L().mlxvs_kmeans_predict(_ptr(xa), xa.shape[0], _ptr(ca), ca.shape[0],
+                                         xa.shape[1], f16, m, _ptr(labels)))
+    else:
+        _check(_L().mlxvs_kmeans_predict_on_stream(_ptr(xa), xa.shape[0], _ptr(ca), ca.shape[0],
+                                                   xa.shape[1], f16, m, _ptr(labels), st))
     return labels
 
 
@@ -286,13 +320,10 @@ def topk_merge(scores, ids, best, id_offset, first, k, *, stream=None):
     among equal scores the lowest ids are kept; -1 / -inf past
     ``min(k, t + (0 if first else k))`` entries.  Mirrors the C++ entry
     reference include/mlxvs/mlxvs.h:892-905 (src/knn.cpp:37-69), which the
-    reference does not bind to Python.  ``stream`` must be None (host arrays
-    go through the null stream; ``topk_merge_device`` takes a stream).
+    reference does not bind to Python.  ``stream``: as for brute_force_knn.
     """
     op = "mlxvs::topk_merge"
-    if stream is not None:
-        raise ValueError(f"[{op}] host arrays run on the null stream; use topk_merge_device "
-                         "for a stream")
+    st = _host_stream(stream, op)
     s = np.asarray(scores)
     if s.ndim != 2 or s.dtype != np.float32:
         raise ValueError(f"[{op}] scores must be float32 [nq, t]")
@@ -309,8 +340,12 @@ def topk_merge(scores, ids, best, id_offset, first, k, *, stream=None):
         ip, bp = _ptr(pi), _ptr(pb)
     out_ids = np.empty((nq, max(k, 0)), dtype=np.int32)
     out_s = np.empty((nq, max(k, 0)), dtype=np.float32)
-    _check(_L().mlxvs_topk_merge(_ptr(s), nq, t, ip, bp, int(id_offset), int(first), k,
-                                 _ptr(out_ids), _ptr(out_s)))
+    if st is None:
+        _check(_L().mlxvs_topk_merge(_ptr(s), nq, t, ip, bp, int(id_offset), int(first), k,
+                                     _ptr(out_ids), _ptr(out_s)))
+    else:
+        _check(_L().mlxvs_topk_merge_on_stream(_ptr(s), nq, t, ip, bp, int(id_offset),
+                                               int(first), k, _ptr(out_ids), _ptr(out_s), st))
     return out_ids, out_s
 
 

@@ -221,6 +221,59 @@ int mlxvs_topk_merge_device(const float* scores, int64_t nq, int64_t t, const in
   });
 }
 
+int mlxvs_brute_force_knn_on_stream(const void* base, int64_t n, const void* queries,
+                                    int64_t nq, int32_t d, int32_t f16, int32_t k,
+                                    mlxvs_metric metric, int32_t* ids, float* distances,
+                                    void* stream) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto b = host_rows(base, n, d, t);
+    auto q = host_rows(queries, nq, d, t);
+    auto r = mlxvs::brute_force_knn(b, q, k, to_metric(metric), {}, stream);
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_hamming_knn_on_stream(const uint8_t* rows, int64_t n, const uint8_t* queries,
+                                int64_t nq, int32_t bytes, int32_t k, int32_t* ids,
+                                float* distances, void* stream) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto b = host_rows(rows, n, bytes, mlxvs::Dtype::Uint8);
+    auto q = host_rows(queries, nq, bytes, mlxvs::Dtype::Uint8);
+    auto r = mlxvs::hamming_knn(b, q, k, stream);
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_kmeans_predict_on_stream(const void* x, int64_t n, const void* centroids, int64_t c,
+                                   int32_t d, int32_t f16, int32_t m, int32_t* labels,
+                                   void* stream) {
+  return guarded([&] {
+    require(labels != nullptr, "labels must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto xr = host_rows(x, n, d, t);
+    auto cr = host_rows(centroids, c, d, t);
+    auto r = mlxvs::kmeans_predict(xr, cr, m, 65536, stream);
+    if (!r.empty()) std::memcpy(labels, r.data(), r.size() * sizeof(int32_t));
+  });
+}
+
+int mlxvs_topk_merge_on_stream(const float* scores, int64_t nq, int64_t t, const int32_t* ids,
+                               const float* best, int32_t id_offset, int32_t first, int32_t k,
+                               int32_t* out_ids, float* out_scores, void* stream) {
+  return guarded([&] {
+    require(nq >= 0 && t >= 0 && t < (1LL << 31), "scores must be float32 [nq, t]");
+    require(out_ids != nullptr || nq == 0, "out_ids must not be NULL.");
+    auto r = mlxvs::topk_merge(mlxvs::Rows{scores, nq, (int32_t)t, mlxvs::Dtype::Float32}, ids,
+                               best, id_offset, first != 0, k, stream);
+    if (!r.first.empty()) std::memcpy(out_ids, r.first.data(), r.first.size() * sizeof(int32_t));
+    if (out_scores && !r.second.empty())
+      std::memcpy(out_scores, r.second.data(), r.second.size() * sizeof(float));
+  });
+}
+
 int mlxvs_profile(int enable) {
   return guarded([&] { mlxvs::profile(enable != 0); });
 }

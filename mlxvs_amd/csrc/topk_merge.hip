@@ -318,7 +318,11 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(TopkMergeArgs a) {
       for (int i = 0; i < NW; ++i) lc = min(lc, wbound[i]);
       L = max(L, lc);
     }
+    // every thread reads the count before any wavefront appends to it (the
+    // decisions below contain barriers, so they must be the same in every
+    // wavefront)
     const int cnt = s_cnt;
+    __syncthreads();
     if (cnt > kCandCap) return false;
     if (cnt > kCandCap / 2) compact(cnt, (int)(seen < k ? seen : k));
     seen += valid;
@@ -581,12 +585,16 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
     }
 #pragma unroll
     for (int e = 0; e < PER; ++e) mx = max(mx, key[e]);
+    // the count after the previous chunk's appends (they ended at that
+    // chunk's last barrier), read before the barrier below, after which
+    // wavefronts append: every wavefront takes the same decisions on it
+    // (they contain barriers)
+    const int cnt0 = sm.cnt;
     // the chunk's bound (see topk_merge_kernel)
     const int j = (k + NW - 1) / NW;
     const uint32_t lw = __shfl(wave_sort_desc(mx, lane), j - 1);
     if (lane == 0) sm.wbound[w] = lw;
     __syncthreads();
-    const int cnt0 = sm.cnt;
     if (cnt0 > kCandCap) {
       overflow = true;
       break;

@@ -101,11 +101,15 @@ def test_python_argument_errors(engine):
         engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 0)
     with pytest.raises(ValueError, match="1 <= k <= 255"):
         engine.all_neighbors(np.zeros((4, 3), np.float32), 300)
-    # a stream given to a host-array call is refused, not ignored
-    with pytest.raises(ValueError, match="brute_force_knn_device"):
-        engine.brute_force_knn(np.zeros((4, 3)), np.zeros((2, 3)), 1, stream=12345)
-    with pytest.raises(ValueError, match="hamming_knn_device"):
-        engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 1, stream=7)
+    # a stream must be a hipStream_t handle (checked before any GPU work)
+    with pytest.raises(ValueError, match="hipStream_t handle"):
+        engine.brute_force_knn(np.zeros((4, 3)), np.zeros((2, 3)), 1, stream="s")
+    with pytest.raises(ValueError, match="hipStream_t handle"):
+        engine.hamming_knn(np.zeros((4, 3), np.uint8), np.zeros((2, 3), np.uint8), 1, stream=-7)
+    with pytest.raises(ValueError, match="hipStream_t handle"):
+        engine.kmeans_predict(np.zeros((4, 3)), np.zeros((2, 3)), 1, stream=1.5)
+    with pytest.raises(ValueError, match="hipStream_t handle"):
+        engine.topk_merge(np.zeros((2, 3), np.float32), None, None, 0, True, 1, stream=[1])
     # topk_merge: the reference's checks and messages (src/knn.cpp:46-54)
     with pytest.raises(ValueError, match=r"scores must be float32 \[nq, t\]"):
         engine.topk_merge(np.zeros((2, 3), np.float64), None, None, 0, True, 1)

@@ -166,3 +166,49 @@ def test_ground_truth_files(tmp_path, oracle):
     back = formats.read_ivecs(tmp_path / "gt.ivecs")
     want, _ = oracle.knn(base, q, 20, "l2")
     assert np.array_equal(back, ids) and np.array_equal(back, want)
+
+
+def test_host_entries_on_a_created_stream(engine, oracle):
+    # reference python/bindings.cpp:55, 125: the host-array entries take a
+    # stream; the copies and kernels run on it and the call waits for it.
+    # The answers are the ones of the null stream, bit for bit.
+    from mlxvs_amd import _hip
+
+    st = _hip.Stream()
+    rng = np.random.default_rng(77)
+    base = rng.integers(0, 9, (40_000, 48)).astype(np.float32)
+    q = rng.integers(0, 9, (300, 48)).astype(np.float32)
+    for s in (st, st.handle, st.handle.value):
+        for metric in ("l2", "inner_product", "cosine"):
+            a = engine.brute_force_knn(base, q, 20, metric)
+            b = engine.brute_force_knn(base, q, 20, metric, stream=s)
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    oid, odist = oracle.knn(base, q, 20, "l2")
+    ids, dist = engine.brute_force_knn(base, q, 20, "l2", stream=st)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    # float16 rows
+    bh, qh = base.astype(np.float16), q.astype(np.float16)
+    a = engine.brute_force_knn(bh, qh, 70, "l2")
+    b = engine.brute_force_knn(bh, qh, 70, "l2", stream=st)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    # Hamming (the MFMA route and the few-query scan)
+    codes = rng.integers(0, 256, (30_000, 64), dtype=np.uint8)
+    for nq in (3, 200):
+        qc = codes[:nq] ^ rng.integers(0, 2, (nq, 64), dtype=np.uint8)
+        a = engine.hamming_knn(codes, qc, 100)
+        b = engine.hamming_knn(codes, qc, 100, stream=st)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+        oi, od = oracle.hamming(codes, qc, 100)
+        assert np.array_equal(b[0], oi) and np.array_equal(b[1], od)
+    # kmeans_predict
+    cen = base[:500]
+    assert np.array_equal(engine.kmeans_predict(base, cen, 3),
+                          engine.kmeans_predict(base, cen, 3, stream=st))
+    # topk_merge, first and with running lists
+    S = rng.standard_normal((64, 20_000), dtype=np.float32)
+    a = engine.topk_merge(S, None, None, 5, True, 40)
+    b = engine.topk_merge(S, None, None, 5, True, 40, stream=st)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    a2 = engine.topk_merge(S, a[0], a[1], 100, False, 40)
+    b2 = engine.topk_merge(S, b[0], b[1], 100, False, 40, stream=st.handle.value)
+    assert np.array_equal(a2[0], b2[0]) and np.array_equal(a2[1], b2[1])

@@ -144,3 +144,42 @@ def test_device_in_place_on_a_stream(engine, oracle):
     _hip.synchronize()
     oi2, _ = oracle.topk_merge(S, None, None, 0, True, k)
     assert np.array_equal(out.download((nq, k), np.int32), oi2)
+
+
+# Rows whose candidate count crosses half of the kernel's 4,096-rank buffer
+# (and the whole of it) while a chunk is being appended: every wavefront
+# must take the same compaction / overflow decision on that count (a
+# wavefront that read it after another had appended took the other branch,
+# whose barriers the rest skipped).  Ascending rows put every element of a
+# chunk above the bound; the stepped rows put about 2,500 per chunk there;
+# the sawtooth mixes both.
+def patterned(nq, t, kind, seed):
+    g = np.random.default_rng(seed)
+    c = np.arange(t, dtype=np.float64)
+    if kind == "ascending":
+        s = np.broadcast_to(c, (nq, t)) + g.integers(0, 3, (nq, t))
+    elif kind == "stepped":
+        # per chunk of 8,192: 2,500 elements above everything before
+        blk = (c // 8192)
+        hi = (c % 8192) < 2500
+        s = np.broadcast_to(np.where(hi, 1000.0 * blk + (c % 8192) % 97, -1e6 + c % 13),
+                            (nq, t)) + g.integers(0, 2, (nq, t))
+    else:  # sawtooth
+        s = np.broadcast_to((c % 6000) + (c // 6000) * 10.0, (nq, t)) + g.integers(0, 2, (nq, t))
+    return np.ascontiguousarray(s, dtype=np.float32)
+
+
+@pytest.mark.parametrize("kind", ["ascending", "stepped", "sawtooth"])
+@pytest.mark.parametrize("t,k", [(4 * 8192 + 77, 256), (12 * 8192, 256), (5 * 4096, 100),
+                                 (3000, 256)])
+def test_count_crossing_within_a_chunk(engine, oracle, kind, t, k):
+    check(engine, oracle, patterned(24, t, kind, t + k), k)
+
+
+@pytest.mark.parametrize("kind", ["ascending", "stepped"])
+def test_count_crossing_with_running_lists(engine, oracle, kind):
+    nq, t, k = 16, 6 * 8192, 256
+    g = np.random.default_rng(3)
+    pb = g.integers(0, 60_000, (nq, k)).astype(np.float32)
+    pi = g.integers(0, 100_000, (nq, k)).astype(np.int32)
+    check(engine, oracle, patterned(nq, t, kind, 5), k, 11, (pi, pb))
