@@ -89,6 +89,46 @@ MLXVS_API void brute_force_knn_device_noalloc(const Rows& base, const Rows& quer
                                               Metric metric, int32_t* ids, float* distances,
                                               void* stream = nullptr);
 
+/** The rows a prefiltered search may return (cuVS's filters; reference
+ * python/mlxvs/cuvs/neighbors/filters.py:39-50). */
+enum class FilterKind {
+  /** Every row. */
+  None = 0,
+  /** One bit per base row: bit i % 32 of words[i / 32] set when row i may be
+   * returned; ceil(n / 32) words. */
+  Bitset = 1,
+  /** One bit per (query, row), row-major over nq * n bits and not padded per
+   * query: bit q n + i of the words set when row i may be returned for
+   * query q; ceil(nq n / 32) words. */
+  Bitmap = 2,
+};
+
+/** A prefilter: its kind and its words (host or device memory, as the
+ * entry's other inputs). */
+struct Prefilter {
+  FilterKind kind = FilterKind::None;
+  const uint32_t* words = nullptr;
+};
+
+/**
+ * brute_force_knn over the rows a prefilter allows: each query's k nearest
+ * allowed rows, ids numbering all rows, -1 / +-inf past the allowed rows
+ * there are.  The filter is applied inside the fused select, so rows it
+ * leaves out never enter a candidate list.  No C++ counterpart in the
+ * reference: its prefiltered search is the Python-level
+ * cuvs.neighbors.brute_force.search (python/mlxvs/cuvs/neighbors/
+ * brute_force.py:97-136), which masks a score matrix before selecting.
+ */
+MLXVS_API Neighbors brute_force_knn_filtered(const Rows& base, const Rows& queries, int k,
+                                             Metric metric, const Prefilter& filter,
+                                             void* stream = nullptr);
+/** brute_force_knn_filtered on device views and device filter words;
+ * returns once the work is enqueued. */
+MLXVS_API void brute_force_knn_filtered_device(const Rows& base, const Rows& queries, int k,
+                                               Metric metric, const Prefilter& filter,
+                                               int32_t* ids, float* distances,
+                                               void* stream = nullptr);
+
 /**
  * Exact Hamming k-NN of bit-packed uint8 rows [n, bytes] for bit-packed
  * queries [nq, bytes]; 1 <= k <= 256.  Replaces reference

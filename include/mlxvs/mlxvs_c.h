@@ -383,6 +383,66 @@ MLXVS_C_API int mlxvs_topk_merge_on_stream(
     float* out_scores,
     void* stream);
 
+/** Prefilter kinds (cuVS's filters; reference
+ * python/mlxvs/cuvs/neighbors/filters.py:39-50). */
+enum {
+  /** every row (the filter words are not read) */
+  MLXVS_FILTER_NONE = 0,
+  /** one bit per base row: bit i % 32 of word i / 32 set when row i may be
+   * returned; ceil(n / 32) words */
+  MLXVS_FILTER_BITSET = 1,
+  /** one bit per (query, row), row-major over nq * n bits and not padded
+   * per query: bit q n + i set when row i may be returned for query q;
+   * ceil(nq n / 32) words */
+  MLXVS_FILTER_BITMAP = 2
+};
+
+/**
+ * Extension: exact k-NN over the rows a prefilter allows.  As
+ * mlxvs_brute_force_knn_on_stream (host arrays, enqueued on stream, waits
+ * for that stream), with filter_kind one of MLXVS_FILTER_* and filter its
+ * host words: each query's k nearest allowed rows, ids numbering all rows,
+ * -1 / +inf (L2) or -inf (similarities) past the allowed rows there are.
+ * Rows the filter leaves out never enter the fused select's lists.  No C
+ * counterpart in the reference, whose prefiltered search is the
+ * Python-level cuvs.neighbors.brute_force.search (python/mlxvs/cuvs/
+ * neighbors/brute_force.py:97-136: scores of excluded rows set to the
+ * worst value before the selection, such picks returned as -1).
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_filtered(
+    const void* base,
+    int64_t n,
+    const void* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    const uint32_t* filter,
+    int32_t filter_kind,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/**
+ * mlxvs_brute_force_knn_filtered on device memory (inputs, filter words
+ * and outputs); returns once the work is enqueued on stream.
+ */
+MLXVS_C_API int mlxvs_brute_force_knn_filtered_device(
+    const void* base,
+    int64_t n,
+    const void* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t f16,
+    int32_t k,
+    mlxvs_metric metric,
+    const uint32_t* filter,
+    int32_t filter_kind,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
 /**
  * Releases the workspace the library keeps on the current device between
  * calls (it is grown on demand and reused).  Safe to call at any time when

@@ -30,6 +30,7 @@ __all__ = [
     "NearestNeighbors",
     "all_neighbors",
     "brute_force_knn",
+    "brute_force_knn_filtered",
     "hamming_knn",
     "ivf_flat_build",
     "ivf_flat_extend",
@@ -72,6 +73,10 @@ def _load():
         "mlxvs_brute_force_knn_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_brute_force_knn_device_noalloc": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int,
                                                  vp, vp, vp],
+        "mlxvs_brute_force_knn_filtered": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int, vp, i32,
+                                           vp, vp, vp],
+        "mlxvs_brute_force_knn_filtered_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int,
+                                                  vp, i32, vp, vp, vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_topk_merge": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp],
@@ -213,6 +218,72 @@ def brute_force_knn(base, queries, k, metric=Metric.l2, *, tile_rows=65536, stre
         _check(_L().mlxvs_brute_force_knn_on_stream(_ptr(b), b.shape[0], _ptr(q), nq,
                                                     b.shape[1], int(f16), k, int(m), _ptr(ids),
                                                     _ptr(dist), st))
+    return ids, dist
+
+
+# prefilter kinds (include/mlxvs/mlxvs_c.h MLXVS_FILTER_*)
+FILTER_NONE, FILTER_BITSET, FILTER_BITMAP = 0, 1, 2
+
+
+def _filter_words(mask, count: int, op: str) -> np.ndarray:
+    """Filter words: a bool mask packed little-endian into uint32 words (as
+    cuVS's filters pack it, reference python/mlxvs/cuvs/neighbors/
+    filters.py:31-37), or uint32 words as they are; at least ceil(count / 32)
+    of them."""
+    a = np.asarray(mask)
+    if a.dtype == np.bool_:
+        b = np.packbits(a.ravel(), bitorder="little")
+        a = np.pad(b, (0, -len(b) % 4)).view(np.uint32)
+    elif a.dtype != np.uint32:
+        raise ValueError(f"[{op}] a filter is a bool mask or uint32 words, not {a.dtype}.")
+    a = np.ascontiguousarray(a.ravel())
+    if len(a) < (count + 31) // 32:
+        raise ValueError(f"[{op}] the filter has {len(a)} words; {(count + 31) // 32} needed.")
+    return a
+
+
+def brute_force_knn_filtered(base, queries, k, metric=Metric.l2, *, bitset=None, bitmap=None,
+                             stream=None):
+    """brute_force_knn over the rows a prefilter allows (an extension: the
+    reference filters only in cuvs.neighbors.brute_force.search,
+    python/mlxvs/cuvs/neighbors/brute_force.py:97-136).
+
+    ``bitset``: the rows any query may return, a bool [n] mask or uint32
+    words (bit i % 32 of word i / 32).  ``bitmap``: per query, a bool
+    [nq, n] mask or uint32 words of nq * n bits, row-major, not padded per
+    query.  At most one of them.  Returns ``(ids int32 [nq, k], distances
+    float32 [nq, k])`` as brute_force_knn, ids numbering all rows; -1 / +-inf
+    past the allowed rows there are.  The filter is applied inside the fused
+    select.  ``stream``: as for brute_force_knn.
+    """
+    op = "mlxvs::brute_force_knn_filtered"
+    st = _host_stream(stream, op)
+    b = _rows(base, "base", op)
+    q = _rows(queries, "queries", op)
+    if b.shape[1] != q.shape[1]:
+        raise ValueError(f"[{op}] base and queries must have the same number of columns.")
+    if bitset is not None and bitmap is not None:
+        raise ValueError(f"[{op}] give a bitset or a bitmap, not both.")
+    m = _metric(metric)
+    k = int(k)
+    n, nq = b.shape[0], q.shape[0]
+    kind, words = FILTER_NONE, None
+    if bitset is not None:
+        kind, words = FILTER_BITSET, _filter_words(bitset, n, op)
+    elif bitmap is not None:
+        bm = np.asarray(bitmap)
+        if bm.dtype == np.bool_ and bm.shape != (nq, n):
+            raise ValueError(f"[{op}] a bool bitmap is [nq, n] = [{nq}, {n}].")
+        kind, words = FILTER_BITMAP, _filter_words(bm, nq * n, op)
+    f16 = b.dtype == np.float16 and q.dtype == np.float16
+    dt = np.float16 if f16 else np.float32
+    b = np.ascontiguousarray(b, dtype=dt)
+    q = np.ascontiguousarray(q, dtype=dt)
+    ids = np.empty((nq, max(k, 0)), dtype=np.int32)
+    dist = np.empty((nq, max(k, 0)), dtype=np.float32)
+    _check(_L().mlxvs_brute_force_knn_filtered(
+        _ptr(b), n, _ptr(q), nq, b.shape[1], int(f16), k, int(m),
+        None if words is None else _ptr(words), kind, _ptr(ids), _ptr(dist), st))
     return ids, dist
 
 
@@ -363,6 +434,15 @@ def brute_force_knn_device(base_ptr, n, queries_ptr, nq, d, k, metric, ids_ptr,
     _check(_L().mlxvs_brute_force_knn_device(
         base_ptr, n, queries_ptr, nq, d, int(bool(f16)), int(k), int(_metric(metric)),
         ids_ptr, dist_ptr, stream))
+
+
+def brute_force_knn_filtered_device(base_ptr, n, queries_ptr, nq, d, k, metric, filter_ptr,
+                                    filter_kind, ids_ptr, dist_ptr, *, f16=False, stream=None):
+    """mlxvs_brute_force_knn_filtered_device on device pointers (ints):
+    enqueued on ``stream`` (a hipStream_t handle), returns at once."""
+    _check(_L().mlxvs_brute_force_knn_filtered_device(
+        base_ptr, n, queries_ptr, nq, d, int(bool(f16)), int(k), int(_metric(metric)), filter_ptr,
+        int(filter_kind), ids_ptr, dist_ptr, stream))
 
 
 def hamming_knn_device(rows_ptr, n, queries_ptr, nq, nbytes, k, ids_ptr, dist_ptr, *,

@@ -163,6 +163,37 @@ int mlxvs_brute_force_knn_device(const void* base, int64_t n, const void* querie
   });
 }
 
+int mlxvs_brute_force_knn_filtered(const void* base, int64_t n, const void* queries, int64_t nq,
+                                   int32_t d, int32_t f16, int32_t k, mlxvs_metric metric,
+                                   const uint32_t* filter, int32_t filter_kind, int32_t* ids,
+                                   float* distances, void* stream) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto b = host_rows(base, n, d, t);
+    auto q = host_rows(queries, nq, d, t);
+    const mlxvs::Prefilter pf{(mlxvs::FilterKind)filter_kind, filter};
+    auto r = mlxvs::brute_force_knn_filtered(b, q, k, to_metric(metric), pf, stream);
+    copy_out(r, ids, distances);
+  });
+}
+
+int mlxvs_brute_force_knn_filtered_device(const void* base, int64_t n, const void* queries,
+                                          int64_t nq, int32_t d, int32_t f16, int32_t k,
+                                          mlxvs_metric metric, const uint32_t* filter,
+                                          int32_t filter_kind, int32_t* ids, float* distances,
+                                          void* stream) {
+  return guarded([&] {
+    require(ids != nullptr || nq == 0, "ids must not be NULL.");
+    const auto t = f16 ? mlxvs::Dtype::Float16 : mlxvs::Dtype::Float32;
+    auto b = host_rows(base, n, d, t);
+    auto q = host_rows(queries, nq, d, t);
+    const mlxvs::Prefilter pf{(mlxvs::FilterKind)filter_kind, filter};
+    mlxvs::brute_force_knn_filtered_device(b, q, k, to_metric(metric), pf, ids, distances,
+                                           stream);
+  });
+}
+
 int mlxvs_brute_force_knn_device_noalloc(const void* base, int64_t n, const void* queries,
                                          int64_t nq, int32_t d, int32_t f16, int32_t k,
                                          mlxvs_metric metric, int32_t* ids, float* distances,

@@ -392,6 +392,10 @@ struct FloatInputs {
   int64_t nq;
   int d;
   bool f16;
+  // prefilter words on the device (null: every row) and their kind:
+  // 1 bitset [ceil(n / 32)], 2 bitmap [ceil(nq n / 32)] (Prefilter)
+  const uint32_t* allow = nullptr;
+  int allow_kind = 0;
 };
 
 // Exhaustive exact k-NN for the queries listed in qsel (device ints), on
@@ -399,7 +403,8 @@ struct FloatInputs {
 void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
                       const float* queries, int ld, const float* bnorm,
                       const float* qnorm, int64_t n, int d, int metric,
-                      const int* qsel_dev, int rows, int k, int32_t* ids, float* dists) {
+                      const int* qsel_dev, int rows, int k, int32_t* ids, float* dists,
+                      const uint32_t* allow = nullptr, int64_t allow_stride = 0) {
   if (rows <= 0) return;
   const int64_t per_block = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t(1) << 28) / std::max<int64_t>(n, 1)));
   float* S = ar.take<float>((size_t)per_block * (size_t)std::max<int64_t>(n, 1));
@@ -407,7 +412,8 @@ void exhaustive_float(Arena& ar, hipStream_t s, const float* base,
     const int cnt = (int)std::min<int64_t>(per_block, rows - r0);
     kern::ScoresArgs sa{base, queries, qsel_dev + r0, bnorm, n, cnt, d, ld, metric, S};
     launch(s, "scores", [&] { return kern::launch_scores(sa, s); });
-    kern::SelectArgs se{S, n, cnt, k, qsel_dev + r0, metric, qnorm, 0, ids, dists};
+    kern::SelectArgs se{S, n, cnt, k, qsel_dev + r0, metric, qnorm, 0, ids, dists, allow,
+                        allow_stride};
     launch(s, "select", [&] { return kern::launch_select(se, s); });
   }
 }
@@ -519,6 +525,16 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     });
     return;
   }
+  // Prefilter: a bitset is read as it is (every query the same words); a
+  // bitmap, row-major over nq * n bits, becomes word-aligned rows per query
+  const uint32_t* allow = in.allow_kind ? in.allow : nullptr;
+  int64_t allow_stride = 0;
+  if (allow && in.allow_kind == 2) {
+    allow_stride = (n + 31) / 32;
+    uint32_t* rows_w = ar.take<uint32_t>((size_t)(nq * allow_stride));
+    launch(s, "prep", [&] { return kern::launch_filter_rows(in.allow, nq, n, rows_w, s); });
+    allow = rows_w;
+  }
   // Operand preparation.  Cosine: unit rows in fp32 (the reference
   // normalises in float32, src/knn.cpp:30-33, also for float16 input,
   // src/utils.h:28).  Otherwise the rows are used in place when they are
@@ -582,8 +598,9 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   const bool use_deep = deep && kern::deep_supported(kld, T, kf16);
-  // at most 32 queries (fp32): rows streamed straight into registers
-  const bool use_stream = !kf16 && !deep && kern::stream_supported(kld, T, nq);
+  // at most 32 queries (fp32): rows streamed straight into registers (not
+  // with a prefilter, which the fused and deep kernels apply)
+  const bool use_stream = !kf16 && !deep && !allow && kern::stream_supported(kld, T, nq);
   // deep rows, at most 32 queries: the deep kernel's wavefronts split the
   // row blocks of a tile instead of the queries
   const bool deep_rs = use_deep && nq <= 32;
@@ -632,7 +649,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     int* qsel = ar.take<int>((size_t)nq);
     launch(s, "prep", [&] { return kern::launch_iota(qsel, nq, s); });
     exhaustive_float(ar, s, eb, eq, kld, bnorm, qnorm, n, d, metric, qsel, (int)nq, k, ids,
-                     dists);
+                     dists, allow, allow_stride);
     return;
   }
 
@@ -647,6 +664,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, bp.m, bp.pubj,
                      (int)qblocks, plan.xcd ? (use_deep ? 2 : 1) : 0};
+  fa.allow = allow;
+  fa.allow_stride = allow_stride;
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, kf16, deep_rs, s); });
   else if (use_stream)
@@ -669,6 +688,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   }
   kern::RedoArgs ra{kbase, kq, l2 ? bnorm : nullptr, qnorm, flags, n, (int)nq, kld, kld,
                     kf16 ? 1 : 0, 0, metric, 0, k, ids, dists};
+  ra.allow = allow;
+  ra.allow_stride = allow_stride;
   launch(s, "redo", [&] { return kern::launch_redo(ra, s); });
 }
 
@@ -1248,6 +1269,61 @@ void brute_force_knn_device(const Rows& base, const Rows& queries, int k, Metric
   float_knn(ss, {base.data, queries.data, base.n, queries.n, base.d,
                  base.dtype == Dtype::Float16},
             k, (int)metric, ids, dists);
+}
+
+namespace {
+// Words of a prefilter: ceil(n / 32) for a bitset, ceil(nq n / 32) for a
+// bitmap (0 when there is nothing to filter).
+int64_t filter_words(const Prefilter& f, int64_t n, int64_t nq, const char* op) {
+  const int kind = (int)f.kind;
+  if (kind < 0 || kind > 2) invalid(op, "unknown prefilter kind.");
+  const int64_t w = kind == 1 ? (n + 31) / 32 : kind == 2 ? (n * nq + 31) / 32 : 0;
+  if (w > 0 && f.words == nullptr) invalid(op, "the prefilter's words must not be NULL.");
+  return w;
+}
+}  // namespace
+
+Neighbors brute_force_knn_filtered(const Rows& base, const Rows& queries, int k, Metric metric,
+                                   const Prefilter& filter, void* stream) {
+  const char* op = "mlxvs::brute_force_knn_filtered";
+  float_args(base, queries, k, metric, op);
+  const int64_t nw = filter_words(filter, base.n, queries.n, op);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int64_t nq = queries.n;
+  const void* db = upload(ar, s, base);
+  const void* dq = upload(ar, s, queries);
+  uint32_t* dw = nullptr;
+  if (nw > 0) {
+    dw = ar.take<uint32_t>((size_t)nw);
+    check_hip(hipMemcpyAsync(dw, filter.words, sizeof(uint32_t) * nw, hipMemcpyHostToDevice, s),
+              "hipMemcpyAsync (prefilter)");
+  }
+  int32_t* ids = ar.take<int32_t>((size_t)std::max<int64_t>(1, nq * k));
+  float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
+  FloatInputs in{db, dq, base.n, nq, base.d, base.dtype == Dtype::Float16};
+  in.allow = dw;
+  in.allow_kind = nw > 0 ? (int)filter.kind : 0;
+  float_knn(ss, in, k, (int)metric, ids, dists);
+  return download(ss, ids, dists, nq, k);
+}
+
+void brute_force_knn_filtered_device(const Rows& base, const Rows& queries, int k,
+                                     Metric metric, const Prefilter& filter, int32_t* ids,
+                                     float* distances, void* stream) {
+  const char* op = "mlxvs::brute_force_knn_filtered";
+  float_args(base, queries, k, metric, op);
+  if (ids == nullptr && queries.n * k > 0) invalid(op, "ids must not be NULL.");
+  const int64_t nw = filter_words(filter, base.n, queries.n, op);
+  Session ss((hipStream_t)stream);
+  float* dists = distances;
+  if (dists == nullptr) dists = ss.arena().take<float>((size_t)std::max<int64_t>(1, queries.n * k));
+  FloatInputs in{base.data, queries.data, base.n, queries.n, base.d,
+                 base.dtype == Dtype::Float16};
+  in.allow = filter.words;
+  in.allow_kind = nw > 0 ? (int)filter.kind : 0;
+  float_knn(ss, in, k, (int)metric, ids, dists);
 }
 
 void brute_force_knn_device_noalloc(const Rows& base, const Rows& queries, int k,

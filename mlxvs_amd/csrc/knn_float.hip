@@ -396,6 +396,11 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const bool share = a.mslots > 0;
   uint32_t* gk = a.gkey + (int64_t)(qvalid ? q : 0) * S;
   const int myslot = share ? (2 * seg + h) % a.mslots : 0;
+  // Prefilter (dense only): the lane's query's filter words; word j covers
+  // global rows 32 j .. 32 j + 31 (the split's first row is a multiple of 32)
+  const bool filt = MODE == 0 && a.allow != nullptr;
+  const uint32_t* fw = filt ? a.allow + (int64_t)(qvalid ? q : 0) * a.allow_stride : nullptr;
+  const int64_t r1g = r0 + nrows;
 
   if (ntiles > 0) issue_loads(tile0, tnorm0, 0);
   // LATE (the buffered select): the select of tile t runs after the
@@ -423,6 +428,18 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     // epilogue) does not wait for the prefetch
     if constexpr (MODE != 2)
       if (share && bound_tile(t)) seen.load(gk, a.mslots);
+    // the prefilter words of the tile's row blocks (rows past the split:
+    // nothing allowed, and no word read past the filter)
+    uint32_t fwd[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) fwd[r] = 0u;
+    if (filt) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int64_t rr = r0 + (int64_t)t * TR + 32 * r;
+        if (qvalid && rr < r1g) fwd[r] = fw[rr >> 5];
+      }
+    }
     // the next tile into the other buffer (read in the previous tile, which
     // every wavefront has left: the barrier below); unconditional (past the
     // last tile the range is empty and the loads write zeros)
@@ -495,8 +512,12 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
           sc0[i] = acc[0][i];
           sc1[i] = acc[1][i];
         }
+        const uint32_t am = filt ? allowed_positions(fwd[0], h) |
+                                       (allowed_positions(fwd[RB - 1], h) << 16)
+                                 : 0xffffffffu;
         inserted = select_pair_buf<T, L2, CB, 256>(K, I, thr, sc0, sc1, h,
-                                              idbase + (uint32_t)(t * TR), nrows - t * TR, cb);
+                                              idbase + (uint32_t)(t * TR), nrows - t * TR, cb,
+                                              am);
       } else
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
@@ -520,7 +541,8 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
             }
           }
         } else {
-          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r);
+          inserted |= select_block<T, L2>(K, I, thr, sc, h, id0, nrows - t * TR - 32 * r,
+                                          filt ? allowed_positions(fwd[r], h) : 0xffffffffu);
         }
       }
       if (MODE != 2 && share && qvalid && inserted) {
@@ -700,6 +722,10 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   // the lane's segment
   const int seg = RS ? 8 * split + 2 * wave + h : 2 * split + h;
   const int myslot = share ? seg % a.mslots : 0;
+  // Prefilter: the lane's query's filter words (word j: global rows 32 j ..
+  // 32 j + 31; the split's first row is a multiple of 128)
+  const bool filt = a.allow != nullptr;
+  const uint32_t* fw = filt ? a.allow + (int64_t)(qvalid ? q : 0) * a.allow_stride : nullptr;
 
   if (nsteps > 0) {
     issue_loads(tA0, tQ0);
@@ -720,9 +746,21 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
     // the bound is used at the tile's last chunk: read it in that step only
     const bool last = c + 1 == NC;
     SharedBound<S> seen;
+    uint32_t fwd[NB];
+#pragma unroll
+    for (int r = 0; r < NB; ++r) fwd[r] = 0u;
     if (last) {
       seen.clear();
       if (share) seen.load(gk, a.mslots);
+      // the prefilter words of the wavefront's row blocks of this tile (rows
+      // past the split: none allowed, and no word read past the filter)
+      if (filt) {
+#pragma unroll
+        for (int r = 0; r < NB; ++r) {
+          const int64_t rr = r0 + (int64_t)t * kDeepRows + 32 * (rb0 + r);
+          if (qvalid && rr < r1) fwd[r] = fw[rr >> 5];
+        }
+      }
     }
     // the fetched tile's parity, read before store_chunk advances pc
     const int ftpar = (c + 1 == NC) ? ((t + 1) & 1) : (t & 1);
@@ -789,7 +827,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
             }
           }
           inserted |= select_block<T, L2>(K, I, thr, sc, h, id0 + 32 * (rb0 + r),
-                                          lim0 - 32 * (rb0 + r));
+                                          lim0 - 32 * (rb0 + r),
+                                          filt ? allowed_positions(fwd[r], h) : 0xffffffffu);
         }
         if (share && qvalid && inserted) {
           const uint32_t kp = list_key(K, a.pubj);
@@ -1432,6 +1471,14 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   __shared__ int s_cnt;
   const int row = blockIdx.x;
   const float* sr = a.S + (int64_t)row * a.n;
+  // prefilter: a row it leaves out ranks 0, below every real rank (~id >=
+  // 2^31), so it is picked only when fewer than k rows are allowed, and
+  // the gather below drops it (an empty slot)
+  const uint32_t* fw = a.allow ? a.allow + (int64_t)a.qsel[row] * a.allow_stride : nullptr;
+  auto rank_at = [&](int64_t j) -> uint64_t {
+    if (fw && !((fw[j >> 5] >> (j & 31)) & 1u)) return 0ull;
+    return rank_of(sr[j], (uint32_t)j);
+  };
   int need = (int)(a.n < a.k ? a.n : a.k);
   uint64_t prefix = 0, mask = 0;
   for (int pass = 0; pass < 8 && need > 0; ++pass) {
@@ -1439,7 +1486,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     hist[threadIdx.x] = 0;
     __syncthreads();
     for (int64_t j = threadIdx.x; j < a.n; j += 256) {
-      const uint64_t r = rank_of(sr[j], (uint32_t)j);
+      const uint64_t r = rank_at(j);
       wave_hist_add(hist, (uint32_t)(r >> shift) & 255u, (r & mask) == prefix);
     }
     __syncthreads();
@@ -1466,9 +1513,10 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   __syncthreads();
   if (a.n > 0) {
     for (int64_t j = threadIdx.x; j < a.n; j += 256) {
-      const uint64_t r = rank_of(sr[j], (uint32_t)j);
-      const int slot = wave_take(&s_cnt, r >= prefix);
-      if (r >= prefix && slot < kMaxK) sel[slot] = r;
+      const uint64_t r = rank_at(j);
+      const bool keep = r >= prefix && r != 0;
+      const int slot = wave_take(&s_cnt, keep);
+      if (keep && slot < kMaxK) sel[slot] = r;
     }
   }
   __syncthreads();
@@ -2082,9 +2130,40 @@ hipError_t launch_ivf_slots(const IvfPlanArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// A row-major bitmap of nq * n bits (not padded per query) as word-aligned
+// rows [nq][W], W = ceil(n / 32): word (q, w) = bits q n + 32 w .. + 31 of the
+// bitmap, those past row n - 1 cleared.  The bitmap holds ceil(nq n / 32)
+// words; a word straddling two input words reads the second only when it
+// exists.
+__global__ void filter_rows_kernel(const uint32_t* bm, int64_t nq, int64_t n, int64_t W,
+                                   uint32_t* out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nq * W) return;
+  const int64_t q = i / W, w = i % W;
+  const uint64_t bit = (uint64_t)q * (uint64_t)n + 32u * (uint64_t)w;
+  const int64_t total = (nq * n + 31) / 32;
+  const int64_t wi = (int64_t)(bit >> 5);
+  const uint32_t sh = (uint32_t)(bit & 31);
+  uint32_t v = bm[wi] >> sh;
+  if (sh != 0 && wi + 1 < total) v |= bm[wi + 1] << (32 - sh);
+  const int64_t left = n - 32 * w;  // rows of this word, >= 1
+  if (left < 32) v &= (1u << left) - 1u;
+  out[i] = v;
+}
+
 __global__ void iota_kernel(int* p, int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < count) p[i] = (int)i;
+}
+
+hipError_t launch_filter_rows(const uint32_t* bitmap, int64_t nq, int64_t n, uint32_t* out,
+                              hipStream_t s) {
+  const int64_t W = (n + 31) / 32;
+  const int64_t count = nq * W;
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(filter_rows_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
+                     bitmap, nq, n, W, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_iota(int* p, int64_t count, hipStream_t s) {

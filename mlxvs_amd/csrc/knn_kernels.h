@@ -85,6 +85,12 @@ struct FusedArgs {
   // when set, the item count is on the device (launch_ivf_plan) and
   // n_items only bounds it: the workgroups past *n_items_dev return at once
   const int* n_items_dev;
+  // Prefilter (dense fused and deep kernels; rows_per_split a multiple of
+  // 32): when set, base row r may be returned for query q only if bit r % 32
+  // of allow[q * allow_stride + r / 32] is set (a bitset: stride 0; a bitmap:
+  // word-aligned rows of words per query, launch_filter_rows).
+  const uint32_t* allow;
+  int64_t allow_stride;
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
@@ -275,8 +281,18 @@ struct SelectArgs {
   int dist_mode;         // 0 float metric, 1 Hamming
   int32_t* ids;
   float* dists;
+  // Prefilter (FusedArgs): row j of S[i] takes part only if bit j % 32 of
+  // allow[qsel[i] * allow_stride + j / 32] is set; null: every row
+  const uint32_t* allow;
+  int64_t allow_stride;
 };
 hipError_t launch_select(const SelectArgs& a, hipStream_t s);
+
+// A prefilter bitmap of nq * n bits, row-major over (query, row) and not
+// padded per query (bit q n + r of the words, as cuVS's filters.from_bitmap
+// packs it), as word-aligned rows: out [nq][ceil(n / 32)], bits past n zero.
+hipError_t launch_filter_rows(const uint32_t* bitmap, int64_t nq, int64_t n, uint32_t* out,
+                              hipStream_t s);
 
 // Shared per-query bounds of the fused kernels: slots per query for list
 // length T, and their initial state for m = ceil(k / T) used slots (0 in the
@@ -391,6 +407,9 @@ struct RedoArgs {
   const int* slots;      // IVF: [nq][P] first column of each probe
   const int* offsets;    // IVF: [lists + 1]
   int P;
+  // Prefilter of float rows (FusedArgs), null: every row
+  const uint32_t* allow;
+  int64_t allow_stride;
 };
 hipError_t launch_redo(const RedoArgs& a, hipStream_t s);
 

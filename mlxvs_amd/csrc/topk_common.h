@@ -169,6 +169,16 @@ __device__ __forceinline__ uint32_t real_rows(int h, int lim) {
   return m;
 }
 
+// Prefilter: the lane's positions of a 32-row block whose rows a filter
+// allows, from the block's filter word w (bit r: row r of the block).
+// Position i is row 8 (i / 4) + 4 h + i % 4, so the lane keeps nibble h of
+// every byte of w: bit i of the result = bit 8 (i / 4) + 4 h + i % 4 of w.
+__device__ __forceinline__ uint32_t allowed_positions(uint32_t w, int h) {
+  uint32_t x = (w >> (4 * h)) & 0x0F0F0F0Fu;  // byte b: nibble h of byte b
+  x = (x | (x >> 4)) & 0x00FF00FFu;           // bytes 0, 2: two nibbles each
+  return (x | (x >> 8)) & 0x0000FFFFu;
+}
+
 // Inserts the scores of one 32-row block (rows id0 + 8 (i / 4) + 4 h + i % 4,
 // the first `lim` of the block real) that pass the lane's threshold.  The
 // common case -- nothing passes -- costs a max tree and one compare; the
@@ -183,10 +193,12 @@ __device__ __forceinline__ uint32_t real_rows(int h, int lim) {
 // HALF: sc holds half scores (s / 2; the score 2 q.b - |b|^2 of L2 as q.b -
 // |b|^2 / 2) and thr a filter on them (filter_of): the keys are made from
 // 2 sc, which is exact, so the lists are those of the full scores.
+// allowm: the positions a prefilter allows (allowed_positions), all by
+// default.
 template <int T, bool HALF = false>
 __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                              const float (&sc)[16], int h, uint32_t id0,
-                                             int lim) {
+                                             int lim, uint32_t allowm = 0xffffffffu) {
   const float m0 = fmaxf(fmaxf(sc[0], sc[1]), sc[2]), m1 = fmaxf(fmaxf(sc[3], sc[4]), sc[5]);
   const float m2 = fmaxf(fmaxf(sc[6], sc[7]), sc[8]), m3 = fmaxf(fmaxf(sc[9], sc[10]), sc[11]);
   const float m4 = fmaxf(fmaxf(sc[12], sc[13]), sc[14]);
@@ -197,6 +209,7 @@ __device__ __forceinline__ bool select_block(uint32_t (&K)[T], uint32_t (&I)[T],
 #pragma unroll
   for (int i = 0; i < 16; ++i) pm |= !(sc[i] < thr) ? (1u << i) : 0u;
   if (lim < 32) pm &= real_rows(h, lim);
+  pm &= allowm;
   const bool any = pm != 0;
   // (a guarded do-while: the list's registers then carry straight round
   // the loop, where a while loop copies them at every iteration)
@@ -306,10 +319,13 @@ __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], fl
 // select_pair with the candidate buffer: the same filter and the same lists
 // once the buffer is flushed.  Returns whether the list changed (a flush
 // took place), which is when the lane's shared-bound key may have risen.
+// allowm: the positions a prefilter allows (block 0 in bits 0-15, block 1
+// in 16-31), all by default.
 template <int T, bool HALF, int B, int S>
 __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                                 const float (&sc0)[16], const float (&sc1)[16],
-                                                int h, uint32_t id0, int lim, CandBuf<B, S>& cb) {
+                                                int h, uint32_t id0, int lim, CandBuf<B, S>& cb,
+                                                uint32_t allowm = 0xffffffffu) {
   // (no max tree and vote first: some lane passes in almost every pair of
   // blocks of a list of 16, so the mask is built anyway)
   // the failing positions: the sign of x - thr (x >= thr gives +0 or more),
@@ -321,7 +337,7 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
   for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc1[i] - thr), 31);
 #pragma unroll
   for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc0[i] - thr), 31);
-  uint32_t pm = ~fm;
+  uint32_t pm = ~fm & allowm;
   if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
   bool flushed = false;
   if (__builtin_amdgcn_ballot_w64(pm != 0) == 0) return false;

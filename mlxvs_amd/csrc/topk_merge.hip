@@ -424,9 +424,17 @@ struct FloatScorer {
   const void* query;
   const float* bnorm;  // -|b|^2 / 2 (L2) or null
   int ld, d, f16;
+  const uint32_t* allow = nullptr;  // the query's prefilter words, or null
   __device__ __forceinline__ int64_t begin(const RedoArgs& a, int q) {
     query = (const char*)a.queries + (int64_t)q * ld * (f16 ? 2 : 4);
+    allow = a.allow ? a.allow + (int64_t)q * a.allow_stride : nullptr;
     return a.n;
+  }
+  // the selection key of row j; 0 (no candidate) for a row the prefilter
+  // leaves out
+  __device__ __forceinline__ uint32_t key(int64_t j) const {
+    if (allow && !((allow[j >> 5] >> (j & 31)) & 1u)) return 0u;
+    return key_nz((*this)(j));
   }
   __device__ __forceinline__ float operator()(int64_t j) const {
     float acc = 0.0f;
@@ -460,6 +468,7 @@ struct HammingScorer {
     for (int c = 0; c < w; ++c) acc += __popc(query[c] ^ b[c]);
     return -(float)acc;
   }
+  __device__ __forceinline__ uint32_t key(int64_t j) const { return key_nz((*this)(j)); }
 };
 // IVF-Flat: the query's candidate columns, probe by probe (probe p's rows
 // from column slots[p]); fp32 rows of a multiple of 4 values, with the
@@ -515,6 +524,7 @@ struct IvfScorer {
     const float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     return bnorm ? 2.0f * (dot + bnorm[row]) : dot;
   }
+  __device__ __forceinline__ uint32_t key(int64_t c) { return key_nz((*this)(c)); }
 };
 
 // LDS of one exact select over scored rows.
@@ -576,10 +586,10 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
           key[e] = (uint32_t)(r >> 32);
           low[e] = (uint32_t)r;
         } else if constexpr (Scorer::kAnyRow) {
-          const uint32_t kk = key_nz(sc(c0 + c));
+          const uint32_t kk = sc.key(c0 + c);
           key[e] = c < valid ? kk : 0u;
         } else {
-          key[e] = c < valid ? key_nz(sc(c0 + c)) : 0u;
+          key[e] = c < valid ? sc.key(c0 + c) : 0u;
         }
       }
     }
@@ -647,10 +657,13 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
     __syncthreads();
     auto visit = [&](auto f) {
       for (int64_t c = c0r + tid; c < c1r; c += NT) {
-        if constexpr (Scorer::kRanks || Scorer::kChunk)
+        if constexpr (Scorer::kRanks || Scorer::kChunk) {
           f(sc.rank(c));
-        else
-          f(((uint64_t)key_nz(sc(c)) << 32) | (uint32_t)(~(uint32_t)c));
+        } else {
+          // (a row left out by a prefilter: rank 0, no candidate)
+          const uint32_t kk = sc.key(c);
+          f(kk ? (((uint64_t)kk << 32) | (uint32_t)(~(uint32_t)c)) : 0ull);
+        }
       }
     };
     radix_pick<NT>(visit, keff, sm.hist, sm.st);

@@ -1,5 +1,5 @@
-"""cuVS's ``cuvs.neighbors``: the brute-force index."""
+"""cuVS's ``cuvs.neighbors``: the brute-force index and its prefilters."""
 
-from mlxvs_amd.cuvs.neighbors import brute_force
+from mlxvs_amd.cuvs.neighbors import brute_force, filters
 
-__all__ = ["brute_force"]
+__all__ = ["brute_force", "filters"]

@@ -10,9 +10,16 @@ version 0, readable by cuVS's own ``brute_force.load``.
 Distance types served: ``"sqeuclidean"`` (L2Expanded), ``"euclidean"`` /
 ``"l2"`` (L2SqrtExpanded), ``"cosine"`` (CosineExpanded),
 ``"inner_product"`` and ``"bitwise_hamming"``.  cuVS's element-wise
-pairwise metrics (cityblock, chebyshev, minkowski, ...) and prefilters are
-evaluated outside a fused top-k path and are not offered: they raise
-``ValueError``.
+pairwise metrics (cityblock, chebyshev, minkowski, ...) are evaluated
+outside a fused top-k path and are not offered: they raise ``ValueError``.
+
+Prefilters (``filters.from_bitset`` / ``from_bitmap``) run inside the fused
+select (``brute_force_knn_filtered``): a row a filter leaves out never
+enters a candidate list, and a query with fewer than k allowed rows gets -1
+ids and the worst distance past them, as the reference's masked selection
+gives (python/mlxvs/cuvs/neighbors/brute_force.py:97-136).  Bit-packed rows
+with a prefilter are searched as {0, 1} float rows, whose squared L2
+distance is their Hamming distance (exact in float32).
 """
 
 from __future__ import annotations
@@ -121,15 +128,27 @@ def search(index, queries, k, neighbors=None, distances=None, resources=None,
     nearest first (for inner product, largest first); -1 past the rows there
     are.  Given ``neighbors`` / ``distances`` arrays are filled and returned.
     """
-    from mlxvs_amd import brute_force_knn, hamming_knn
+    from mlxvs_amd import brute_force_knn, brute_force_knn_filtered, hamming_knn
 
     if not getattr(index, "trained", False):
         raise ValueError("search needs a built index (see brute_force.build)")
-    if prefilter is not None and getattr(prefilter, "type", "none") != "none":
-        raise ValueError("prefilters are not offered by this exact engine")
+    kind = "none" if prefilter is None else getattr(prefilter, "type", None)
+    if kind not in ("none", "bitset", "bitmap"):
+        raise ValueError(f"prefilter must come from cuvs.neighbors.filters, got {prefilter!r}")
     dist = index._distance
     q = np.asarray(queries)
-    if dist.engine is None:
+    if kind != "none":
+        words = np.asarray(prefilter.array, dtype=np.uint32)
+        fkw = {kind: words}
+        if dist.engine is None:
+            # {0, 1} rows: squared L2 distance = Hamming distance
+            bits = np.unpackbits(index._rows, axis=1).astype(np.float32)
+            qbits = np.unpackbits(np.asarray(q, dtype=np.uint8), axis=1).astype(np.float32)
+            ids, out = brute_force_knn_filtered(bits, qbits, k, "l2", **fkw)
+        else:
+            ids, raw = brute_force_knn_filtered(index._rows, q, k, dist.engine, **fkw)
+            out = dist.units(raw)
+    elif dist.engine is None:
         ids, out = hamming_knn(index._rows, q, k)
     else:
         ids, raw = brute_force_knn(index._rows, q, k, dist.engine)

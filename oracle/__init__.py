@@ -41,6 +41,7 @@ def lib():
         L = ctypes.CDLL(str(LIB_PATH))
         vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         L.oracle_knn_f32.argtypes = [vp, i64, vp, i64, ci, ci, ci, ci, vp, vp]
+        L.oracle_knn_filtered_f32.argtypes = [vp, i64, vp, i64, ci, ci, ci, ci, vp, ci, vp, vp]
         L.oracle_self_graph_f32.argtypes = [vp, i64, ci, ci, ci, ci, vp, vp]
         L.oracle_self_graph_rows.argtypes = [vp, i64, ci, ci, ci, ci, i64, vp, vp]
         L.oracle_hamming.argtypes = [vp, i64, vp, i64, ci, ci, ci, vp, vp]
@@ -50,7 +51,7 @@ def lib():
         L.oracle_ivf_flat.argtypes = [vp, ci, vp, vp, vp, ci, ci, vp, i64, ci, ci, ci, vp, vp]
         L.oracle_topk_merge.argtypes = [vp, i64, i64, vp, vp, ctypes.c_int32, ci, ci, vp, vp]
         L.oracle_key.restype = ctypes.c_uint32
-        for f in ("oracle_knn_f32", "oracle_self_graph_f32", "oracle_self_graph_rows",
+        for f in ("oracle_knn_f32", "oracle_knn_filtered_f32", "oracle_self_graph_f32", "oracle_self_graph_rows",
                   "oracle_hamming", "oracle_topk_merge",
                   "oracle_f16_to_f32", "oracle_pack_words"):
             getattr(L, f).restype = ci
@@ -86,6 +87,37 @@ def knn(base, queries, k, metric="l2", nthreads=None):
                               nthreads or threads(), _p(ids), _p(dist))
     if rc:
         raise ValueError(f"oracle_knn_f32 rejected the arguments ({rc})")
+    return ids, dist
+
+
+def filter_words(mask):
+    """A bool mask as filter words, as cuVS's filters.from_bitset /
+    from_bitmap pack it (python/mlxvs/cuvs/neighbors/filters.py:31-37): the
+    flattened bits little-endian, padded to whole uint32 words."""
+    m = np.asarray(mask, dtype=np.bool_).ravel()
+    b = np.packbits(m, bitorder="little")
+    return np.pad(b, (0, -len(b) % 4)).view(np.uint32).copy()
+
+
+def knn_filtered(base, queries, k, metric="l2", bitset=None, bitmap=None, nthreads=None):
+    """Restated prefiltered brute-force search (python/mlxvs/cuvs/neighbors/
+    brute_force.py:97-136): brute_force_knn over the rows a bool bitset
+    [n] or bitmap [nq, n] allows (at most one of them)."""
+    b = np.ascontiguousarray(base, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq = q.shape[0]
+    kind, words = 0, None
+    if bitset is not None:
+        kind, words = 1, filter_words(bitset)
+    elif bitmap is not None:
+        kind, words = 2, filter_words(bitmap)
+    ids = np.empty((nq, k), np.int32)
+    dist = np.empty((nq, k), np.float32)
+    rc = lib().oracle_knn_filtered_f32(_p(b), b.shape[0], _p(q), nq, b.shape[1], k, _m(metric),
+                                       nthreads or threads(), None if words is None else _p(words),
+                                       kind, _p(ids), _p(dist))
+    if rc:
+        raise ValueError(f"oracle_knn_filtered_f32 rejected the arguments ({rc})")
     return ids, dist
 
 

@@ -38,6 +38,14 @@
  *      min(k, width) columns by key, then lowest column; a pick whose score is
  *      infinite or that is buffer padding is missing (-1, +inf for L2, -inf
  *      otherwise); L2 distance = -score.
+ *  - prefiltered search         python/mlxvs/cuvs/neighbors/brute_force.py:97-136
+ *      with filters.py:39-50 and _common.py:55-66 (oracle_knn_filtered_f32):
+ *      a bitset is one bit per row (bit i % 32 of word i / 32), a bitmap one
+ *      bit per (query, row), bit q n + i of the words, row-major and not
+ *      padded per query; a row whose bit is clear takes no part (its score
+ *      is replaced by the worst value before the selection, :120-127, and a
+ *      pick of it becomes -1, :135); the rest is brute_force_knn over the
+ *      allowed rows, ids still numbering all rows.
  *  - self k-NN graph            src/all_neighbors.cpp:250-263 (k + 1
  *      neighbours) and 56-95 (merge_lists: drop -1 and the row itself, sort by
  *      distance, keep k, pad -1 / +inf for L2 or -inf otherwise).
@@ -246,7 +254,16 @@ typedef struct {
   int d, k, metric;
   int32_t* ids;
   float* dists;
+  const uint32_t* allow; /* filter words or NULL (every row allowed) */
+  int allow_kind;        /* 1: bitset, bit j; 2: bitmap, bit q n + j */
 } knn_ctx;
+
+/* Whether row j may be returned for query q (filters.py:39-50). */
+static inline int row_allowed(const knn_ctx* c, int64_t q, int64_t j) {
+  if (!c->allow) return 1;
+  const uint64_t b = c->allow_kind == 2 ? (uint64_t)q * (uint64_t)c->n + (uint64_t)j : (uint64_t)j;
+  return (int)((c->allow[b >> 5] >> (b & 31)) & 1u);
+}
 
 static void knn_rows(void* p, int64_t lo, int64_t hi) {
   knn_ctx* c = (knn_ctx*)p;
@@ -259,6 +276,7 @@ static void knn_rows(void* p, int64_t lo, int64_t hi) {
     const float* qr = c->queries + (size_t)q * c->d;
     heap_t h = {hv, hs, hi_, 0, k};
     for (int64_t j = 0; j < c->n; ++j) {
+      if (!row_allowed(c, q, j)) continue;
       float dot = dot8(qr, c->base + (size_t)j * c->d, c->d);
       /* src/knn.cpp:114-115: 2 * scores - |b|^2 (2 * dot is exact) */
       float s = c->metric == M_L2 ? 2.0f * dot - c->bnorm[j] : dot;
@@ -307,9 +325,9 @@ static void unit_part(void* p, int64_t lo, int64_t hi) {
  * dists [nq, k] float32.  k in [1, 256] is required when n >= 1; for n == 0
  * every slot is -1 / +-inf.
  */
-int oracle_knn_f32(const float* base, int64_t n, const float* queries,
+static int knn_f32(const float* base, int64_t n, const float* queries,
                    int64_t nq, int d, int k, int metric, int threads,
-                   int32_t* ids, float* dists) {
+                   const uint32_t* allow, int allow_kind, int32_t* ids, float* dists) {
   if (d < 1 || n < 0 || nq < 0 || k < 0 || metric < 0 || metric > 2)
     return ORACLE_EINVAL;
   if (n >= 1 && (k < 1 || k > 256)) return ORACLE_EINVAL;
@@ -331,10 +349,31 @@ int oracle_knn_f32(const float* base, int64_t n, const float* queries,
     norm_ctx nc = {base, d, bn};
     parallel_for(n, threads, norm_rows, &nc);
   }
-  knn_ctx c = {ub ? ub : base, bn, uq ? uq : queries, n, d, k, metric, ids, dists};
+  knn_ctx c = {ub ? ub : base, bn, uq ? uq : queries, n, d, k, metric, ids, dists,
+               allow, allow_kind};
   parallel_for(nq, threads, knn_rows, &c);
   free(ub); free(uq); free(bn);
   return ORACLE_OK;
+}
+
+int oracle_knn_f32(const float* base, int64_t n, const float* queries,
+                   int64_t nq, int d, int k, int metric, int threads,
+                   int32_t* ids, float* dists) {
+  return knn_f32(base, n, queries, nq, d, k, metric, threads, NULL, 0, ids, dists);
+}
+
+/*
+ * The same over the rows a filter allows (python/mlxvs/cuvs/neighbors/
+ * brute_force.py:97-136): kind 0 none (filter unused), 1 bitset of
+ * ceil(n / 32) words, 2 bitmap of ceil(nq n / 32) words.  Fewer allowed rows
+ * than k leave -1 / +-inf slots, as for n < k.
+ */
+int oracle_knn_filtered_f32(const float* base, int64_t n, const float* queries,
+                            int64_t nq, int d, int k, int metric, int threads,
+                            const uint32_t* filter, int kind, int32_t* ids, float* dists) {
+  if (kind < 0 || kind > 2 || (kind != 0 && !filter && n > 0 && nq > 0)) return ORACLE_EINVAL;
+  return knn_f32(base, n, queries, nq, d, k, metric, threads, kind ? filter : NULL, kind,
+                 ids, dists);
 }
 
 /* ---- float16 input ------------------------------------------------------ */

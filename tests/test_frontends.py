@@ -190,11 +190,11 @@ def test_brute_force_errors(tmp_path):
     with pytest.raises(ValueError, match="built"):
         brute_force.search(brute_force.Index(), x, 1)
 
-    class Bitset:
-        type = "bitset"
+    class Ranges:
+        type = "ranges"
 
     with pytest.raises(ValueError, match="prefilter"):
-        brute_force.search(brute_force.build(x), x, 1, prefilter=Bitset())
+        brute_force.search(brute_force.build(x), x, 1, prefilter=Ranges())
     p = tmp_path / "nodata.bin"
     brute_force.save(str(p), brute_force.build(x), include_dataset=False)
     with pytest.raises(ValueError, match="without its dataset"):
@@ -240,3 +240,39 @@ def test_kmeans_predict_arguments():
         mlxvs_amd.kmeans_predict(x, np.zeros((2, 4), np.float32), 0)
     with pytest.raises(ValueError, match="2-D"):
         mlxvs_amd.kmeans_predict(np.zeros(4, np.float32), np.zeros((2, 4), np.float32))
+
+
+def test_filters_pack_like_cuvs():
+    # cuVS's filters (reference python/mlxvs/cuvs/neighbors/filters.py:31-50):
+    # bool masks packed little-endian into uint32 words; words kept as they are
+    from mlxvs_amd.cuvs.neighbors import filters
+
+    keep = np.zeros(40, bool)
+    keep[[0, 5, 31, 32, 39]] = True
+    f = filters.from_bitset(keep)
+    assert f.type == "bitset" and f.array.dtype == np.uint32
+    assert f.array.tolist() == [(1 << 0) | (1 << 5) | (1 << 31), (1 << 0) | (1 << 7)]
+    assert filters.from_bitset(np.array([7, 9], np.uint32)).array.tolist() == [7, 9]
+    # a bitmap is row-major over (query, row), not padded per query: 3 x 5
+    # bits fill one word
+    bm = np.zeros((3, 5), bool)
+    bm[1, 0] = bm[2, 4] = True
+    assert filters.from_bitmap(bm).array.tolist() == [(1 << 5) | (1 << 14)]
+    assert filters.no_filter().type == "none"
+    with pytest.raises(ValueError):
+        filters.Prefilter("ranges")
+    with pytest.raises(ValueError):
+        filters.from_bitset(np.zeros(3, np.float32))
+
+
+def test_filtered_argument_checks():
+    import mlxvs_amd
+
+    x = np.zeros((40, 4), np.float32)
+    with pytest.raises(ValueError, match="not both"):
+        mlxvs_amd.brute_force_knn_filtered(x, x, 1, bitset=np.ones(40, bool),
+                                           bitmap=np.ones((40, 40), bool))
+    with pytest.raises(ValueError, match="words"):
+        mlxvs_amd.brute_force_knn_filtered(x, x, 1, bitset=np.ones(1, np.uint32))
+    with pytest.raises(ValueError, match=r"\[40, 40\]"):
+        mlxvs_amd.brute_force_knn_filtered(x, x, 1, bitmap=np.ones((40, 39), bool))

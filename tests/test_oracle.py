@@ -396,3 +396,87 @@ def test_topk_merge_known_answers(oracle):
     ids, _ = oracle.topk_merge(np.array([[5, 4]], np.float32), np.array([[3, 7]], np.int32),
                                np.array([[4.5, 9]], np.float32), 10, True, 2)
     assert ids.tolist() == [[10, 11]]
+
+
+# ---- prefiltered search (python/mlxvs/cuvs/neighbors/brute_force.py:97-136) -------
+
+def _masked_best(s, allowed, k):
+    """ids of the k best allowed rows per query by (score desc, id asc)."""
+    nq, n = s.shape
+    out = np.full((nq, k), -1, np.int64)
+    for i in range(nq):
+        idx = np.flatnonzero(allowed[i])
+        order = idx[np.lexsort((idx, -s[i, idx]))][:k]
+        out[i, :len(order)] = order
+    return out
+
+
+def _filter(kind, nq, n, p, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "bitmap":
+        allowed = rng.random((nq, n)) < p
+        return allowed, {"bitmap": allowed}
+    keep = rng.random(n) < p
+    return np.broadcast_to(keep, (nq, n)), {"bitset": keep}
+
+
+@pytest.mark.parametrize("kind", ["bitset", "bitmap"])
+@pytest.mark.parametrize("metric", ["l2", "inner_product"])
+@pytest.mark.parametrize("n,nq,d,k,p", [(300, 20, 16, 7, 0.3), (1000, 9, 8, 64, 0.05),
+                                        (77, 5, 3, 10, 0.5)])
+def test_filtered_integer_exact(oracle, kind, metric, n, nq, d, k, p):
+    # n = 77: a bitmap row starts mid-word (the bits are row-major over
+    # nq * n, not padded per query), so a per-query padded reading fails
+    b, q = int_rows(n, d, 11), int_rows(nq, d, 12)
+    allowed, kw = _filter(kind, nq, n, p, 13)
+    ids, dist = oracle.knn_filtered(b, q, k, metric, **kw)
+    s = oracle.exact_scores(q, b, metric)
+    want = _masked_best(s, allowed, k)
+    assert np.array_equal(ids, want)
+    got = np.take_along_axis(s, np.maximum(want, 0), 1)
+    exp = (-got if metric == "l2" else got).astype(np.float32)
+    pad = np.inf if metric == "l2" else -np.inf
+    assert np.array_equal(dist, np.where(want >= 0, exp, pad).astype(np.float32))
+
+
+@pytest.mark.parametrize("kind", ["bitset", "bitmap"])
+def test_filtered_reference_case(oracle, kind):
+    # python/tests/test_cuvs.py:196-211: the allowed rows' k nearest by
+    # scipy's sqeuclidean, as sets
+    from scipy.spatial.distance import cdist
+    rng = np.random.default_rng(4)
+    index = rng.random((300, 16)).astype(np.float32)
+    queries = rng.random((20, 16)).astype(np.float32)
+    if kind == "bitset":
+        keep = rng.random(300) < 0.3
+        allowed, kw = np.broadcast_to(keep, (20, 300)), {"bitset": keep}
+    else:
+        allowed = rng.random((20, 300)) < 0.3
+        kw = {"bitmap": allowed}
+    ids, _ = oracle.knn_filtered(index, queries, 7, "l2", **kw)
+    pw = np.where(allowed, cdist(queries, index, "sqeuclidean"), np.inf)
+    assert np.array_equal(np.sort(ids, 1), np.sort(np.argsort(pw, 1)[:, :7], 1))
+
+
+def test_filtered_limits(oracle):
+    b, q = int_rows(200, 8, 21), int_rows(6, 8, 22)
+    # every row allowed: the unfiltered search
+    full = oracle.knn_filtered(b, q, 12, "l2", bitset=np.ones(200, bool))
+    plain = oracle.knn(b, q, 12, "l2")
+    assert np.array_equal(full[0], plain[0]) and np.array_equal(full[1], plain[1])
+    # no row allowed: every slot missing, +inf for L2, -inf for similarities
+    ids, dist = oracle.knn_filtered(b, q, 5, "l2", bitmap=np.zeros((6, 200), bool))
+    assert (ids == -1).all() and (dist == np.inf).all()
+    ids, dist = oracle.knn_filtered(b, q, 5, "cosine", bitset=np.zeros(200, bool))
+    assert (ids == -1).all() and (dist == -np.inf).all()
+    # two allowed rows and k = 4: those two, then padding
+    keep = np.zeros(200, bool)
+    keep[[17, 190]] = True
+    ids, dist = oracle.knn_filtered(b, q, 4, "l2", bitset=keep)
+    assert (np.sort(ids[:, :2], 1) == [17, 190]).all() and (ids[:, 2:] == -1).all()
+    assert np.isfinite(dist[:, :2]).all() and (dist[:, 2:] == np.inf).all()
+    # the packing: bit i % 32 of word i / 32 (filters.py:39-43)
+    w = oracle.filter_words(np.arange(40) % 3 == 0)
+    assert w.dtype == np.uint32 and len(w) == 2
+    assert w[0] == sum(1 << i for i in range(0, 32, 3))
+    assert w[1] == sum(1 << (i - 32) for i in range(33, 40, 3))
