@@ -594,7 +594,8 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     }
   }
 
-  const int T = list_len_float(k);
+  // lists of 16 with a prefilter (its kernel instances; exact for every k)
+  const int T = allow ? 16 : list_len_float(k);
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;
   SplitPlan plan;
   const bool use_deep = deep && kern::deep_supported(kld, T, kf16);

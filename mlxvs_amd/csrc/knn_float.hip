@@ -230,7 +230,8 @@ constexpr int fused_rb() {
 // MODE 0: dense (split x query block).  MODE 1: IVF-Flat item, per-lane
 // lists (ids = buffer columns).  MODE 2: IVF-Flat item, scores written to
 // the candidate buffers.
-template <bool F16, int DH, int T, bool L2, int MODE = 0>
+// FILT: the dense search with a prefilter (FusedArgs::allow), lists of 16.
+template <bool F16, int DH, int T, bool L2, int MODE = 0, bool FILT = false>
 __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kernel(FusedArgs a) {
   using E = typename std::conditional<F16, _Float16, float>::type;
   constexpr int EPV = F16 ? 8 : 4;    // elements per 16-byte vector
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
   const int myslot = share ? (2 * seg + h) % a.mslots : 0;
   // Prefilter (dense only): the lane's query's filter words; word j covers
   // global rows 32 j .. 32 j + 31 (the split's first row is a multiple of 32)
-  const bool filt = MODE == 0 && a.allow != nullptr;
+  constexpr bool filt = FILT && MODE == 0;
   const uint32_t* fw = filt ? a.allow + (int64_t)(qvalid ? q : 0) * a.allow_stride : nullptr;
   const int64_t r1g = r0 + nrows;
 
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(256, (fused_min_blocks<F16, DH>())) void fused_kern
     uint32_t fwd[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) fwd[r] = 0u;
-    if (filt) {
+    if constexpr (filt) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int64_t rr = r0 + (int64_t)t * TR + 32 * r;
@@ -610,7 +611,8 @@ constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
 // 0) and 2 v + 1 (half 1), four steps per stage.  fp32: 32 dims per stage,
 // lane half h takes vectors 4 h .. 4 h + 3, four v_mfma_f32_32x32x2_f32
 // steps per vector.
-template <int T, bool L2, bool F16, bool RS>
+// FILT: with a prefilter (FusedArgs::allow), lists of 16.
+template <int T, bool L2, bool F16, bool RS, bool FILT = false>
 __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   constexpr int esize = F16 ? 2 : 4;
   constexpr int CH = kDeepChunkBytes / esize;  // dims per stage
@@ -724,7 +726,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const int myslot = share ? seg % a.mslots : 0;
   // Prefilter: the lane's query's filter words (word j: global rows 32 j ..
   // 32 j + 31; the split's first row is a multiple of 128)
-  const bool filt = a.allow != nullptr;
+  constexpr bool filt = FILT;
   const uint32_t* fw = filt ? a.allow + (int64_t)(qvalid ? q : 0) * a.allow_stride : nullptr;
 
   if (nsteps > 0) {
@@ -754,7 +756,7 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
       if (share) seen.load(gk, a.mslots);
       // the prefilter words of the wavefront's row blocks of this tile (rows
       // past the split: none allowed, and no word read past the filter)
-      if (filt) {
+      if constexpr (filt) {
 #pragma unroll
         for (int r = 0; r < NB; ++r) {
           const int64_t rr = r0 + (int64_t)t * kDeepRows + 32 * (rb0 + r);
@@ -1861,6 +1863,17 @@ int occupancy_t(int T) {
 template <bool F16, int DH, int T>
 hipError_t launch_inst(const FusedArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit * a.nqb);
+  if constexpr (T == 16) {
+    // a prefilter: its own instances (lists of 16 only)
+    if (a.allow) {
+      if (a.metric == kL2)
+        hipLaunchKernelGGL((fused_kernel<F16, DH, T, true, 0, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((fused_kernel<F16, DH, T, false, 0, true>), grid, dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  if (a.allow) return hipErrorInvalidValue;
   if (a.metric == kL2)
     hipLaunchKernelGGL((fused_kernel<F16, DH, T, true>), grid, dim3(256), 0, s, a);
   else
@@ -1946,6 +1959,17 @@ int deep_occupancy(bool f16) {
 template <int T, bool F16, bool RS>
 hipError_t deep_inst(const FusedArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit * a.nqb);
+  if constexpr (T == 16) {
+    // a prefilter: its own instances (lists of 16 only)
+    if (a.allow) {
+      if (a.metric == kL2)
+        hipLaunchKernelGGL((deep_kernel<T, true, F16, RS, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((deep_kernel<T, false, F16, RS, true>), grid, dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  if (a.allow) return hipErrorInvalidValue;
   if (a.metric == kL2)
     hipLaunchKernelGGL((deep_kernel<T, true, F16, RS>), grid, dim3(256), 0, s, a);
   else

@@ -85,8 +85,8 @@ struct FusedArgs {
   // when set, the item count is on the device (launch_ivf_plan) and
   // n_items only bounds it: the workgroups past *n_items_dev return at once
   const int* n_items_dev;
-  // Prefilter (dense fused and deep kernels; rows_per_split a multiple of
-  // 32): when set, base row r may be returned for query q only if bit r % 32
+  // Prefilter (dense fused and deep kernels, T = 16 only; rows_per_split a
+  // multiple of 32): when set, base row r may be returned for query q only if bit r % 32
   // of allow[q * allow_stride + r / 32] is set (a bitset: stride 0; a bitmap:
   // word-aligned rows of words per query, launch_filter_rows).
   const uint32_t* allow;
