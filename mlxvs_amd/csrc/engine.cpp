@@ -544,6 +544,17 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   const bool l2 = metric == kern::kL2;
   const bool kf16 = in.f16 && !cosine;
   const int esize = kf16 ? 2 : 4;
+  // At most kScanQueries queries and rows of 128 to 1,024 bytes: the VALU
+  // scan (HBM-bound at this size, where the MFMA kernels would leave all but
+  // a few of their query lanes idle), which sums the row norms itself and
+  // merges the splits' lists in its last workgroup: one launch
+  auto scan_nl = [](int64_t bytes) {
+    return (bytes == 128 || bytes == 256 || bytes == 512 || bytes == 1024) ? (int)(bytes / 128) : 0;
+  };
+  const bool in_place = ((uintptr_t)in.base % 16 == 0) && ((uintptr_t)in.queries % 16 == 0);
+  const int scan_nl_v = cosine ? scan_nl((int64_t)((d + 3) / 4 * 4) * 4)
+                               : (in_place ? scan_nl((int64_t)d * esize) : 0);
+  const bool use_scan = !allow && nq <= kern::kScanQueries && k <= 32 && scan_nl_v != 0;
   // rows longer than the register-resident kernels take go through the
   // deep kernel, which reads them in 128-byte chunks (32 fp32 / 64 fp16 dims)
   const bool deep = d > kern::kMaxFusedDimF32;
@@ -572,7 +583,7 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     kbase = ub;
     kq = uq;
   } else {
-    if (l2) {
+    if (l2 && !use_scan) {
       // the base norms are launched once the kernel is chosen (the streamed
       // small-batch scan sums them itself)
       bnorm = ar.take<float>((size_t)n);
@@ -594,6 +605,29 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     }
   }
 
+  if (use_scan && kld * esize == 128 * scan_nl_v) {
+    // whole chunks of 4,096 rows a split where there are enough of them,
+    // about one workgroup per CU in all
+    const int64_t want = std::max<int64_t>(8, device_slots(1) / nq);
+    int64_t rps = std::max<int64_t>(256, (n + want - 1) / want);
+    if (rps > 2048) rps = (rps + 4095) / 4096 * 4096;
+    const int64_t nsplit = ((n + rps - 1) / rps + 7) / 8 * 8;
+    if ((rps + 4096) * kld * esize < (int64_t(1) << 31)) {
+      uint64_t* part = ar.take<uint64_t>((size_t)(nq * nsplit * k));
+      kern::ScanFloatArgs sa{kbase, kq, n, (int)nq, kld, kf16 ? 1 : 0,
+                             cosine ? kern::kInnerProduct : metric, scan_nl_v, rps, (int)nsplit,
+                             k, part, ids, dists};
+      launch(s, "scan_f32", [&] { return kern::launch_scan_float(sa, s); });
+      return;
+    }
+  }
+  if (use_scan && l2) {
+    // (not taken after all: the norms the other kernels read)
+    bnorm = ar.take<float>((size_t)n);
+    qnorm = ar.take<float>((size_t)nq);
+    kern::PrepArgs pq{in.queries, nq, d, d, f16, qnorm, nullptr, nullptr, 0, 0};
+    launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
+  }
   // lists of 16 with a prefilter (its kernel instances; exact for every k)
   const int T = allow ? 16 : list_len_float(k);
   const int64_t qblocks = (nq + kQueriesPerBlock - 1) / kQueriesPerBlock;

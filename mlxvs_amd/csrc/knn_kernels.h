@@ -433,6 +433,35 @@ struct ScanBitsArgs {
   uint64_t* part;           // [nq][nsplit][k] out
 };
 hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s);
+// Exact float k-NN of a few queries (at most kScanQueries), HBM-bound:
+// workgroup (split, query) scores its split's rows against the query with
+// VALU dot products -- eight lanes a row, each reading nl 16-byte vectors
+// of it, the row's squared norm summed in the same pass for L2 -- and
+// selects their best k exactly (chunk bounds, candidates in LDS, radix
+// select) into part[q][split][k].  The last workgroup of each query to
+// finish (a counter per query in device memory, reset by that workgroup)
+// selects the query's best k of its nsplit * k ranks and writes ids and
+// distances in the output order: one launch a search.  Splits of one XCD
+// (id % 8) share its L2.
+constexpr int kScanQueries = 4;
+struct ScanFloatArgs {
+  const void* rows;         // [n][ld] fp32 or binary16, 16-byte aligned
+  const void* queries;      // [nq][ld]
+  int64_t n;
+  int nq;                   // 1 .. kScanQueries
+  int ld;                   // row length: ld * esize = 128 nl bytes, zero past d
+  int f16;
+  int metric;               // kL2 or kInnerProduct (cosine: unit rows, inner product)
+  int nl;                   // 16-byte vectors a lane reads per row: 1, 2, 4 or 8
+  int64_t rows_per_split;
+  int nsplit;               // a multiple of 8
+  int k;
+  uint64_t* part;           // [nq][nsplit][k] scratch
+  int32_t* ids;             // [nq][k] out
+  float* dists;             // [nq][k] out (may be null)
+};
+hipError_t launch_scan_float(const ScanFloatArgs& a, hipStream_t s);
+
 // The best k of each query's m ranks part[q][0, m) (0: none), as Hamming
 // results: ids, distances -score.  Groups of 4,096 ranks are reduced to
 // their best k on a workgroup each, level by level, into `scratch`

@@ -854,6 +854,130 @@ __global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
   for (int i = threadIdx.x; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
 }
 
+// ---- exact float scan of a few queries --------------------------------------------
+
+// Scores of float rows (fp32, or binary16 converted exactly) against one
+// query with VALU dot products, for the chunked select: eight lanes take a
+// row, lane j reading its 16-byte vectors j + 8 u (u < NL) and multiplying
+// them with the query's matching elements, which it holds in registers; the
+// row's squared norm is summed in the same pass (L2: score 2 q.b - |b|^2,
+// reference src/knn.cpp:114-115; otherwise q.b).  The eight partial sums
+// meet by lane exchanges (xor 1, 2, 4).  A load instruction of a wavefront
+// covers 128 NL contiguous bytes of each of eight rows.  chunk(): set s of
+// wavefront w is rows R (4 s + w) .. + 7 of the chunk (R = 8), and lane l
+// keeps the set with s % 8 == l % 8: sixteen rows a lane.  rank(r): one
+// row, with the same sums in the same order (for the rare pass over every
+// row).
+template <int NL, bool F16>
+struct FloatChunkScorer {
+  static constexpr bool kAnyRow = true;
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = true;
+  static constexpr int G = 8;          // lanes a row
+  static constexpr int R = 64 / G;     // rows a load instruction covers
+  static constexpr int EPV = F16 ? 8 : 4;
+  __amdgpu_buffer_rsrc_t rs;           // the split's rows (reads past them are zero)
+  int64_t r0;
+  bool l2;
+  const char* query;                   // the query row (rank())
+  float qv[NL][EPV];                   // the lane's query elements: vectors j + 8 u
+
+  __device__ __forceinline__ static void elems(u32x4 x, float (&e)[EPV]) {
+    if constexpr (F16) {
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const h8 h = __builtin_bit_cast(h8, x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = (float)h[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = __uint_as_float(x[i]);
+    }
+  }
+  // vector u of the lane's share of a row, into (dot, nrm)
+  __device__ __forceinline__ static void acc(const float (&q)[EPV], u32x4 x, float& dot,
+                                             float& nrm) {
+    float b[EPV];
+    elems(x, b);
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      dot = __builtin_fmaf(q[i], b[i], dot);
+      nrm = __builtin_fmaf(b[i], b[i], nrm);
+    }
+  }
+  __device__ __forceinline__ uint64_t rank_of_sums(float dot, float nrm, int64_t r) const {
+    const float sv = l2 ? 2.0f * dot - nrm : dot;
+    return ((uint64_t)key_nz(sv) << 32) | (uint32_t)(~(uint32_t)r);
+  }
+  __device__ __forceinline__ void chunk(int64_t c0, int64_t valid, uint32_t (&key)[16],
+                                        uint32_t (&low)[16]) const {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = lane % G, g = lane / G;
+    constexpr uint32_t rowb = 128u * NL;
+    const uint32_t base = (uint32_t)(c0 - r0 + R * w + g) * rowb + 16u * j;
+    constexpr uint32_t sstep = 4u * R * rowb;  // between a wavefront's sets
+    constexpr int NS = 16 * G;                 // sets a wavefront takes per chunk
+    constexpr int RING = (16 + NL - 1) / NL;   // sets in flight (16 loads)
+    u32x4 x[RING][NL];
+    auto issue = [&](int st) {
+#pragma unroll
+      for (int u = 0; u < NL; ++u)
+        x[st % RING][u] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + (uint32_t)st * sstep + 16u * G * u,
+                                                         0, 0));
+    };
+#pragma unroll
+    for (int st = 0; st < RING; ++st) issue(st);
+    float mdot = 0.0f, mnrm = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      u32x4 v[NL];
+#pragma unroll
+      for (int u = 0; u < NL; ++u) v[u] = x[st % RING][u];
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + RING < NS) issue(st + RING);
+      __builtin_amdgcn_sched_barrier(0);
+      float dot = 0.0f, nrm = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NL; ++u) acc(qv[u], v[u], dot, nrm);
+#pragma unroll
+      for (int o = 1; o < G; o <<= 1) {
+        dot += __shfl_xor(dot, o);
+        nrm += __shfl_xor(nrm, o);
+      }
+      const int e = st / G, jj = st % G;
+      mdot = j == jj ? dot : mdot;
+      mnrm = j == jj ? nrm : mnrm;
+      if (jj == G - 1) {
+        const int64_t c = (int64_t)R * (4 * (e * G + j) + w) + g;  // the lane's row in the chunk
+        const uint64_t r = rank_of_sums(mdot, mnrm, c0 + c);
+        key[e] = c < valid ? (uint32_t)(r >> 32) : 0u;
+        low[e] = (uint32_t)r;
+      }
+    }
+  }
+  __device__ __forceinline__ uint64_t rank(int64_t r) const {
+    const uint32_t off = (uint32_t)(r - r0) * (128u * NL);
+    float pd[G], pn[G];
+#pragma unroll
+    for (int jl = 0; jl < G; ++jl) {
+      pd[jl] = pn[jl] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NL; ++u) {
+        const int vec = jl + G * u;
+        const u32x4 xv = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u * vec, 0, 0));
+        float qe[EPV];
+        elems(*(const u32x4*)(query + 16 * vec), qe);
+        acc(qe, xv, pd[jl], pn[jl]);
+      }
+    }
+    // the exchanges' order: ((0 + 1) + (2 + 3)) + ((4 + 5) + (6 + 7))
+    const float dot = ((pd[0] + pd[1]) + (pd[2] + pd[3])) + ((pd[4] + pd[5]) + (pd[6] + pd[7]));
+    const float nrm = ((pn[0] + pn[1]) + (pn[2] + pn[3])) + ((pn[4] + pn[5]) + (pn[6] + pn[7]));
+    return rank_of_sums(dot, nrm, r);
+  }
+};
+
 // The per-split lists of one query as a rank source (through a buffer
 // resource: reads past the m ranks return 0, no rank).
 struct RankSource {
@@ -867,6 +991,92 @@ struct RankSource {
     return ((uint64_t)v[1] << 32) | v[0];
   }
 };
+
+// Searches of the float scan in flight: per query slot, the workgroups that
+// have written their split's list; the last one merges and resets it (zero
+// when the module loads; calls on a device are ordered, so one search uses
+// the counters at a time).
+__device__ uint32_t g_scan_done[kScanQueries];
+
+template <int NL, bool F16>
+__global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
+  constexpr int NT = 256;
+  constexpr int esize = F16 ? 2 : 4;
+  __shared__ RowSelect sm;
+  __shared__ int s_last;
+  __shared__ float s_qn;
+  const int tid = threadIdx.x;
+  // (split, query): XCD id % 8 takes splits xcd, xcd + 8, ..., each with
+  // its nq queries in a row
+  const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+  const int split = (local / a.nq) * 8 + xcd, q = local % a.nq;
+  const int64_t r0 = min(a.n, (int64_t)split * a.rows_per_split);
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  constexpr int rowb = 128 * NL;
+  FloatChunkScorer<NL, F16> sc;
+  sc.rs = __builtin_amdgcn_make_buffer_rsrc((void*)((const char*)a.rows + r0 * rowb), (short)0,
+                                           (int)((r1 - r0) * rowb), 0x00020000);
+  sc.r0 = r0;
+  sc.l2 = a.metric == kL2;
+  sc.query = (const char*)a.queries + (int64_t)q * rowb;
+  {
+    const int j = (tid & 63) % FloatChunkScorer<NL, F16>::G;
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+      FloatChunkScorer<NL, F16>::elems(*(const u32x4*)(sc.query + 16 * (j + 8 * u)), sc.qv[u]);
+  }
+  // the merge takes each list as a set: no sort
+  const int keff = select_rows(sc, r0, r1, a.k, sm, false);
+  uint64_t* dst = a.part + ((int64_t)q * a.nsplit + split) * a.k;
+  for (int i = tid; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+  // the last of the query's workgroups to get here selects its best k:
+  // every list is written before its workgroup counts itself (release), and
+  // the last reads them after the count (acquire)
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&g_scan_done[q], 1u) == (uint32_t)(a.nsplit - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const int64_t m = (int64_t)a.nsplit * a.k;
+  RankSource src{__builtin_amdgcn_make_buffer_rsrc((void*)(a.part + (int64_t)q * m), (short)0,
+                                                   (int)(m * 8), 0x00020000)};
+  const int kq = select_rows(src, 0, m, a.k, sm, true);
+  const bool l2 = a.metric == kL2;
+  if (tid == 0) {
+    g_scan_done[q] = 0u;
+    // |q|^2 in the order of the CPU restatement (eight interleaved partial
+    // sums, added pairwise), as the norm kernel sums it
+    float p8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (l2) {
+      const int d = a.ld;  // zero past the real dims
+      for (int i = 0; i < d; ++i) {
+        const float v = F16 ? (float)((const _Float16*)sc.query)[i] : ((const float*)sc.query)[i];
+        p8[i & 7] += v * v;
+      }
+    }
+    s_qn = ((p8[0] + p8[1]) + (p8[2] + p8[3])) + ((p8[4] + p8[5]) + (p8[6] + p8[7]));
+  }
+  __syncthreads();
+  const float qn = s_qn;
+  for (int i = tid; i < a.k; i += NT) {
+    const uint64_t r = i < kq ? sm.buf[i] : 0ull;
+    const int64_t o = (int64_t)q * a.k + i;
+    a.ids[o] = r ? id_of_rank(r) : -1;
+    if (!a.dists) continue;
+    if (!r) {
+      a.dists[o] = l2 ? INFINITY : -INFINITY;
+    } else {
+      const float sv = score_of_key((uint32_t)(r >> 32));
+      if (l2) {
+        const float v = qn - sv;  // reference src/knn.cpp:126-129
+        a.dists[o] = v > 0.0f ? v : 0.0f;
+      } else {
+        a.dists[o] = sv;
+      }
+    }
+  }
+}
 
 // The best k of each query's m ranks (the splits' lists of scan_bits).
 // Workgroup (q, g) takes ranks [g w, g w + w) of query q: with `out` set it
@@ -949,6 +1159,36 @@ hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s) {
     case 8: hipLaunchKernelGGL(scan_bits_kernel<8>, grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_scan_float(const ScanFloatArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.nsplit <= 0) return hipSuccess;
+  if (a.nq > kScanQueries || a.nsplit % 8 != 0 || a.k < 1 || a.k > kMaxK ||
+      a.rows_per_split <= 0 || (int64_t)a.nsplit * a.rows_per_split < a.n ||
+      (a.metric != kL2 && a.metric != kInnerProduct) || a.ld * (a.f16 ? 2 : 4) != 128 * a.nl ||
+      (uintptr_t)a.rows % 16 != 0 || (uintptr_t)a.queries % 16 != 0)
+    return hipErrorInvalidValue;
+  // a split's rows and the chunk past them, and the merge's ranks, in 32 bits
+  if ((a.rows_per_split + 4096) * 128 * a.nl >= (int64_t(1) << 31) ||
+      ((int64_t)a.nsplit * a.k + 4096) * 8 >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(a.nsplit * a.nq));
+#define MLXVS_SCAN(NL)                                                                        \
+  case NL:                                                                                    \
+    if (a.f16)                                                                                \
+      hipLaunchKernelGGL((scan_float_kernel<NL, true>), grid, dim3(256), 0, s, a);            \
+    else                                                                                      \
+      hipLaunchKernelGGL((scan_float_kernel<NL, false>), grid, dim3(256), 0, s, a);           \
+    break;
+  switch (a.nl) {
+    MLXVS_SCAN(1)
+    MLXVS_SCAN(2)
+    MLXVS_SCAN(4)
+    MLXVS_SCAN(8)
+    default: return hipErrorInvalidValue;
+  }
+#undef MLXVS_SCAN
   return hipGetLastError();
 }
 
