@@ -992,11 +992,100 @@ struct RankSource {
   }
 };
 
-// Searches of the float scan in flight: per query slot, the workgroups that
-// have written their split's list; the last one merges and resets it (zero
-// when the module loads; calls on a device are ordered, so one search uses
-// the counters at a time).
+// Searches of the float scan in flight, per query slot: the workgroups that
+// have written their split's list, and the largest k-th best rank of those
+// lists; the last workgroup merges and resets both (zero when the module
+// loads; calls on a device are ordered, so one search uses them at a time).
 __device__ uint32_t g_scan_done[kScanQueries];
+__device__ unsigned long long g_scan_bound[kScanQueries];
+
+// 64-bit bitonic sort across a wavefront, descending: lane i ends with the
+// i-th largest of the 64 values.
+__device__ __forceinline__ uint64_t wave_sort_desc64(uint64_t v, int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = __shfl_xor(v, stride);
+      const bool lo = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;
+      v = (lo == desc) ? (v > o ? v : o) : (v < o ? v : o);
+    }
+  }
+  return v;
+}
+
+// The best k of one query's split lists part[0, m) (ranks, 0: none), given
+// B, the largest of the lists' k-th best ranks (0 when no list has k): the
+// list holding B has k ranks at or above it, so the query's best k are all
+// at or above B, and only those ranks are gathered -- typically k and a
+// few more, which one wavefront sorts in registers; more than 64 go through
+// the radix select of the LDS buffer, more than the buffer holds through
+// select_rows over every rank.  Leaves the best keff in sm.buf[0, keff) in
+// the output order and returns keff.  All threads call it.
+__device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_t B,
+                                 RowSelect& sm) {
+  constexpr int NT = 256, PER = 16;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid == 0) sm.cnt = 0;
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)part, (short)0, (int)(m * 8), 0x00020000);
+  for (int64_t c0 = 0; c0 < m; c0 += (int64_t)NT * PER) {
+    // all of the thread's loads in flight at once (reads past m are zero)
+    uint64_t r[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                     rs, (uint32_t)(c0 + (int64_t)e * NT + tid) * 8u, 0, 0));
+      r[e] = ((uint64_t)v[1] << 32) | v[0];
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const bool take = r[e] != 0 && r[e] >= B;
+      const int slot = wave_take(&sm.cnt, take);
+      if (take && slot < kCandCap) sm.buf[slot] = r[e];
+    }
+  }
+  __syncthreads();
+  const int c = sm.cnt;
+  const int keff = c < k ? c : k;
+  if (c > kCandCap) {
+    // too many ranks tie at the bound to hold: every rank again
+    RankSource src{rs};
+    return select_rows(src, 0, m, k, sm, true);
+  }
+  if (c <= 64) {
+    // one wavefront: the keff best in rank order, which is the output order
+    // unless a -0 score is among them
+    bool negz = false;
+    if (tid < 64) {
+      const uint64_t v = wave_sort_desc64(lane < c ? sm.buf[lane] : 0ull, lane);
+      if (lane < keff) sm.buf[lane] = v;
+      negz = __builtin_amdgcn_ballot_w64(lane < keff && (uint32_t)(v >> 32) == 0x7fffffffu) != 0;
+    }
+    __shared__ int s_negz;
+    if (tid == 0) s_negz = negz;
+    __syncthreads();
+    if (!s_negz) return keff;
+  } else {
+    auto visit = [&](auto f) {
+      for (int i = tid; i < c; i += NT) f(sm.buf[i]);
+    };
+    radix_pick<NT>(visit, keff, sm.hist, sm.st);
+    radix_gather(visit, sm.st, sm.tmp);
+    __syncthreads();
+    for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
+    __syncthreads();
+  }
+  const int P = pow2_at_least(keff > 1 ? keff : 1);
+  for (int i = keff + tid; i < P; i += NT) sm.buf[i] = 0;
+  __syncthreads();
+  bitonic_desc<NT>(sm.buf, P, OutputOrder{});
+  return keff;
+}
 
 template <int NL, bool F16>
 __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
@@ -1025,13 +1114,40 @@ __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
     for (int u = 0; u < NL; ++u)
       FloatChunkScorer<NL, F16>::elems(*(const u32x4*)(sc.query + 16 * (j + 8 * u)), sc.qv[u]);
   }
+  const bool l2 = a.metric == kL2;
+  // |q|^2 (L2) in the order of the CPU restatement, as the norm kernel sums
+  // it: lane j < 8 of wavefront 0 adds the squares of elements j, j + 8, ...
+  // in turn, and the eight sums meet pairwise (xor 1, 2, 4)
+  if (l2 && tid < 64) {
+    float p = 0.0f;
+    if (tid < 8)
+      for (int i = tid; i < a.ld; i += 8) {
+        const float v = F16 ? (float)((const _Float16*)sc.query)[i] : ((const float*)sc.query)[i];
+        p += v * v;
+      }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) p += __shfl_xor(p, o);
+    if (tid == 0) s_qn = p;
+  }
   // the merge takes each list as a set: no sort
   const int keff = select_rows(sc, r0, r1, a.k, sm, false);
   uint64_t* dst = a.part + ((int64_t)q * a.nsplit + split) * a.k;
   for (int i = tid; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+  // the list's k-th best rank raises the query's bound (a list shorter than
+  // k does not bound)
+  if (tid < 64) {
+    const uint64_t v = (tid < a.k && keff == a.k) ? sm.buf[tid] : ~0ull;
+    uint64_t mn = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t w = __shfl_xor(mn, o);
+      mn = w < mn ? w : mn;
+    }
+    if (tid == 0 && keff == a.k) atomicMax(&g_scan_bound[q], (unsigned long long)mn);
+  }
   // the last of the query's workgroups to get here selects its best k:
-  // every list is written before its workgroup counts itself (release), and
-  // the last reads them after the count (acquire)
+  // every list and bound is written before its workgroup counts itself
+  // (release), and the last reads them after the count (acquire)
   __threadfence();
   __syncthreads();
   if (tid == 0) s_last = atomicAdd(&g_scan_done[q], 1u) == (uint32_t)(a.nsplit - 1);
@@ -1039,26 +1155,13 @@ __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
   if (!s_last) return;
   __threadfence();
   const int64_t m = (int64_t)a.nsplit * a.k;
-  RankSource src{__builtin_amdgcn_make_buffer_rsrc((void*)(a.part + (int64_t)q * m), (short)0,
-                                                   (int)(m * 8), 0x00020000)};
-  const int kq = select_rows(src, 0, m, a.k, sm, true);
-  const bool l2 = a.metric == kL2;
+  const uint64_t B = __hip_atomic_load(&g_scan_bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int kq = merge_split_lists(a.part + (int64_t)q * m, m, a.k, B, sm);
   if (tid == 0) {
     g_scan_done[q] = 0u;
-    // |q|^2 in the order of the CPU restatement (eight interleaved partial
-    // sums, added pairwise), as the norm kernel sums it
-    float p8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (l2) {
-      const int d = a.ld;  // zero past the real dims
-      for (int i = 0; i < d; ++i) {
-        const float v = F16 ? (float)((const _Float16*)sc.query)[i] : ((const float*)sc.query)[i];
-        p8[i & 7] += v * v;
-      }
-    }
-    s_qn = ((p8[0] + p8[1]) + (p8[2] + p8[3])) + ((p8[4] + p8[5]) + (p8[6] + p8[7]));
+    g_scan_bound[q] = 0ull;
   }
-  __syncthreads();
-  const float qn = s_qn;
+  const float qn = l2 ? s_qn : 0.0f;
   for (int i = tid; i < a.k; i += NT) {
     const uint64_t r = i < kq ? sm.buf[i] : 0ull;
     const int64_t o = (int64_t)q * a.k + i;
