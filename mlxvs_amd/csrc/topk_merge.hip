@@ -856,13 +856,25 @@ __global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
 
 // ---- exact float scan of a few queries --------------------------------------------
 
+// The sum of x over each aligned group of eight lanes, in every lane of the
+// group, by DPP moves (no LDS round trip): quad_perm [1,0,3,2] (xor 1),
+// quad_perm [2,3,0,1] (xor 2), then the half-row mirror (lane i and 7 - i):
+// lane j ends with ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7)) in the
+// group's order (each pairwise sum is the same either way round).
+__device__ __forceinline__ float dpp_sum8(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true));
+  return x;
+}
+
 // Scores of float rows (fp32, or binary16 converted exactly) against one
 // query with VALU dot products, for the chunked select: eight lanes take a
 // row, lane j reading its 16-byte vectors j + 8 u (u < NL) and multiplying
 // them with the query's matching elements, which it holds in registers; the
 // row's squared norm is summed in the same pass (L2: score 2 q.b - |b|^2,
 // reference src/knn.cpp:114-115; otherwise q.b).  The eight partial sums
-// meet by lane exchanges (xor 1, 2, 4).  A load instruction of a wavefront
+// meet by DPP lane moves (dpp_sum8).  A load instruction of a wavefront
 // covers 128 NL contiguous bytes of each of eight rows.  chunk(): set s of
 // wavefront w is rows R (4 s + w) .. + 7 of the chunk (R = 8), and lane l
 // keeps the set with s % 8 == l % 8: sixteen rows a lane.  rank(r): one
@@ -939,11 +951,8 @@ struct FloatChunkScorer {
       float dot = 0.0f, nrm = 0.0f;
 #pragma unroll
       for (int u = 0; u < NL; ++u) acc(qv[u], v[u], dot, nrm);
-#pragma unroll
-      for (int o = 1; o < G; o <<= 1) {
-        dot += __shfl_xor(dot, o);
-        nrm += __shfl_xor(nrm, o);
-      }
+      dot = dpp_sum8(dot);
+      nrm = dpp_sum8(nrm);
       const int e = st / G, jj = st % G;
       mdot = j == jj ? dot : mdot;
       mnrm = j == jj ? nrm : mnrm;

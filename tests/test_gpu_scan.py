@@ -73,3 +73,34 @@ def test_scan_calls_in_a_row(engine, oracle):
         ids, dist = engine.brute_force_knn(base, q, 10, "l2")
         oid, odist = oracle.knn(base, q, 10, "l2")
         assert np.array_equal(ids, oid) and np.array_equal(dist, odist), (n, nq)
+
+
+# ---- the Hamming few-query scan (scan_bits_kernel + rank merges) ------------
+
+@pytest.mark.parametrize("nbytes", [32, 64, 128])
+@pytest.mark.parametrize("nq,k", [(1, 1), (1, 100), (3, 37), (4, 256)])
+def test_hamming_scan_bit_exact(engine, oracle, nbytes, nq, k):
+    rng = np.random.default_rng(nbytes + nq * 10 + k)
+    rows = rng.integers(0, 256, (150_001, nbytes), dtype=np.uint8)
+    q = rng.integers(0, 256, (nq, nbytes), dtype=np.uint8)
+    q[0] = rows[77_777]          # an exact match: distance 0 (a -0 score)
+    ids, dist = engine.hamming_knn(rows, q, k)
+    oid, odist = oracle.hamming(rows, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    assert ids[0, 0] == 77_777 and dist[0, 0] == 0.0 and not np.signbit(dist[0, 0])
+
+
+def test_hamming_scan_ties_and_calls_in_a_row(engine, oracle):
+    # every row equal: all distances tie, the k lowest ids win
+    rows = np.full((80_000, 64), 0x5A, np.uint8)
+    ids, dist = engine.hamming_knn(rows, np.full((2, 64), 0x5B, np.uint8), 200)
+    assert (ids == np.arange(200)).all() and (dist == 64.0).all()
+    # searches of different split and query counts back to back
+    rng = np.random.default_rng(5)
+    for i, (n, nq, k) in enumerate([(300_000, 1, 100), (5_000, 4, 10), (40_000, 2, 256),
+                                    (300, 1, 100), (300_000, 1, 100)]):
+        r = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+        q = rng.integers(0, 256, (nq, 128), dtype=np.uint8)
+        ids, dist = engine.hamming_knn(r, q, k)
+        oid, odist = oracle.hamming(r, q, k)
+        assert np.array_equal(ids, oid) and np.array_equal(dist, odist), (n, nq, k)
