@@ -566,7 +566,14 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   float* bnorm = nullptr;
   float* qnorm = nullptr;
   const int f16 = in.f16 ? 1 : 0;
-  if (cosine) {
+  // Cosine on deep fp32 rows with k <= 16 (lists never drop a member, so
+  // nothing is redone): the deep kernel scales each dot product by the row's
+  // and the query's inverse norms instead of reading unit-row copies (C3:
+  // 6 GB written and read again every call)
+  const bool cos_factors = cosine && !in.f16 && deep && k <= 16 && !allow && !use_scan;
+  float* cnb = nullptr;  // cos_factors: |b|^2, |q|^2
+  float* cnq = nullptr;
+  if (cosine && !cos_factors) {
     kld = round_up(d, vmul);
     float* nb = ar.take<float>((size_t)n);
     float* nqv = ar.take<float>((size_t)nq);
@@ -583,6 +590,14 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     kbase = ub;
     kq = uq;
   } else {
+    if (cos_factors) {
+      cnb = ar.take<float>((size_t)n);
+      cnq = ar.take<float>((size_t)nq);
+      kern::PrepArgs pb{in.base, n, d, d, f16, cnb, nullptr, nullptr, 0, 0};
+      kern::PrepArgs pq{in.queries, nq, d, d, f16, cnq, nullptr, nullptr, 0, 0};
+      launch(s, "prep", [&] { return kern::launch_norms(pb, s); });
+      launch(s, "prep", [&] { return kern::launch_norms(pq, s); });
+    }
     if (l2 && !use_scan) {
       // the base norms are launched once the kernel is chosen (the streamed
       // small-batch scan sums them itself)
@@ -675,6 +690,17 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
     *out = p;
   };
 
+  if (!plan.ok && cos_factors) {
+    // (the exhaustive path reads unit rows: made here from the norms)
+    float* ub = ar.take<float>((size_t)n * kld);
+    float* uq = ar.take<float>((size_t)nq * kld);
+    kern::PrepArgs tb{kbase, n, kld, kld, 0, nullptr, cnb, ub, kld, 0};
+    kern::PrepArgs tq{kq, nq, kld, kld, 0, nullptr, cnq, uq, kld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(tb, s); });
+    launch(s, "prep", [&] { return kern::launch_transform(tq, s); });
+    kbase = ub;
+    kq = uq;
+  }
   if (!plan.ok) {
     // the exhaustive path stages its query list from the host
     if (ar.fixed()) invalid("mlxvs::brute_force_knn_noalloc", "these sizes need the exhaustive path, which the no-allocation entry does not take.");
@@ -696,11 +722,13 @@ void float_knn(Session& ss, const FloatInputs& in, int k, int metric, int32_t* i
   launch(s, "prep", [&] { return kern::launch_bounds_init(gkey, nq, slots, bp.m, s); });
   // XCD order: the register-resident kernels share only the row tiles
   // (split-major); the deep kernel streams query chunks too (split-minor)
-  kern::FusedArgs fa{kbase, kq, bnorm, n, (int)nq, kld, cosine ? kern::kInnerProduct : metric,
+  kern::FusedArgs fa{kbase, kq, cos_factors ? cnb : bnorm, n, (int)nq, kld,
+                     cos_factors ? kern::kCosine : cosine ? kern::kInnerProduct : metric,
                      plan.rows_per_split, plan.nsplit, T, k, part, gkey, bp.m, bp.pubj,
                      (int)qblocks, plan.xcd ? (use_deep ? 2 : 1) : 0};
   fa.allow = allow;
   fa.allow_stride = allow_stride;
+  fa.qnorm = cnq;
   if (use_deep)
     launch(s, "fused_deep", [&] { return kern::launch_deep(fa, kf16, deep_rs, s); });
   else if (use_stream)

@@ -611,8 +611,10 @@ constexpr int kDeepRB = kDeepRows / 32;        // MFMA row blocks per wavefront
 // 0) and 2 v + 1 (half 1), four steps per stage.  fp32: 32 dims per stage,
 // lane half h takes vectors 4 h .. 4 h + 3, four v_mfma_f32_32x32x2_f32
 // steps per vector.
-// FILT: with a prefilter (FusedArgs::allow), lists of 16.
-template <int T, bool L2, bool F16, bool RS, bool FILT = false>
+// FILT: with a prefilter (FusedArgs::allow), lists of 16.  COS: cosine by
+// factors (FusedArgs::qnorm), the tile's norm slots hold the rows' inverse
+// norms.
+template <int T, bool L2, bool F16, bool RS, bool FILT = false, bool COS = false>
 __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   constexpr int esize = F16 ? 2 : 4;
   constexpr int CH = kDeepChunkBytes / esize;  // dims per stage
@@ -662,9 +664,10 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   const int qrows = min(kQueriesPerBlock, a.nq - qb0);
   const char* qbase = (const char*)a.queries + (int64_t)qb0 * ld * esize;
   const int qrows_bytes = qrows * ld * esize;
-  const float* snorm = L2 ? a.bnorm + r0 : (const float*)a.base;
+  constexpr bool NORM = L2 || COS;  // the tiles carry a norm per row
+  const float* snorm = NORM ? a.bnorm + r0 : (const float*)a.base;
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)snorm, (short)0, L2 ? nrows * 4 : 0, 0x00020000);
+      (void*)snorm, (short)0, NORM ? nrows * 4 : 0, 0x00020000);
 
   // Lane l of load instruction j of wavefront w fills LDS vector p = 64 (w
   // NV + j) + l of a chunk buffer: row p / 8, slot p % 8, so it fetches
@@ -700,11 +703,17 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
       load16_to_lds(ra, dA + 256 * (wv * NV + j), voff[j]);
       load16_to_lds(rq, dQ + 256 * (wv * NV + j), voff[j]);
     }
-    if (L2) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
+    // the norms once a tile, with its first chunk (store_chunk keeps them)
+    if (NORM && pc == 0) pn = __builtin_amdgcn_raw_buffer_load_b32(rn, noff, 0, 0);
   };
   // stores the fetched chunk's norms (at chunk 0 of a tile) and moves on
   auto store_chunk = [&](int tpar) {
-    if (L2 && pc == 0 && tid < kDeepRows) tnorm[tpar][tid] = __uint_as_float(pn);
+    if (NORM && pc == 0 && tid < kDeepRows) {
+      const float x = __uint_as_float(pn);
+      // COS: 1 / max(|b|, 1e-30) (reference src/knn.cpp:30-33; a zero row
+      // scales a zero dot product)
+      tnorm[tpar][tid] = COS ? 1.0f / fmaxf(sqrtf(x), 1e-30f) : x;
+    }
     if (++pc == NC) {
       pc = 0;
       ++pt;
@@ -728,6 +737,8 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
   // 32 j + 31; the split's first row is a multiple of 128)
   constexpr bool filt = FILT;
   const uint32_t* fw = filt ? a.allow + (int64_t)(qvalid ? q : 0) * a.allow_stride : nullptr;
+  // COS: the lane's query's inverse norm
+  const float qinv = (COS && qvalid) ? 1.0f / fmaxf(sqrtf(a.qnorm[q]), 1e-30f) : 0.0f;
 
   if (nsteps > 0) {
     issue_loads(tA0, tQ0);
@@ -819,7 +830,11 @@ __global__ __launch_bounds__(256, 2) void deep_kernel(FusedArgs a) {
           float sc[16];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            if constexpr (L2) {
+            if constexpr (COS) {
+              const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * (rb0 + r) + 8 * j + 4 * h];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) sc[4 * j + u] = (acc[r][4 * j + u] * hn[u]) * qinv;
+            } else if constexpr (L2) {
               const floatx4 hn = *(const floatx4*)&tnorm[t & 1][32 * (rb0 + r) + 8 * j + 4 * h];
 #pragma unroll
               for (int u = 0; u < 4; ++u) sc[4 * j + u] = acc[r][4 * j + u] + hn[u];
@@ -1970,6 +1985,16 @@ hipError_t deep_inst(const FusedArgs& a, hipStream_t s) {
     }
   }
   if (a.allow) return hipErrorInvalidValue;
+  if (a.metric == kCosine) {
+    // cosine by factors: fp32 rows only
+    if constexpr (F16) {
+      return hipErrorInvalidValue;
+    } else {
+      if (!a.bnorm || !a.qnorm) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((deep_kernel<T, false, F16, RS, false, true>), grid, dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   if (a.metric == kL2)
     hipLaunchKernelGGL((deep_kernel<T, true, F16, RS>), grid, dim3(256), 0, s, a);
   else

@@ -91,6 +91,11 @@ struct FusedArgs {
   // word-aligned rows of words per query, launch_filter_rows).
   const uint32_t* allow;
   int64_t allow_stride;
+  // Cosine by factors (deep kernel, fp32 rows, metric kCosine): bnorm holds
+  // |b|^2 of the rows and qnorm |q|^2 of the queries, and each score is the
+  // rows' dot product times 1 / max(|b|, 1e-30) and 1 / max(|q|, 1e-30), the
+  // factors the reference's unit rows divide by (src/knn.cpp:30-33)
+  const float* qnorm;
 };
 hipError_t launch_fused_f32(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused_f16(const FusedArgs& a, hipStream_t s);
