@@ -152,33 +152,57 @@ constexpr int kBitsRows = kDeepRows;
 // puts the 16 rows a quarter-wavefront reads (16-byte reads) on distinct banks
 constexpr int kBitsStride = 20;
 
-// One code word -> 32 e2m1 nibbles of value 0 or 1.0 (code 0x2): dword m
-// holds bits 4 j + m of the word in its nibbles j.  Rows and queries use the
-// same order, so the dot products are those of the codes.
-__device__ __forceinline__ u32x4 unpack_word(uint32_t v) {
-  return u32x4{(v << 1) & 0x22222222u, v & 0x22222222u, (v >> 1) & 0x22222222u,
-               (v >> 2) & 0x22222222u};
+// bits_kernel's stages hold a 128-bit chunk (words i = 0 .. 3) of a row
+// bit-position-major: dword 4 m + i holds bit 4 j + m of word i in its nibble
+// j, with the bit in place -- nibble bit m for m < 3, bit 2 for m = 3 -- so
+// the e2m1 value of a set bit is 2^(m - 1) (0.5, 1, 2) and 2 for m = 3, one
+// shift and four masks a word (where scaling every bit to 1.0 took three
+// shifts).  MFMA step v of lane half h reads dwords 4 m .. 4 m + 3 with
+// m = 2 v + h, and the lane's block scale for the A operand, scale_of_bit(m),
+// brings them back to 1: the products and sums are those of the codes.
+__device__ __forceinline__ u32x4 unpack_bits(uint32_t v) {
+  return u32x4{v & 0x11111111u, v & 0x22222222u, v & 0x44444444u, (v >> 1) & 0x44444444u};
 }
+// E8M0 scale undoing unpack_bits' value of bit position m: 2, 1, 1/2, 1/2
+__device__ __forceinline__ int scale_of_bit(int m) { return m == 0 ? 0x80 : m == 1 ? 0x7f : 0x7e; }
 
-// Two code words at dwords 0 .. 7 of dst.
+// Words 2 p and 2 p + 1 of a chunk into a stage row (dst: the row's dword
+// 2 p): bit position m at dwords 4 m + 2 p, 4 m + 2 p + 1.
 __device__ __forceinline__ void unpack_pair(uint32_t* dst, u32x2 x) {
-  *(u32x4*)dst = unpack_word(x[0]);
-  *(u32x4*)(dst + 4) = unpack_word(x[1]);
+  const u32x4 a = unpack_bits(x[0]), b = unpack_bits(x[1]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) *(u32x2*)(dst + 4 * m) = u32x2{a[m], b[m]};
 }
 
-// A query word in the same order: nibble code 0x1 (+0.5) for a set bit,
-// 0x9 (-0.5) for a clear one.
+// A query word for stream_bits_kernel: dword m holds bits 4 j + m of the
+// word in its nibbles j, code 0x1 (+0.5) for a set bit, 0x9 (-0.5) for a
+// clear one (the rows' bits there are all 1.0).
 __device__ __forceinline__ u32x4 unpack_qword(uint32_t v) {
   constexpr uint32_t m = 0x88888888u, c = 0x99999999u;
   return u32x4{c ^ ((v << 3) & m), c ^ ((v << 2) & m), c ^ ((v << 1) & m), c ^ (v & m)};
 }
 
-// A 128-bit chunk (four words) at dwords 0 .. 15 of dst: word w at 4 w
-// (Q: query nibbles).
+// Bit 4 j + m of a query word as nibble j: code 0x1 (+0.5) for a set bit,
+// 0x9 (-0.5) for a clear one (scale 1).
+__device__ __forceinline__ uint32_t query_bits(uint32_t v, int m) {
+  return 0x99999999u ^ ((v << (3 - m)) & 0x88888888u);
+}
+
+// A 128-bit chunk (four words) at dwords 0 .. 15 of dst, bit-position-major
+// as unpack_bits lays out a stage row (Q: query nibbles in the same order).
 template <bool Q = false>
 __device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
+  if constexpr (Q) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) *(u32x4*)(dst + 4 * w) = Q ? unpack_qword(x[w]) : unpack_word(x[w]);
+    for (int m = 0; m < 4; ++m)
+      *(u32x4*)(dst + 4 * m) = u32x4{query_bits(x[0], m), query_bits(x[1], m),
+                                     query_bits(x[2], m), query_bits(x[3], m)};
+  } else {
+    const u32x4 a = unpack_bits(x[0]), b = unpack_bits(x[1]), c = unpack_bits(x[2]),
+                d = unpack_bits(x[3]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) *(u32x4*)(dst + 4 * m) = u32x4{a[m], b[m], c[m], d[m]};
+  }
 }
 
 // QREG (codes of up to 128 bytes): each lane holds its query's B fragments
@@ -231,15 +255,26 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const char*)a.queries + (int64_t)qb0 * ldb), (short)0, qrows * ldb, 0x00020000);
 
-  // QREG: MFMA step v of chunk c takes, in lane half h, code word 4 c + 2 v + h
+  // QREG: MFMA step v of chunk c takes, in lane half h, bit position
+  // m = 2 v + h of the chunk's four words (unpack_bits)
   u32x4 qf[QREG ? NCT : 1][2];
   if constexpr (QREG) {
     const uint32_t* qr = (const uint32_t*)((const char*)a.queries + (int64_t)(qvalid ? q : 0) * ldb);
 #pragma unroll
-    for (int c = 0; c < NCT; ++c)
+    for (int c = 0; c < NCT; ++c) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (qvalid) w = *(const u32x4*)(qr + 4 * c);
 #pragma unroll
-      for (int v = 0; v < 2; ++v) qf[c][v] = unpack_qword(qvalid ? qr[4 * c + 2 * v + h] : 0u);
+      for (int v = 0; v < 2; ++v) {
+        const int m = 2 * v + h;
+        qf[c][v] = u32x4{query_bits(w[0], m), query_bits(w[1], m), query_bits(w[2], m),
+                         query_bits(w[3], m)};
+      }
+    }
   }
+  // the A operand's block scales of the two steps of a chunk (bit positions
+  // h and 2 + h)
+  const int sa[2] = {scale_of_bit(h), scale_of_bit(2 + h)};
 
   // The thread's fetch: QREG, words 2 p .. 2 p + 1 of each chunk of row
   // idx; otherwise the whole row idx (wavefronts 0-1) or query idx (2-3).
@@ -247,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   const int idx = tid & 127;
   const bool row_role = QREG || __builtin_amdgcn_readfirstlane(wave) < 2;
   const int part = QREG ? tid >> 7 : 0;
-  uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 8 * part]
+  uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 2 * part]
                              : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
   constexpr int kBuf = CPS * kChunk;  // dwords per LDS buffer
   typedef typename std::conditional<QREG, u32x2, u32x4>::type frag_t;
@@ -326,13 +361,14 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
             const i32x4 a4 = *(const i32x4*)(arow + r * 32 * kBitsStride + 8 * v);
             const i32x8 av = {a4[0], a4[1], a4[2], a4[3], 0, 0, 0, 0};
             // formats 4, 4: e2m1 A and B (only the first 4 registers are
-            // read); scales 0x7f: 2^0.  The tile's first step starts from
-            // zero (an inline constant), and the accumulators end at the
-            // half score q.b - pop(b) / 2 (the query's +-0.5 nibbles):
-            // acc[r][i] is row 32 r + 8 (i / 4) + 4 h + i % 4
+            // read); the A scale undoes the bit position's value, B's is
+            // 2^0.  The tile's first step starts from zero (an inline
+            // constant), and the accumulators end at the half score q.b -
+            // pop(b) / 2 (the query's +-0.5 nibbles): acc[r][i] is row
+            // 32 r + 8 (i / 4) + 4 h + i % 4
             const floatx16 c0 = {};
             acc[r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                av, bq, (c == 0 && v == 0) ? c0 : acc[r], 4, 4, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+                av, bq, (c == 0 && v == 0) ? c0 : acc[r], 4, 4, 0, sa[v], 0, 0x7f7f7f7f);
           }
         }
       }
