@@ -207,8 +207,13 @@ __device__ __forceinline__ void unpack_chunk(uint32_t* dst, u32x4 x) {
 
 // QREG (codes of up to 128 bytes): each lane holds its query's B fragments
 // for the whole code, unpacked once (4 registers per word, 64 for 128-byte
-// codes), and all four wavefronts fetch and unpack the tile's rows (thread t:
-// words 2 p, 2 p + 1 of every chunk of row t % 128, p = t / 128).  Longer
+// codes), and all four wavefronts fetch and unpack the tile's rows: with two
+// chunks a stage, thread t the whole chunk 2 s + p of stage s of row t % 128
+// (p = t / 128), written as four 16-byte stores at the offsets the MFMA
+// reads take, which put 16 consecutive rows on distinct bank quads (as
+// 8-byte stores of half chunks at the 80-byte row stride they conflicted:
+// the counters read 3.2e8 bank-conflict cycles per C4 launch); with one
+// chunk (16-byte codes), words 2 p, 2 p + 1 of it.  Longer
 // codes (256 bytes: 128 registers of fragments would spill) keep the
 // queries in LDS too: wavefronts 0-1 fetch and unpack the rows' chunks,
 // 2-3 the queries' (the same chunks again every tile).
@@ -226,6 +231,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   // MFMAs between barriers instead of 8
   constexpr int CPS = (QREG && NCT % 2 == 0) ? 2 : 1;
   constexpr int NST = NCT / CPS;                   // stages per tile
+  constexpr bool WHOLE = QREG && CPS == 2;         // a whole chunk per thread and stage
   constexpr int kChunk = kBitsRows * kBitsStride;  // dwords per unpacked chunk
   __shared__ __align__(16) uint32_t tA[2][CPS * kChunk];
   __shared__ __align__(16) uint32_t tQ[2][QREG ? 4 : kQueriesPerBlock * kBitsStride];
@@ -276,29 +282,36 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   // h and 2 + h)
   const int sa[2] = {scale_of_bit(h), scale_of_bit(2 + h)};
 
-  // The thread's fetch: QREG, words 2 p .. 2 p + 1 of each chunk of row
-  // idx; otherwise the whole row idx (wavefronts 0-1) or query idx (2-3).
-  // Out-of-range rows read zero.
+  // The thread's fetch: WHOLE, chunk 2 s + p of each stage s of row idx;
+  // QREG with one chunk, its words 2 p .. 2 p + 1; otherwise the whole row
+  // idx (wavefronts 0-1) or query idx (2-3).  Out-of-range rows read zero.
   const int idx = tid & 127;
   const bool row_role = QREG || __builtin_amdgcn_readfirstlane(wave) < 2;
   const int part = QREG ? tid >> 7 : 0;
-  uint32_t* const my0 = QREG ? &tA[0][idx * kBitsStride + 2 * part]
-                             : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
+  uint32_t* const my0 = WHOLE  ? &tA[0][part * kChunk + idx * kBitsStride]
+                        : QREG ? &tA[0][idx * kBitsStride + 2 * part]
+                               : (row_role ? &tA[0][idx * kBitsStride] : &tQ[0][idx * kBitsStride]);
   constexpr int kBuf = CPS * kChunk;  // dwords per LDS buffer
-  typedef typename std::conditional<QREG, u32x2, u32x4>::type frag_t;
-  frag_t pk[NCT];
+  typedef typename std::conditional<QREG && !WHOLE, u32x2, u32x4>::type frag_t;
+  // the thread's packed chunks: WHOLE, chunk 2 s + part at pk[s]
+  constexpr int NPK = WHOLE ? NST : NCT;
+  frag_t pk[NPK];
   const __amdgpu_buffer_rsrc_t rf = row_role ? rb : rq;
   // offset of the thread's fetch in the tile being fetched
-  uint32_t roff = (uint32_t)(idx * ldb + 8 * part);
+  uint32_t roff = (uint32_t)(idx * ldb + (WHOLE ? 16 : 8) * part);
   const uint32_t rstep = row_role ? (uint32_t)(kBitsRows * ldb) : 0u;
   auto fetch = [&](int c) {
-    if constexpr (QREG)
+    if constexpr (WHOLE)
+      pk[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 32 * c, 0, 0);
+    else if constexpr (QREG)
       pk[c] = __builtin_amdgcn_raw_buffer_load_b64(rf, roff + 16 * c, 0, 0);
     else
       pk[c] = __builtin_amdgcn_raw_buffer_load_b128(rf, roff + 16 * c, 0, 0);
   };
   auto unpack = [&](uint32_t* dst, frag_t x) {
-    if constexpr (QREG)
+    if constexpr (WHOLE)
+      unpack_chunk<false>(dst, x);
+    else if constexpr (QREG)
       unpack_pair(dst, x);
     else if (row_role)
       unpack_chunk<false>(dst, x);
@@ -306,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       unpack_chunk<true>(dst, x);
   };
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) fetch(c);
+  for (int c = 0; c < NPK; ++c) fetch(c);
   roff += rstep;
 
   uint32_t K[T], I[T];
@@ -327,10 +340,15 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   uint32_t pend = 0;  // slot value returned by the last publish (used a tile later)
 
   // stage 0 of tile 0, then the refetch of its chunks for tile 1
+  if constexpr (WHOLE) {
+    unpack(my0, pk[0]);
+    fetch(0);
+  } else {
 #pragma unroll
-  for (int u = 0; u < CPS; ++u) unpack(my0 + u * kChunk, pk[u]);
+    for (int u = 0; u < CPS; ++u) unpack(my0 + u * kChunk, pk[u]);
 #pragma unroll
-  for (int u = 0; u < CPS; ++u) fetch(u);
+    for (int u = 0; u < CPS; ++u) fetch(u);
+  }
   __syncthreads();
 
   floatx16 acc[4];
@@ -377,11 +395,17 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       // the other buffer, then their refetch one tile further
       const int j = ((st + 1) % NST) * CPS;
       const int nb = buf ^ 1;
+      if constexpr (WHOLE) {
+        unpack(my0 + nb * kBuf, pk[(st + 1) % NST]);
+        if (j == 0) roff += rstep;
+        fetch((st + 1) % NST);
+      } else {
 #pragma unroll
-      for (int u = 0; u < CPS; ++u) unpack(my0 + nb * kBuf + u * kChunk, pk[j + u]);
-      if (j == 0) roff += rstep;
+        for (int u = 0; u < CPS; ++u) unpack(my0 + nb * kBuf + u * kChunk, pk[j + u]);
+        if (j == 0) roff += rstep;
 #pragma unroll
-      for (int u = 0; u < CPS; ++u) fetch(j + u);
+        for (int u = 0; u < CPS; ++u) fetch(j + u);
+      }
       par ^= 1;
       __syncthreads();
     }
