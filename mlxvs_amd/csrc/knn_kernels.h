@@ -460,7 +460,7 @@ struct ScanFloatArgs {
   int nl;                   // 16-byte vectors a lane reads per row: 1, 2, 4 or 8
   int64_t rows_per_split;
   int nsplit;               // a multiple of 8
-  int k;
+  int k;                    // 1 .. 32
   uint64_t* part;           // [nq][nsplit][k] scratch
   int32_t* ids;             // [nq][k] out
   float* dists;             // [nq][k] out (may be null)

@@ -1002,11 +1002,15 @@ struct RankSource {
 };
 
 // Searches of the float scan in flight, per query slot: the workgroups that
-// have written their split's list, and the largest k-th best rank of those
-// lists; the last workgroup merges and resets both (zero when the module
-// loads; calls on a device are ordered, so one search uses them at a time).
+// have written their split's list, the largest k-th best rank of those
+// lists, and k bound slots, slot c the largest best rank of the splits
+// s with s % k == c; the last workgroup merges and resets them (zero when
+// the module loads; calls on a device are ordered, so one search uses them
+// at a time).
+constexpr int kScanSlots = 32;  // the largest k of the float scan
 __device__ uint32_t g_scan_done[kScanQueries];
 __device__ unsigned long long g_scan_bound[kScanQueries];
+__device__ unsigned long long g_scan_slot[kScanQueries][kScanSlots];
 
 // 64-bit bitonic sort across a wavefront, descending: lane i ends with the
 // i-th largest of the 64 values.
@@ -1025,13 +1029,13 @@ __device__ __forceinline__ uint64_t wave_sort_desc64(uint64_t v, int lane) {
 }
 
 // The best k of one query's split lists part[0, m) (ranks, 0: none), given
-// B, the largest of the lists' k-th best ranks (0 when no list has k): the
-// list holding B has k ranks at or above it, so the query's best k are all
-// at or above B, and only those ranks are gathered -- typically k and a
-// few more, which one wavefront sorts in registers; more than 64 go through
-// the radix select of the LDS buffer, more than the buffer holds through
-// select_rows over every rank.  Leaves the best keff in sm.buf[0, keff) in
-// the output order and returns keff.  All threads call it.
+// B, a rank that at least k of the lists' ranks reach (0 if none is known),
+// so that the query's best k are all at or above it: only those ranks are
+// gathered, which one wavefront sorts in registers when there are at most
+// 64; more go through the radix select of the LDS buffer, more than the
+// buffer holds through select_rows over every rank.  Leaves the best keff in
+// sm.buf[0, keff) in the output order and returns keff.  All threads call
+// it.
 __device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_t B,
                                  RowSelect& sm) {
   constexpr int NT = 256, PER = 16;
@@ -1142,17 +1146,20 @@ __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
   const int keff = select_rows(sc, r0, r1, a.k, sm, false);
   uint64_t* dst = a.part + ((int64_t)q * a.nsplit + split) * a.k;
   for (int i = tid; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
-  // the list's k-th best rank raises the query's bound (a list shorter than
-  // k does not bound)
+  // the query's bounds: the list's k-th best rank (a list shorter than k
+  // does not bound), and its best rank into slot split % k
   if (tid < 64) {
     const uint64_t v = (tid < a.k && keff == a.k) ? sm.buf[tid] : ~0ull;
-    uint64_t mn = v;
+    const uint64_t u = tid < keff ? sm.buf[tid] : 0ull;
+    uint64_t mn = v, mx = u;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t w = __shfl_xor(mn, o);
+      const uint64_t w = __shfl_xor(mn, o), x = __shfl_xor(mx, o);
       mn = w < mn ? w : mn;
+      mx = x > mx ? x : mx;
     }
     if (tid == 0 && keff == a.k) atomicMax(&g_scan_bound[q], (unsigned long long)mn);
+    if (tid == 0 && mx) atomicMax(&g_scan_slot[q][split % a.k], (unsigned long long)mx);
   }
   // the last of the query's workgroups to get here selects its best k:
   // every list and bound is written before its workgroup counts itself
@@ -1164,12 +1171,34 @@ __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
   if (!s_last) return;
   __threadfence();
   const int64_t m = (int64_t)a.nsplit * a.k;
-  const uint64_t B = __hip_atomic_load(&g_scan_bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Two bounds that at least k ranks reach: the largest k-th best of a
+  // list (that list's k ranks), and the smallest of the k slots (each the
+  // best rank of a split of its own class: k ranks of distinct splits; 0
+  // while a class has no rank).  On C2's rows at k = 10 the first leaves
+  // 700-1,100 ranks at or above it, the second 15-50.
+  __shared__ unsigned long long s_bound;
+  if (tid < 64) {
+    uint64_t mn = tid < a.k ? (uint64_t)__hip_atomic_load(&g_scan_slot[q][tid], __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                            : ~0ull;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t w = __shfl_xor(mn, o);
+      mn = w < mn ? w : mn;
+    }
+    if (tid == 0) {
+      const uint64_t b = __hip_atomic_load(&g_scan_bound[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_bound = b > mn ? b : mn;
+    }
+  }
+  __syncthreads();
+  const uint64_t B = s_bound;
   const int kq = merge_split_lists(a.part + (int64_t)q * m, m, a.k, B, sm);
   if (tid == 0) {
     g_scan_done[q] = 0u;
     g_scan_bound[q] = 0ull;
   }
+  if (tid < a.k) g_scan_slot[q][tid] = 0ull;
   const float qn = l2 ? s_qn : 0.0f;
   for (int i = tid; i < a.k; i += NT) {
     const uint64_t r = i < kq ? sm.buf[i] : 0ull;
@@ -1276,7 +1305,7 @@ hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s) {
 
 hipError_t launch_scan_float(const ScanFloatArgs& a, hipStream_t s) {
   if (a.nq <= 0 || a.nsplit <= 0) return hipSuccess;
-  if (a.nq > kScanQueries || a.nsplit % 8 != 0 || a.k < 1 || a.k > kMaxK ||
+  if (a.nq > kScanQueries || a.nsplit % 8 != 0 || a.k < 1 || a.k > kScanSlots ||
       a.rows_per_split <= 0 || (int64_t)a.nsplit * a.rows_per_split < a.n ||
       (a.metric != kL2 && a.metric != kInnerProduct) || a.ld * (a.f16 ? 2 : 4) != 128 * a.nl ||
       (uintptr_t)a.rows % 16 != 0 || (uintptr_t)a.queries % 16 != 0)
