@@ -91,14 +91,15 @@ void launch(hipStream_t s, const char* stage, F&& f) {
 
 void prof_collect() {
   for (auto& r : g_prof_pending) {
+    // a stage whose events did not complete is left out of the totals
     float ms = 0.0f;
-    hipEventSynchronize(r.b);
-    hipEventElapsedTime(&ms, r.a, r.b);
-    auto& t = g_prof_totals[r.name];
-    t.first += 1;
-    t.second += ms;
-    hipEventDestroy(r.a);
-    hipEventDestroy(r.b);
+    if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+      auto& t = g_prof_totals[r.name];
+      t.first += 1;
+      t.second += ms;
+    }
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
   }
   g_prof_pending.clear();
 }

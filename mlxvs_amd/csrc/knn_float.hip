@@ -182,12 +182,16 @@ __device__ __forceinline__ void load16_to_lds(__amdgpu_buffer_rsrc_t r, void* ld
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
                                            voff, 0, 0, 0);
+#else
+  (void)r, (void)lds, (void)voff;
 #endif
 }
 __device__ __forceinline__ void load4_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
                                            voff, 0, 0, 0);
+#else
+  (void)r, (void)lds, (void)voff;
 #endif
 }
 

@@ -1103,7 +1103,6 @@ __device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_
 template <int NL, bool F16>
 __global__ __launch_bounds__(256) void scan_float_kernel(ScanFloatArgs a) {
   constexpr int NT = 256;
-  constexpr int esize = F16 ? 2 : 4;
   __shared__ RowSelect sm;
   __shared__ int s_last;
   __shared__ float s_qn;
