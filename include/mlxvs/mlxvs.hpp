@@ -130,6 +130,19 @@ MLXVS_API void brute_force_knn_filtered_device(const Rows& base, const Rows& que
                                                void* stream = nullptr);
 
 /**
+ * Exact k-NN under one of cuVS's distances the fused kernels do not serve
+ * (distance_type: cuVS's DistanceType value 3, 7, 8, 9, 10, 12, 14, 15, 16,
+ * 17 or 18; metric_arg: the exponent of Lp), float32 rows, smallest
+ * distances first, lower id first among equal ones; -1 / +inf past the rows
+ * a query may return.  No C++ counterpart in the reference: its
+ * cuvs.neighbors.brute_force.search computes these in Python
+ * (python/mlxvs/cuvs/distance.py:85-151).
+ */
+MLXVS_API Neighbors pairwise_knn(const Rows& base, const Rows& queries, int k,
+                                 int distance_type, float metric_arg,
+                                 const Prefilter& filter = {}, void* stream = nullptr);
+
+/**
  * Exact Hamming k-NN of bit-packed uint8 rows [n, bytes] for bit-packed
  * queries [nq, bytes]; 1 <= k <= 256.  Replaces reference
  * include/mlxvs/mlxvs.h:775-784.

@@ -444,6 +444,36 @@ MLXVS_C_API int mlxvs_brute_force_knn_filtered_device(
     void* stream);
 
 /**
+ * Extension: exact k-NN under one of cuVS's distances that the fused
+ * kernels do not serve, for cuVS's brute_force.search: distance_type is
+ * cuVS's DistanceType value -- 3 L1 (cityblock), 7 Linf (chebyshev), 8
+ * Canberra, 9 Lp (minkowski, exponent metric_arg), 10 correlation, 12
+ * Hellinger, 14 Bray-Curtis, 15 Jensen-Shannon, 16 Hamming (the share of
+ * differing columns), 17 KL divergence, 18 Russell-Rao -- with the
+ * reference's definitions (python/mlxvs/cuvs/distance.py:85-151, which
+ * brute_force.search applies at python/mlxvs/cuvs/neighbors/brute_force.py:
+ * 118-136).  float32 host rows; 1 <= k <= 256 (any n: -1 / +inf past the
+ * rows a query may return); each query's k smallest distances, nearest
+ * first, lower id first among equal ones; filter / filter_kind as
+ * mlxvs_brute_force_knn_filtered.  No C counterpart in the reference, whose
+ * search computes these distance matrices in Python.  Waits for its stream.
+ */
+MLXVS_C_API int mlxvs_pairwise_knn(
+    const float* base,
+    int64_t n,
+    const float* queries,
+    int64_t nq,
+    int32_t d,
+    int32_t k,
+    int32_t distance_type,
+    float metric_arg,
+    const uint32_t* filter,
+    int32_t filter_kind,
+    int32_t* ids,
+    float* distances,
+    void* stream);
+
+/**
  * Releases the workspace the library keeps on the current device between
  * calls (it is grown on demand and reused).  Safe to call at any time when
  * no other call is running on that device.

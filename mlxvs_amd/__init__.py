@@ -37,6 +37,7 @@ __all__ = [
     "ivf_flat_search",
     "kmeans_predict",
     "library_path",
+    "pairwise_knn",
     "topk_merge",
     "topk_merge_device",
 ]
@@ -77,6 +78,8 @@ def _load():
                                            vp, vp, vp],
         "mlxvs_brute_force_knn_filtered_device": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_int,
                                                   vp, i32, vp, vp, vp],
+        "mlxvs_pairwise_knn": [vp, i64, vp, i64, i32, i32, i32, ctypes.c_float, vp, i32, vp, vp,
+                               vp],
         "mlxvs_hamming_knn_device": [vp, i64, vp, i64, i32, i32, vp, vp, vp],
         "mlxvs_knn_self_graph_device": [vp, i64, i32, i32, i32, ctypes.c_int, vp, vp, vp],
         "mlxvs_topk_merge": [vp, i64, i64, vp, vp, i32, i32, i32, vp, vp],
@@ -283,6 +286,62 @@ def brute_force_knn_filtered(base, queries, k, metric=Metric.l2, *, bitset=None,
     dist = np.empty((nq, max(k, 0)), dtype=np.float32)
     _check(_L().mlxvs_brute_force_knn_filtered(
         _ptr(b), n, _ptr(q), nq, b.shape[1], int(f16), k, int(m),
+        None if words is None else _ptr(words), kind, _ptr(ids), _ptr(dist), st))
+    return ids, dist
+
+
+# cuVS DistanceType values pairwise_knn computes (reference
+# python/mlxvs/cuvs/distance.py:12-32)
+PAIRWISE_DISTANCES = {
+    "l1": 3, "cityblock": 3, "chebyshev": 7, "canberra": 8, "lp": 9, "minkowski": 9,
+    "correlation": 10, "hellinger": 12, "braycurtis": 14, "jensenshannon": 15, "hamming": 16,
+    "kl_divergence": 17, "russellrao": 18,
+}
+
+
+def pairwise_knn(base, queries, k, distance, metric_arg=2.0, *, bitset=None, bitmap=None,
+                 stream=None):
+    """Exact k-NN under one of cuVS's distances the fused kernels do not
+    serve (an extension: the reference computes them in Python for
+    cuvs.neighbors.brute_force.search, python/mlxvs/cuvs/distance.py:85-151,
+    brute_force.py:118-136).
+
+    ``distance``: a name of PAIRWISE_DISTANCES or its cuVS DistanceType value;
+    ``metric_arg``: the exponent of ``"minkowski"`` / ``"lp"``.  Rows are
+    taken as float32.  ``bitset`` / ``bitmap``: as brute_force_knn_filtered.
+    Returns ``(ids int32 [nq, k], distances float32 [nq, k])``, nearest first,
+    lower id first among equal distances; -1 / +inf past the rows a query may
+    return.  ``stream``: as for brute_force_knn.
+    """
+    op = "mlxvs::pairwise_knn"
+    st = _host_stream(stream, op)
+    if isinstance(distance, str):
+        if distance not in PAIRWISE_DISTANCES:
+            raise ValueError(f"[{op}] distance {distance!r} is not one of "
+                             f"{sorted(PAIRWISE_DISTANCES)}.")
+        code = PAIRWISE_DISTANCES[distance]
+    else:
+        code = int(distance)
+    b = np.ascontiguousarray(_rows(base, "base", op), dtype=np.float32)
+    q = np.ascontiguousarray(_rows(queries, "queries", op), dtype=np.float32)
+    if b.shape[1] != q.shape[1]:
+        raise ValueError(f"[{op}] base and queries must have the same number of columns.")
+    if bitset is not None and bitmap is not None:
+        raise ValueError(f"[{op}] give a bitset or a bitmap, not both.")
+    k = int(k)
+    n, nq = b.shape[0], q.shape[0]
+    kind, words = FILTER_NONE, None
+    if bitset is not None:
+        kind, words = FILTER_BITSET, _filter_words(bitset, n, op)
+    elif bitmap is not None:
+        bm = np.asarray(bitmap)
+        if bm.dtype == np.bool_ and bm.shape != (nq, n):
+            raise ValueError(f"[{op}] a bool bitmap is [nq, n] = [{nq}, {n}].")
+        kind, words = FILTER_BITMAP, _filter_words(bm, nq * n, op)
+    ids = np.empty((nq, max(k, 0)), dtype=np.int32)
+    dist = np.empty((nq, max(k, 0)), dtype=np.float32)
+    _check(_L().mlxvs_pairwise_knn(
+        _ptr(b), n, _ptr(q), nq, b.shape[1], k, code, float(metric_arg),
         None if words is None else _ptr(words), kind, _ptr(ids), _ptr(dist), st))
     return ids, dist
 

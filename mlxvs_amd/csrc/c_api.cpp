@@ -194,6 +194,19 @@ int mlxvs_brute_force_knn_filtered_device(const void* base, int64_t n, const voi
   });
 }
 
+int mlxvs_pairwise_knn(const float* base, int64_t n, const float* queries, int64_t nq, int32_t d,
+                       int32_t k, int32_t distance_type, float metric_arg, const uint32_t* filter,
+                       int32_t filter_kind, int32_t* ids, float* distances, void* stream) {
+  return guarded([&] {
+    require(ids != nullptr, "ids must not be NULL.");
+    auto b = host_rows(base, n, d, mlxvs::Dtype::Float32);
+    auto q = host_rows(queries, nq, d, mlxvs::Dtype::Float32);
+    const mlxvs::Prefilter pf{(mlxvs::FilterKind)filter_kind, filter};
+    auto r = mlxvs::pairwise_knn(b, q, k, distance_type, metric_arg, pf, stream);
+    copy_out(r, ids, distances);
+  });
+}
+
 int mlxvs_brute_force_knn_device_noalloc(const void* base, int64_t n, const void* queries,
                                          int64_t nq, int32_t d, int32_t f16, int32_t k,
                                          mlxvs_metric metric, int32_t* ids, float* distances,

@@ -1390,6 +1390,53 @@ void brute_force_knn_filtered_device(const Rows& base, const Rows& queries, int 
   float_knn(ss, in, k, (int)metric, ids, dists);
 }
 
+Neighbors pairwise_knn(const Rows& base, const Rows& queries, int k, int distance_type,
+                       float metric_arg, const Prefilter& filter, void* stream) {
+  const char* op = "mlxvs::pairwise_knn";
+  check_rows(base, op, "base");
+  check_rows(queries, op, "queries");
+  if (base.dtype != Dtype::Float32 || queries.dtype != Dtype::Float32)
+    invalid(op, "rows must be float32.");
+  if (base.d != queries.d) invalid(op, "base and queries must have the same number of columns.");
+  if (!kern::pairwise_supported(distance_type))
+    invalid(op, "distance type " + std::to_string(distance_type) + " is not supported.");
+  if (k < 1 || k > kern::kMaxK) invalid(op, "k must be in [1, 256].");
+  const int64_t nw = filter_words(filter, base.n, queries.n, op);
+  Session ss((hipStream_t)stream);
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int64_t n = base.n, nq = queries.n;
+  const void* db = upload(ar, s, base);
+  const void* dq = upload(ar, s, queries);
+  int32_t* ids = ar.take<int32_t>((size_t)std::max<int64_t>(1, nq * k));
+  float* dists = ar.take<float>((size_t)std::max<int64_t>(1, nq * k));
+  if (nq > 0 && n == 0) {
+    launch(s, "fill", [&] { return kern::launch_fill(ids, dists, nq * k, INFINITY, s); });
+  } else if (nq > 0) {
+    // the prefilter: a bitset as it is (the same words for every query), a
+    // bitmap as word-aligned rows per query
+    const uint32_t* allow = nullptr;
+    int64_t stride = 0;
+    if (nw > 0) {
+      uint32_t* dw = ar.take<uint32_t>((size_t)nw);
+      check_hip(hipMemcpyAsync(dw, filter.words, sizeof(uint32_t) * nw, hipMemcpyHostToDevice, s),
+                "hipMemcpyAsync (prefilter)");
+      allow = dw;
+      if (filter.kind == FilterKind::Bitmap) {
+        stride = (n + 31) / 32;
+        uint32_t* rows_w = ar.take<uint32_t>((size_t)(nq * stride));
+        launch(s, "prep", [&] { return kern::launch_filter_rows(dw, nq, n, rows_w, s); });
+        allow = rows_w;
+      }
+    }
+    kern::PairwiseArgs pa{(const float*)db, (const float*)dq, n, nq, base.d, k, distance_type,
+                          metric_arg, (float)(1.0 / (double)metric_arg), allow, stride, ids,
+                          dists};
+    launch(s, "pairwise", [&] { return kern::launch_pairwise(pa, s); });
+  }
+  return download(ss, ids, dists, nq, k);
+}
+
 void brute_force_knn_device_noalloc(const Rows& base, const Rows& queries, int k,
                                     Metric metric, int32_t* ids, float* distances,
                                     void* stream) {

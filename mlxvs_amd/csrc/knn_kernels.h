@@ -418,6 +418,44 @@ struct RedoArgs {
 };
 hipError_t launch_redo(const RedoArgs& a, hipStream_t s);
 
+// Exact k-NN under cuVS's distances that no fused kernel serves (reference
+// python/mlxvs/cuvs/distance.py:85-151, used by brute_force.search,
+// python/mlxvs/cuvs/neighbors/brute_force.py:118-136): the distance type is
+// cuVS's DistanceType value.  Workgroup per query (a grid-stride loop over
+// the queries): a row per thread, fp32 in row order, selected smallest
+// first with the chunked exact select (lowest id among equal distances);
+// ids -1 and distances +inf past the rows a query may return.
+enum PairwiseMetric {
+  kPwL1 = 3,
+  kPwLinf = 7,
+  kPwCanberra = 8,
+  kPwLp = 9,
+  kPwCorrelation = 10,
+  kPwHellinger = 12,
+  kPwBrayCurtis = 14,
+  kPwJensenShannon = 15,
+  kPwHamming = 16,
+  kPwKLDivergence = 17,
+  kPwRusselRao = 18,
+};
+bool pairwise_supported(int metric);
+struct PairwiseArgs {
+  const float* base;        // [n][d]
+  const float* queries;     // [nq][d]
+  int64_t n;
+  int64_t nq;
+  int d;
+  int k;                    // 1 .. kMaxK
+  int metric;               // a PairwiseMetric
+  float p;                  // kPwLp: the exponent
+  float inv_p;              // kPwLp: 1 / p (rounded once, as the reference's 1.0 / p)
+  const uint32_t* allow;    // prefilter words, a row of allow_stride words per query (0:
+  int64_t allow_stride;     // the same words for every query), or null
+  int32_t* ids;             // [nq][k] out
+  float* dists;             // [nq][k] out
+};
+hipError_t launch_pairwise(const PairwiseArgs& a, hipStream_t s);
+
 // Exact Hamming k-NN of a few queries, HBM-bound: workgroup (split, query)
 // scores its split's rows against the query with VALU popcounts (a row per
 // thread, 16-byte loads) and selects their best k exactly (chunk bounds,

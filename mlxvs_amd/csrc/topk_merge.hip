@@ -470,6 +470,109 @@ struct HammingScorer {
   }
   __device__ __forceinline__ uint32_t key(int64_t j) const { return key_nz((*this)(j)); }
 };
+// cuVS's other distances of a query to row j, in fp32 over the columns in
+// order, as the reference defines them (python/mlxvs/cuvs/distance.py:
+// 85-151; a = the query, b = the row): L1 sum |a - b|; Linf max |a - b|;
+// Canberra sum |a - b| / (|a| + |b|), a zero denominator adding 0; Lp
+// (sum |a - b|^p)^(1 / p); correlation 1 - (d a.b - sa sb) /
+// sqrt((d saa - sa^2)(d sbb - sb^2)); Hellinger sqrt(max(1 - sqrt(a).sqrt(b),
+// 0)); Bray-Curtis sum |a - b| / sum |a + b|; Jensen-Shannon
+// sqrt(0.5 sum(-a (lm - la) - b (lm - lb))), m = (a + b) / 2, lm = log m or
+// 0 where m = 0, la = log a (log 1 where a = 0), lb alike; Hamming the share
+// of columns where a != b; KL divergence 0.5 sum a (la - lb), lb = 0 where
+// b = 0; Russell-Rao (d - a.b) / d.  Smaller is nearer: the selection key
+// is that of -distance, 0 (no candidate) for a row the prefilter leaves out.
+template <int MET>
+struct PairwiseScorer {
+  static constexpr bool kAnyRow = false;  // rows past the end must not be read
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = false;
+  const float* base;
+  const float* query;
+  int d;
+  float p, inv_p;
+  float qs, qss;                    // correlation: the query's sum and sum of squares
+  const uint32_t* allow = nullptr;  // the query's prefilter words, or null
+  __device__ __forceinline__ uint32_t key(int64_t j) const {
+    if (allow && !((allow[j >> 5] >> (j & 31)) & 1u)) return 0u;
+    return key_nz(-dist(j));
+  }
+  __device__ __forceinline__ float dist(int64_t j) const {
+    const float* b = base + j * d;
+    const float* a = query;
+    const float fd = (float)d;
+    if constexpr (MET == kPwL1) {
+      float s = 0.0f;
+      for (int c = 0; c < d; ++c) s += fabsf(a[c] - b[c]);
+      return s;
+    } else if constexpr (MET == kPwLinf) {
+      float m = 0.0f;
+      for (int c = 0; c < d; ++c) m = fmaxf(m, fabsf(a[c] - b[c]));
+      return m;
+    } else if constexpr (MET == kPwCanberra) {
+      float s = 0.0f;
+      for (int c = 0; c < d; ++c) {
+        const float add = fabsf(a[c]) + fabsf(b[c]);
+        s += add != 0.0f ? fabsf(a[c] - b[c]) / add : 0.0f;
+      }
+      return s;
+    } else if constexpr (MET == kPwLp) {
+      float s = 0.0f;
+      for (int c = 0; c < d; ++c) s += powf(fabsf(a[c] - b[c]), p);
+      return powf(s, inv_p);
+    } else if constexpr (MET == kPwCorrelation) {
+      float ab = 0.0f, sb = 0.0f, sbb = 0.0f;
+      for (int c = 0; c < d; ++c) {
+        ab += a[c] * b[c];
+        sb += b[c];
+        sbb += b[c] * b[c];
+      }
+      const float numer = fd * ab - qs * sb;
+      return 1.0f - numer / sqrtf((fd * qss - qs * qs) * (fd * sbb - sb * sb));
+    } else if constexpr (MET == kPwHellinger) {
+      float s = 0.0f;
+      for (int c = 0; c < d; ++c) s += sqrtf(a[c]) * sqrtf(b[c]);
+      return sqrtf(fmaxf(1.0f - s, 0.0f));
+    } else if constexpr (MET == kPwBrayCurtis) {
+      float num = 0.0f, den = 0.0f;
+      for (int c = 0; c < d; ++c) {
+        num += fabsf(a[c] - b[c]);
+        den += fabsf(a[c] + b[c]);
+      }
+      return num / den;
+    } else if constexpr (MET == kPwJensenShannon) {
+      float acc = 0.0f;
+      for (int c = 0; c < d; ++c) {
+        const float x = a[c], y = b[c];
+        const float m = 0.5f * (x + y);
+        const float lm = m == 0.0f ? 0.0f : logf(m);
+        const float la = logf(x == 0.0f ? 1.0f : x);
+        const float lb = logf(y == 0.0f ? 1.0f : y);
+        acc += -x * (lm - la) - y * (lm - lb);
+      }
+      return sqrtf(0.5f * acc);
+    } else if constexpr (MET == kPwHamming) {
+      int cnt = 0;
+      for (int c = 0; c < d; ++c) cnt += a[c] != b[c] ? 1 : 0;
+      return (float)cnt / fd;
+    } else if constexpr (MET == kPwKLDivergence) {
+      float acc = 0.0f;
+      for (int c = 0; c < d; ++c) {
+        const float x = a[c], y = b[c];
+        const float la = logf(x == 0.0f ? 1.0f : x);
+        const float lb = y == 0.0f ? 0.0f : logf(y);
+        acc += x * (la - lb);
+      }
+      return 0.5f * acc;
+    } else {
+      static_assert(MET == kPwRusselRao, "a PairwiseMetric");
+      float ab = 0.0f;
+      for (int c = 0; c < d; ++c) ab += a[c] * b[c];
+      return (fd - ab) / fd;
+    }
+  }
+};
+
 // IVF-Flat: the query's candidate columns, probe by probe (probe p's rows
 // from column slots[p]); fp32 rows of a multiple of 4 values, with the
 // arithmetic of the IVF VALU scan (four partial sums, then pairs), so both
@@ -750,6 +853,51 @@ __global__ __launch_bounds__(256) void redo_kernel(RedoArgs a, Scorer sc) {
       __syncthreads();  // sm is reused by the next query
     }
     __syncthreads();  // flagged and nflagged are rewritten for the next block
+  }
+}
+
+// Queries blockIdx.x, + gridDim.x, ...: each query's rows scored by
+// PairwiseScorer<MET> and selected exactly (select_rows), nearest first;
+// ids -1 and distances +inf past the rows the query may return.
+template <int MET>
+__global__ __launch_bounds__(256) void pairwise_knn_kernel(PairwiseArgs a) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  __shared__ float s_q[2];
+  const int tid = threadIdx.x;
+  const int k = a.k;
+  PairwiseScorer<MET> sc;
+  sc.base = a.base;
+  sc.d = a.d;
+  sc.p = a.p;
+  sc.inv_p = a.inv_p;
+  sc.qs = sc.qss = 0.0f;
+  for (int64_t q = blockIdx.x; q < a.nq; q += gridDim.x) {
+    sc.query = a.queries + q * a.d;
+    sc.allow = a.allow ? a.allow + q * a.allow_stride : nullptr;
+    if constexpr (MET == kPwCorrelation) {
+      if (tid == 0) {
+        float s = 0.0f, ss = 0.0f;
+        for (int c = 0; c < a.d; ++c) {
+          s += sc.query[c];
+          ss += sc.query[c] * sc.query[c];
+        }
+        s_q[0] = s;
+        s_q[1] = ss;
+      }
+      __syncthreads();
+      sc.qs = s_q[0];
+      sc.qss = s_q[1];
+    }
+    const int keff = select_rows(sc, 0, a.n, k, sm);
+    for (int i = tid; i < k; i += NT) {
+      const uint64_t r = i < keff ? sm.buf[i] : 0ull;
+      const int64_t o = q * k + i;
+      a.ids[o] = r ? id_of_rank(r) : -1;
+      a.dists[o] = r ? -score_of_key((uint32_t)(r >> 32)) : INFINITY;
+    }
+    // (sm and s_q are the next query's)
+    __syncthreads();
   }
 }
 
@@ -1282,6 +1430,46 @@ hipError_t launch_redo(const RedoArgs& a, hipStream_t s) {
     FloatScorer sc{a.base, nullptr, a.bnorm, a.ld, a.d, a.f16};
     hipLaunchKernelGGL((redo_kernel<FloatScorer>), dim3(g), dim3(256), 0, s, a, sc);
   }
+  return hipGetLastError();
+}
+
+bool pairwise_supported(int metric) {
+  switch (metric) {
+    case kPwL1: case kPwLinf: case kPwCanberra: case kPwLp: case kPwCorrelation:
+    case kPwHellinger: case kPwBrayCurtis: case kPwJensenShannon: case kPwHamming:
+    case kPwKLDivergence: case kPwRusselRao:
+      return true;
+    default:
+      return false;
+  }
+}
+
+hipError_t launch_pairwise(const PairwiseArgs& a, hipStream_t s) {
+  if (a.nq <= 0) return hipSuccess;
+  if (a.k < 1 || a.k > kMaxK || a.d < 1 || a.n < 0 || !pairwise_supported(a.metric) ||
+      (a.allow && a.allow_stride != 0 && a.allow_stride < (a.n + 31) / 32))
+    return hipErrorInvalidValue;
+  // a persistent grid: about four workgroups per CU walk the queries
+  const unsigned g = (unsigned)std::min<int64_t>(a.nq, 1024);
+#define MLXVS_PW(M)                                                                           \
+  case M:                                                                                     \
+    hipLaunchKernelGGL((pairwise_knn_kernel<M>), dim3(g), dim3(256), 0, s, a);                \
+    break;
+  switch (a.metric) {
+    MLXVS_PW(kPwL1)
+    MLXVS_PW(kPwLinf)
+    MLXVS_PW(kPwCanberra)
+    MLXVS_PW(kPwLp)
+    MLXVS_PW(kPwCorrelation)
+    MLXVS_PW(kPwHellinger)
+    MLXVS_PW(kPwBrayCurtis)
+    MLXVS_PW(kPwJensenShannon)
+    MLXVS_PW(kPwHamming)
+    MLXVS_PW(kPwKLDivergence)
+    MLXVS_PW(kPwRusselRao)
+    default: return hipErrorInvalidValue;
+  }
+#undef MLXVS_PW
   return hipGetLastError();
 }
 

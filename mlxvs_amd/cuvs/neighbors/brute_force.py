@@ -7,11 +7,19 @@ the fused k-NN (``brute_force_knn``, or ``hamming_knn`` for bit-packed rows)
 and reports cuVS's distance units.  Files are cuVS's brute-force format,
 version 0, readable by cuVS's own ``brute_force.load``.
 
-Distance types served: ``"sqeuclidean"`` (L2Expanded), ``"euclidean"`` /
-``"l2"`` (L2SqrtExpanded), ``"cosine"`` (CosineExpanded),
-``"inner_product"`` and ``"bitwise_hamming"``.  cuVS's element-wise
-pairwise metrics (cityblock, chebyshev, minkowski, ...) are evaluated
-outside a fused top-k path and are not offered: they raise ``ValueError``.
+Distance types: ``"sqeuclidean"`` (L2Expanded), ``"euclidean"`` / ``"l2"``
+(L2SqrtExpanded), ``"cosine"`` (CosineExpanded), ``"inner_product"`` and
+``"bitwise_hamming"`` run the fused kernels; L2Unexpanded and
+L2SqrtUnexpanded (by type value) too.  The others the reference's search
+computes through ``distance._pairwise`` (python/mlxvs/cuvs/distance.py:
+85-151) -- ``"cityblock"`` / ``"l1"``, ``"chebyshev"``, ``"canberra"``,
+``"minkowski"`` / ``"lp"`` (``metric_arg`` = p), ``"correlation"``,
+``"hellinger"``, ``"braycurtis"``, ``"jensenshannon"``, ``"hamming"``,
+``"kl_divergence"``, ``"russellrao"`` -- run ``pairwise_knn``: each query's
+rows scored with the metric and selected exactly on the GPU, in one
+kernel.  ``"jaccard"`` and ``"dice"`` build, and their search raises
+``ValueError``, as the reference's does.  Search returns min(k, n) columns,
+as the reference's selection does (``k = min(k, dist.shape[1])``).
 
 Prefilters (``filters.from_bitset`` / ``from_bitmap``) run inside the fused
 select (``brute_force_knn_filtered``): a row a filter leaves out never
@@ -47,16 +55,39 @@ class _Distance:
 
 # cuVS DistanceType values (cuvs/distance/distance.hpp, as the reference's
 # python/mlxvs/cuvs/distance.py:12-32 lists them)
+def _same(d):
+    return d
+
+
 _DISTANCES = (
     _Distance(0, "sqeuclidean", "l2", "squared", lambda d: np.maximum(d, 0)),
     _Distance(1, "euclidean", "l2", "squared", lambda d: np.sqrt(np.maximum(d, 0))),
     _Distance(2, "cosine", "cosine", "plain", lambda s: 1 - s),
-    _Distance(6, "inner_product", "inner_product", None, lambda s: s),
-    _Distance(20, "bitwise_hamming", None, None, lambda d: d),
+    _Distance(4, "l2_unexpanded", "l2", None, lambda d: np.maximum(d, 0)),
+    _Distance(5, "l2_sqrt_unexpanded", "l2", None, lambda d: np.sqrt(np.maximum(d, 0))),
+    _Distance(6, "inner_product", "inner_product", None, _same),
+    _Distance(20, "bitwise_hamming", None, None, _same),
+    # the reference's distance._pairwise metrics: pairwise_knn
+    _Distance(3, "cityblock", "pairwise", None, _same),
+    _Distance(7, "chebyshev", "pairwise", None, _same),
+    _Distance(8, "canberra", "pairwise", None, _same),
+    _Distance(9, "minkowski", "pairwise", None, _same),
+    _Distance(10, "correlation", "pairwise", None, _same),
+    _Distance(12, "hellinger", "pairwise", None, _same),
+    _Distance(14, "braycurtis", "pairwise", None, _same),
+    _Distance(15, "jensenshannon", "pairwise", None, _same),
+    _Distance(16, "hamming", "pairwise", None, _same),
+    _Distance(17, "kl_divergence", "pairwise", None, _same),
+    _Distance(18, "russellrao", "pairwise", None, _same),
+    # names the reference builds with but cannot search
+    _Distance(11, "jaccard", "unsupported", None, _same),
+    _Distance(19, "dice", "unsupported", None, _same),
 )
 _BY_CODE = {d.code: d for d in _DISTANCES}
-_BY_NAME = {d.name: d for d in _DISTANCES}
+_BY_NAME = {d.name: d for d in _DISTANCES if d.code not in (4, 5)}
 _BY_NAME["l2"] = _BY_CODE[1]
+_BY_NAME["l1"] = _BY_CODE[3]
+_BY_NAME["lp"] = _BY_CODE[9]
 
 FORMAT_VERSION = 0
 
@@ -124,11 +155,12 @@ def build(dataset, metric="sqeuclidean", metric_arg=2.0, resources=None) -> Inde
 
 def search(index, queries, k, neighbors=None, distances=None, resources=None,
            prefilter=None):
-    """``(distances float32 [nq, k], neighbors int64 [nq, k])`` of every query,
-    nearest first (for inner product, largest first); -1 past the rows there
-    are.  Given ``neighbors`` / ``distances`` arrays are filled and returned.
+    """``(distances float32 [nq, m], neighbors int64 [nq, m])`` of every
+    query, m = min(k, rows), nearest first (for inner product, largest
+    first); -1 past the rows a prefilter allows.  Given ``neighbors`` /
+    ``distances`` arrays are filled and returned.  k at most 256.
     """
-    from mlxvs_amd import brute_force_knn, brute_force_knn_filtered, hamming_knn
+    from mlxvs_amd import brute_force_knn, brute_force_knn_filtered, hamming_knn, pairwise_knn
 
     if not getattr(index, "trained", False):
         raise ValueError("search needs a built index (see brute_force.build)")
@@ -136,8 +168,21 @@ def search(index, queries, k, neighbors=None, distances=None, resources=None,
     if kind not in ("none", "bitset", "bitmap"):
         raise ValueError(f"prefilter must come from cuvs.neighbors.filters, got {prefilter!r}")
     dist = index._distance
+    if dist.engine == "unsupported":
+        raise ValueError(f"metric {dist.name} is not supported")
     q = np.asarray(queries)
-    if kind != "none":
+    n = len(index)
+    # the reference selects min(k, n) per query (its select_k)
+    k = min(int(k), n)
+    if k <= 0:
+        out = np.zeros((q.shape[0], 0), dtype=np.float32)
+        ids = np.zeros((q.shape[0], 0), dtype=np.int64)
+    elif dist.engine == "pairwise":
+        fkw = {} if kind == "none" else {kind: np.asarray(prefilter.array, dtype=np.uint32)}
+        ids, out = pairwise_knn(index._rows, q, k, dist.code, index._metric_arg, **fkw)
+        # as the reference's pairwise branch: an infinite distance is no neighbor
+        ids[np.isinf(out)] = -1
+    elif kind != "none":
         words = np.asarray(prefilter.array, dtype=np.uint32)
         fkw = {kind: words}
         if dist.engine is None:

@@ -270,3 +270,84 @@ def recall(ids, scores, k, tol=1e-4):
     got = np.take_along_axis(scores, np.maximum(ids[:, :keff], 0), axis=1)
     hit = (got >= kth - tol * np.maximum(1.0, np.abs(kth))) & ok
     return hit.sum() / (ids.shape[0] * keff)
+
+
+# ---- cuVS's other distances (test infrastructure: float64 restatement) -------------
+#
+# The reference's brute_force.search computes these through
+# python/mlxvs/cuvs/distance.py:_pairwise (lines 154-168), with the
+# expanded forms of _dot_metric (lines 90-118) and the element-wise ones of
+# _elementwise (lines 121-151); a = the query, b = the row.  Restated here
+# in float64, one query at a time; pinned in tests/test_oracle.py against
+# scipy.spatial.distance.cdist, scipy.special.rel_entr and identities that
+# a different formula gives.
+
+PAIRWISE_CODES = {"cityblock": 3, "l1": 3, "chebyshev": 7, "canberra": 8, "minkowski": 9,
+                  "lp": 9, "correlation": 10, "hellinger": 12, "braycurtis": 14,
+                  "jensenshannon": 15, "hamming": 16, "kl_divergence": 17, "russellrao": 18}
+
+
+def pairwise_distances(queries, rows, metric, p=2.0):
+    """float64 [nq, n] distances of the reference's definitions."""
+    t = PAIRWISE_CODES[metric] if isinstance(metric, str) else int(metric)
+    x = np.asarray(queries, dtype=np.float64)
+    y = np.asarray(rows, dtype=np.float64)
+    d = x.shape[1]
+    if t == 10:  # distance.py:105-111
+        sx, sy = x.sum(1)[:, None], y.sum(1)[None]
+        sx2, sy2 = (x * x).sum(1)[:, None], (y * y).sum(1)[None]
+        numer = d * (x @ y.T) - sx * sy
+        return 1 - numer / np.sqrt((d * sx2 - sx * sx) * (d * sy2 - sy * sy))
+    if t == 12:  # distance.py:112-114
+        return np.sqrt(np.maximum(1 - np.sqrt(x) @ np.sqrt(y).T, 0))
+    if t == 18:  # distance.py:115-116
+        return (d - x @ y.T) / d
+    out = np.empty((x.shape[0], y.shape[0]))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        for i, a in enumerate(x):
+            a = a[None, :]
+            if t == 3:
+                out[i] = np.abs(a - y).sum(1)
+            elif t == 7:
+                out[i] = np.abs(a - y).max(1)
+            elif t == 8:
+                add = np.abs(a) + np.abs(y)
+                out[i] = np.where(add != 0, np.abs(a - y) / np.where(add == 0, 1, add), 0).sum(1)
+            elif t == 9:
+                out[i] = (np.abs(a - y) ** p).sum(1) ** (1.0 / p)
+            elif t == 14:
+                out[i] = np.abs(a - y).sum(1) / np.abs(a + y).sum(1)
+            elif t == 15:
+                m = 0.5 * (a + y)
+                lm = np.where(m == 0, 0, np.log(np.where(m == 0, 1, m)))
+                la = np.log(np.where(a == 0, 1, a))
+                lb = np.log(np.where(y == 0, 1, y))
+                out[i] = np.sqrt(0.5 * (-a * (lm - la) - y * (lm - lb)).sum(1))
+            elif t == 16:
+                out[i] = (a != y).mean(1)
+            elif t == 17:
+                la = np.log(np.where(a == 0, 1, a))
+                lb = np.where(y == 0, 0, np.log(np.where(y == 0, 1, y)))
+                out[i] = 0.5 * (a * (la - lb)).sum(1)
+            else:
+                raise ValueError(f"distance type {t} is not one of the pairwise ones")
+    return out
+
+
+def pairwise_knn(queries, rows, k, metric, p=2.0, allowed=None):
+    """(ids int64 [nq, k], distances float64 [nq, k]): the k smallest
+    distances, lowest id first among equal ones, rows outside ``allowed`` (a
+    bool [n] or [nq, n] mask) left out, -1 / +inf past the rows there are."""
+    dist = pairwise_distances(queries, rows, metric, p)
+    nq, n = dist.shape
+    if allowed is not None:
+        dist = np.where(np.broadcast_to(np.asarray(allowed, bool), dist.shape), dist, np.inf)
+    ids = np.full((nq, k), -1, np.int64)
+    out = np.full((nq, k), np.inf)
+    col = np.arange(n)
+    for i in range(nq):
+        order = np.lexsort((col, dist[i]))[:k]
+        order = order[~np.isinf(dist[i, order])]  # left out (or infinitely far): -1
+        ids[i, :len(order)] = order
+        out[i, :len(order)] = dist[i, order]
+    return ids, out

@@ -182,7 +182,12 @@ def test_brute_force_file_float16_and_hamming(tmp_path):
 def test_brute_force_errors(tmp_path):
     x = np.zeros((4, 3), np.float32)
     with pytest.raises(ValueError, match="not supported"):
-        brute_force.build(x, "cityblock")
+        brute_force.build(x, "manhattan")
+    # the reference builds with these names, and its search refuses them
+    # (python/mlxvs/cuvs/distance.py:151)
+    for name in ("jaccard", "dice"):
+        with pytest.raises(ValueError, match=f"metric {name} is not supported"):
+            brute_force.search(brute_force.build(x, name), x, 1)
     with pytest.raises(ValueError, match="matrix"):
         brute_force.build(np.zeros(3, np.float32))
     with pytest.raises(ValueError, match="uint8"):
@@ -276,3 +281,30 @@ def test_filtered_argument_checks():
         mlxvs_amd.brute_force_knn_filtered(x, x, 1, bitset=np.ones(1, np.uint32))
     with pytest.raises(ValueError, match=r"\[40, 40\]"):
         mlxvs_amd.brute_force_knn_filtered(x, x, 1, bitmap=np.ones((40, 39), bool))
+
+
+def test_pairwise_argument_checks():
+    import mlxvs_amd
+
+    x = np.zeros((40, 4), np.float32)
+    with pytest.raises(ValueError, match="not one of"):
+        mlxvs_amd.pairwise_knn(x, x, 1, "manhattan")
+    with pytest.raises(ValueError, match="not both"):
+        mlxvs_amd.pairwise_knn(x, x, 1, "cityblock", bitset=np.ones(40, bool),
+                               bitmap=np.ones((40, 40), bool))
+    with pytest.raises(ValueError, match="columns"):
+        mlxvs_amd.pairwise_knn(x, np.zeros((3, 5), np.float32), 1, "chebyshev")
+    # checked by the engine before any device work
+    with pytest.raises(ValueError, match="distance type 11 is not supported"):
+        mlxvs_amd.pairwise_knn(x, x, 1, 11)
+    with pytest.raises(ValueError, match=r"k must be in \[1, 256\]"):
+        mlxvs_amd.pairwise_knn(x, x, 257, "cityblock")
+    # the cuVS names the search routes here
+    from mlxvs_amd.cuvs.neighbors import brute_force
+
+    for name, code in (("cityblock", 3), ("l1", 3), ("chebyshev", 7), ("canberra", 8),
+                       ("minkowski", 9), ("lp", 9), ("correlation", 10), ("hellinger", 12),
+                       ("braycurtis", 14), ("jensenshannon", 15), ("hamming", 16),
+                       ("kl_divergence", 17), ("russellrao", 18)):
+        assert brute_force.build(x, name).distance_type == code
+        assert mlxvs_amd.PAIRWISE_DISTANCES[name] == code

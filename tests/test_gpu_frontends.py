@@ -96,13 +96,17 @@ def test_nearest_neighbors_self():
 
 # ---- cuVS brute force (reference python/tests/test_cuvs.py:147-193, 777-794) -----------
 
-@pytest.mark.parametrize("metric", ["euclidean", "sqeuclidean", "cosine", "inner_product"])
+@pytest.mark.parametrize("metric", ["euclidean", "cityblock", "chebyshev", "canberra",
+                                    "correlation", "russellrao", "cosine", "sqeuclidean",
+                                    "inner_product"])
 @pytest.mark.parametrize("inplace", [True, False])
 @pytest.mark.parametrize("serialize", [True, False])
 def test_cuvs_brute_force(tmp_path, metric, inplace, serialize):
     rng = np.random.default_rng(3)
     index = rng.random((100, 40)).astype(np.float32)
     queries = rng.random((32, 40)).astype(np.float32)
+    if metric == "russellrao":
+        index, queries = (index >= 0.5).astype(np.float32), (queries >= 0.5).astype(np.float32)
     k = 5
     neighbors = np.zeros((32, k), np.int64)
     distances = np.zeros((32, k), np.float32)
@@ -146,11 +150,15 @@ def test_cuvs_bitwise_hamming(tmp_path, nbytes):
     np.testing.assert_array_equal(np.take_along_axis(_hamming(queries, data), i, 1), want)
 
 
-def test_cuvs_padding_when_k_exceeds_rows():
+def test_cuvs_k_exceeding_rows():
+    # the reference selects min(k, n) per query (brute_force.py:113-136 with
+    # _common.py:70-71): three rows, k = 5 -> three columns, for the fused
+    # and the pairwise metrics alike
     x = rows(3, 8, 1)
-    d, i = brute_force.search(brute_force.build(x, "euclidean"), rows(2, 8, 2), 5)
-    assert (i[:, 3:] == -1).all() and np.isinf(d[:, 3:]).all()
-    assert sorted(i[0, :3].tolist()) == [0, 1, 2]
+    for metric in ("euclidean", "chebyshev"):
+        d, i = brute_force.search(brute_force.build(x, metric), rows(2, 8, 2), 5)
+        assert d.shape == (2, 3) and i.shape == (2, 3)
+        assert sorted(i[0].tolist()) == [0, 1, 2] and np.isfinite(d).all()
 
 
 # ---- .ivecs ground truth (reference examples/ground_truth.py) --------------------------

@@ -480,3 +480,79 @@ def test_filtered_limits(oracle):
     assert w.dtype == np.uint32 and len(w) == 2
     assert w[0] == sum(1 << i for i in range(0, 32, 3))
     assert w[1] == sum(1 << (i - 32) for i in range(33, 40, 3))
+
+
+# ---- cuVS's other distances (oracle.pairwise_distances / pairwise_knn) ----------------
+
+@pytest.mark.parametrize("metric,kw", [("cityblock", {}), ("chebyshev", {}), ("canberra", {}),
+                                       ("minkowski", {"p": 3.0}), ("minkowski", {"p": 1.5}),
+                                       ("correlation", {}), ("braycurtis", {}),
+                                       ("hamming", {})])
+def test_pairwise_matches_scipy(oracle, metric, kw):
+    from scipy.spatial.distance import cdist
+
+    rng = np.random.default_rng(31)
+    # small integers: equal columns (hamming) and zero pairs (canberra's 0 / 0)
+    q = rng.integers(0, 4, (9, 13)).astype(np.float32)
+    b = rng.integers(0, 4, (40, 13)).astype(np.float32)
+    q[0] = b[5]
+    if metric == "correlation":
+        q += rng.random(q.shape).astype(np.float32)  # no constant rows
+        b += rng.random(b.shape).astype(np.float32)
+    got = oracle.pairwise_distances(q, b, metric, kw.get("p", 2.0))
+    want = cdist(q.astype(np.float64), b.astype(np.float64), metric, **kw)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_pairwise_russellrao_jensenshannon_kl_hellinger(oracle):
+    from scipy.spatial.distance import cdist
+    from scipy.special import rel_entr
+
+    rng = np.random.default_rng(32)
+    # Russell-Rao on {0, 1} rows: scipy's boolean definition (n - c_TT) / n
+    qb = (rng.random((6, 20)) < 0.5).astype(np.float32)
+    bb = (rng.random((30, 20)) < 0.5).astype(np.float32)
+    np.testing.assert_allclose(oracle.pairwise_distances(qb, bb, "russellrao"),
+                               cdist(qb.astype(bool), bb.astype(bool), "russellrao"), rtol=1e-12)
+    # distributions with zeros: Jensen-Shannon as scipy's (natural log)
+    q = rng.random((5, 16))
+    b = rng.random((25, 16))
+    q[:, :3] = 0
+    b[::2, 5:7] = 0
+    q /= q.sum(1, keepdims=True)
+    b /= b.sum(1, keepdims=True)
+    np.testing.assert_allclose(oracle.pairwise_distances(q, b, "jensenshannon"),
+                               cdist(q, b, "jensenshannon"), rtol=1e-10, atol=1e-12)
+    # KL: half the relative entropy where b > 0; where b = 0 the reference
+    # takes log b as 0 (a log a, not the infinite entropy)
+    bp = b + 1e-3
+    np.testing.assert_allclose(oracle.pairwise_distances(q, bp, "kl_divergence"),
+                               0.5 * rel_entr(q[:, None, :], bp[None]).sum(2), rtol=1e-10)
+    one = oracle.pairwise_distances(np.array([[0.5, 0.5]]), np.array([[1.0, 0.0]]),
+                                    "kl_divergence")
+    assert np.isclose(one[0, 0], 0.5 * (0.5 * np.log(0.5) + 0.5 * np.log(0.5)))
+    # Hellinger of distributions: 1 - sum sqrt(a b) = sum (sqrt a - sqrt b)^2 / 2
+    want = np.sqrt(0.5 * ((np.sqrt(q)[:, None, :] - np.sqrt(b)[None]) ** 2).sum(2))
+    np.testing.assert_allclose(oracle.pairwise_distances(q, b, "hellinger"), want, atol=1e-7)
+    assert np.allclose(np.diag(oracle.pairwise_distances(b[:5], b[:5], "hellinger")), 0,
+                       atol=1e-7)
+
+
+def test_pairwise_knn_selection(oracle):
+    # integer rows with many equal L1 distances: smallest first, lowest id
+    # among equal ones; prefilter masks; padding past the allowed rows
+    rng = np.random.default_rng(33)
+    b = rng.integers(0, 2, (60, 4)).astype(np.float32)
+    q = rng.integers(0, 2, (7, 4)).astype(np.float32)
+    ids, dist = oracle.pairwise_knn(q, b, 12, "cityblock")
+    full = np.abs(q[:, None, :] - b[None]).sum(2)
+    for i in range(7):
+        order = sorted(range(60), key=lambda j: (full[i, j], j))[:12]
+        assert ids[i].tolist() == order and dist[i].tolist() == full[i, order].tolist()
+    keep = np.zeros(60, bool)
+    keep[[3, 41, 59]] = True
+    ids, dist = oracle.pairwise_knn(q, b, 5, "chebyshev", allowed=keep)
+    assert (np.sort(ids[:, :3], 1) == [3, 41, 59]).all() and (ids[:, 3:] == -1).all()
+    assert np.isinf(dist[:, 3:]).all()
+    with pytest.raises(ValueError):
+        oracle.pairwise_distances(q, b, 11)
