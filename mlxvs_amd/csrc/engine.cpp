@@ -1390,6 +1390,55 @@ void brute_force_knn_filtered_device(const Rows& base, const Rows& queries, int 
   float_knn(ss, in, k, (int)metric, ids, dists);
 }
 
+namespace {
+// Rows of at most 128 columns: the split-parallel scan over rows zero-padded
+// to 32, 64 or 128 columns (each split's exact best k), then the rank merge
+// of each query's lists; wider rows (whose scan would spill registers): a
+// query per workgroup over all rows (launch_pairwise).
+void pairwise_search(Session& ss, kern::PairwiseArgs pa) {
+  Arena& ar = ss.arena();
+  hipStream_t s = ss.stream();
+  const int d = pa.d;
+  const int ld = d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : 0;
+  if (ld == 0) {
+    launch(s, "pairwise", [&] { return kern::launch_pairwise(pa, s); });
+    return;
+  }
+  const int64_t n = pa.n, nq = pa.nq;
+  if (ld != d || (uintptr_t)pa.base % 16 != 0 || (uintptr_t)pa.queries % 16 != 0) {
+    float* pb = ar.take<float>((size_t)n * ld);
+    float* pq = ar.take<float>((size_t)nq * ld);
+    kern::PrepArgs tb{pa.base, n, d, d, 0, nullptr, nullptr, pb, ld, 0};
+    kern::PrepArgs tq{pa.queries, nq, d, d, 0, nullptr, nullptr, pq, ld, 0};
+    launch(s, "prep", [&] { return kern::launch_transform(tb, s); });
+    launch(s, "prep", [&] { return kern::launch_transform(tq, s); });
+    pa.base = pb;
+    pa.queries = pq;
+  }
+  // about four workgroups per CU slot in all, splits of whole 4,096-row
+  // chunks when there are enough rows
+  const int64_t want = std::max<int64_t>(8, 4 * device_slots(1) / nq);
+  int64_t rps = std::max<int64_t>(256, (n + want - 1) / want);
+  if (rps > 2048) rps = (rps + 4095) / 4096 * 4096;
+  const int64_t nsplit = ((n + rps - 1) / rps + 7) / 8 * 8;
+  const int64_t m = nsplit * pa.k;
+  if ((rps + 4096) * 4 * ld >= (int64_t(1) << 31) || (m + 4096) * 8 >= (int64_t(1) << 31) ||
+      nsplit * nq >= (int64_t(1) << 31)) {
+    launch(s, "pairwise", [&] { return kern::launch_pairwise(pa, s); });
+    return;
+  }
+  pa.ld = ld;
+  pa.rows_per_split = rps;
+  pa.nsplit = (int)nsplit;
+  pa.part = ar.take<uint64_t>((size_t)(nq * m));
+  uint64_t* lev = ar.take<uint64_t>((size_t)std::max<int64_t>(1, kern::merge_ranks_scratch(nq, m, pa.k)));
+  launch(s, "pairwise", [&] { return kern::launch_pairwise_scan(pa, s); });
+  launch(s, "merge", [&] {
+    return kern::launch_merge_ranks(pa.part, nq, m, pa.k, lev, pa.ids, pa.dists, s);
+  });
+}
+}  // namespace
+
 Neighbors pairwise_knn(const Rows& base, const Rows& queries, int k, int distance_type,
                        float metric_arg, const Prefilter& filter, void* stream) {
   const char* op = "mlxvs::pairwise_knn";
@@ -1432,7 +1481,7 @@ Neighbors pairwise_knn(const Rows& base, const Rows& queries, int k, int distanc
     kern::PairwiseArgs pa{(const float*)db, (const float*)dq, n, nq, base.d, k, distance_type,
                           metric_arg, (float)(1.0 / (double)metric_arg), allow, stride, ids,
                           dists};
-    launch(s, "pairwise", [&] { return kern::launch_pairwise(pa, s); });
+    pairwise_search(ss, pa);
   }
   return download(ss, ids, dists, nq, k);
 }

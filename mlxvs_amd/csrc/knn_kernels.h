@@ -453,8 +453,22 @@ struct PairwiseArgs {
   int64_t allow_stride;     // the same words for every query), or null
   int32_t* ids;             // [nq][k] out
   float* dists;             // [nq][k] out
+  // launch_pairwise_scan only: rows and queries [.][ld] fp32, 16-byte
+  // aligned, zero past d, ld one of 32, 64, 128; the splits' lists
+  int ld;
+  int64_t rows_per_split;
+  int nsplit;               // a multiple of 8
+  uint64_t* part;           // [nq][nsplit][k] out
 };
 hipError_t launch_pairwise(const PairwiseArgs& a, hipStream_t s);
+// The same distances for rows of at most 128 columns, split-parallel:
+// workgroup (split, query) scores its split's rows -- eight lanes a row,
+// 16-byte loads, the lanes' partial sums met by DPP moves -- and selects
+// their best k exactly into part[q][split][k] (ranks of -distance, zero past
+// the rows there are), for launch_merge_ranks (which writes ids and
+// distances).  The queries of a split run on one XCD (id % 8) and share its
+// rows in L2.
+hipError_t launch_pairwise_scan(const PairwiseArgs& a, hipStream_t s);
 
 // Exact Hamming k-NN of a few queries, HBM-bound: workgroup (split, query)
 // scores its split's rows against the query with VALU popcounts (a row per

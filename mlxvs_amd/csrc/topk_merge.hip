@@ -1135,6 +1135,176 @@ struct FloatChunkScorer {
   }
 };
 
+// The maximum of x over each aligned group of eight lanes (dpp_sum8's moves).
+__device__ __forceinline__ float dpp_max8(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true)));
+  return x;
+}
+
+// PairwiseScorer's distances for the chunked select of a split (fp32 rows of
+// 128 NL bytes, zero past d: every metric here adds nothing for a column
+// that is zero in both), laid out as FloatChunkScorer lays its rows: eight
+// lanes a row, lane j taking the row's 16-byte vectors j + 8 u and the
+// query's matching elements (in registers, with the per-element terms of
+// the query that some metrics need: sqrt a for Hellinger, log a for
+// Jensen-Shannon and KL); each lane's partial sums (up to three) meet by
+// DPP moves, in the order rank() uses for a single row.
+template <int NL, int MET>
+struct MetricChunkScorer {
+  static constexpr bool kAnyRow = true;
+  static constexpr bool kRanks = false;
+  static constexpr bool kChunk = true;
+  static constexpr int G = 8;        // lanes a row
+  static constexpr int R = 64 / G;   // rows a load instruction covers
+  static constexpr int NA = MET == kPwCorrelation ? 3 : (MET == kPwBrayCurtis ? 2 : 1);
+  static constexpr bool AUX = MET == kPwHellinger || MET == kPwJensenShannon ||
+                              MET == kPwKLDivergence;
+  __amdgpu_buffer_rsrc_t rs;         // the split's rows (reads past them are zero)
+  int64_t r0;
+  const float* query;                // the query row (rank())
+  float qv[NL][4];                   // the lane's query elements: vectors j + 8 u
+  float qa[AUX ? NL : 1][4];         // their per-element terms
+  float fd, p, inv_p, qs, qss;
+  const uint32_t* allow = nullptr;   // the query's prefilter words, or null
+
+  __device__ __forceinline__ static float aux_of(float a) {
+    if constexpr (MET == kPwHellinger) return sqrtf(a);
+    else return logf(a == 0.0f ? 1.0f : a);
+  }
+  __device__ __forceinline__ void acc(const float (&q)[4], const float (&qx)[4], u32x4 x,
+                                      float (&A)[3]) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = q[i], b = __uint_as_float(x[i]);
+      if constexpr (MET == kPwL1) {
+        A[0] += fabsf(a - b);
+      } else if constexpr (MET == kPwLinf) {
+        A[0] = fmaxf(A[0], fabsf(a - b));
+      } else if constexpr (MET == kPwCanberra) {
+        const float add = fabsf(a) + fabsf(b);
+        A[0] += add != 0.0f ? fabsf(a - b) / add : 0.0f;
+      } else if constexpr (MET == kPwLp) {
+        A[0] += powf(fabsf(a - b), p);
+      } else if constexpr (MET == kPwCorrelation) {
+        A[0] += a * b;
+        A[1] += b;
+        A[2] += b * b;
+      } else if constexpr (MET == kPwHellinger) {
+        A[0] += qx[i] * sqrtf(b);
+      } else if constexpr (MET == kPwBrayCurtis) {
+        A[0] += fabsf(a - b);
+        A[1] += fabsf(a + b);
+      } else if constexpr (MET == kPwJensenShannon) {
+        const float m = 0.5f * (a + b);
+        const float lm = m == 0.0f ? 0.0f : logf(m);
+        const float lb = logf(b == 0.0f ? 1.0f : b);
+        A[0] += -a * (lm - qx[i]) - b * (lm - lb);
+      } else if constexpr (MET == kPwHamming) {
+        A[0] += a != b ? 1.0f : 0.0f;
+      } else if constexpr (MET == kPwKLDivergence) {
+        const float lb = b == 0.0f ? 0.0f : logf(b);
+        A[0] += a * (qx[i] - lb);
+      } else {
+        A[0] += a * b;  // Russell-Rao
+      }
+    }
+  }
+  __device__ __forceinline__ float finish(const float (&A)[3]) const {
+    if constexpr (MET == kPwL1 || MET == kPwLinf || MET == kPwCanberra) return A[0];
+    else if constexpr (MET == kPwLp) return powf(A[0], inv_p);
+    else if constexpr (MET == kPwCorrelation)
+      return 1.0f - (fd * A[0] - qs * A[1]) / sqrtf((fd * qss - qs * qs) * (fd * A[2] - A[1] * A[1]));
+    else if constexpr (MET == kPwHellinger) return sqrtf(fmaxf(1.0f - A[0], 0.0f));
+    else if constexpr (MET == kPwBrayCurtis) return A[0] / A[1];
+    else if constexpr (MET == kPwJensenShannon) return sqrtf(0.5f * A[0]);
+    else if constexpr (MET == kPwHamming) return A[0] / fd;
+    else if constexpr (MET == kPwKLDivergence) return 0.5f * A[0];
+    else return (fd - A[0]) / fd;
+  }
+  __device__ __forceinline__ uint64_t rank_of_dist(float dist, int64_t r) const {
+    if (allow && !((allow[r >> 5] >> (r & 31)) & 1u)) return 0ull;
+    return ((uint64_t)key_nz(-dist) << 32) | (uint32_t)(~(uint32_t)r);
+  }
+  __device__ __forceinline__ void chunk(int64_t c0, int64_t valid, uint32_t (&key)[16],
+                                        uint32_t (&low)[16]) const {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = lane % G, g = lane / G;
+    constexpr uint32_t rowb = 128u * NL;
+    const uint32_t base = (uint32_t)(c0 - r0 + R * w + g) * rowb + 16u * j;
+    constexpr uint32_t sstep = 4u * R * rowb;  // between a wavefront's sets
+    constexpr int NS = 16 * G;                 // sets a wavefront takes per chunk
+    constexpr int RING = (16 + NL - 1) / NL;   // sets in flight (16 loads)
+    u32x4 x[RING][NL];
+    auto issue = [&](int st) {
+#pragma unroll
+      for (int u = 0; u < NL; ++u)
+        x[st % RING][u] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + (uint32_t)st * sstep + 16u * G * u,
+                                                         0, 0));
+    };
+#pragma unroll
+    for (int st = 0; st < RING; ++st) issue(st);
+    float mine[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      u32x4 v[NL];
+#pragma unroll
+      for (int u = 0; u < NL; ++u) v[u] = x[st % RING][u];
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + RING < NS) issue(st + RING);
+      __builtin_amdgcn_sched_barrier(0);
+      float A[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < NL; ++u) acc(qv[u], qa[AUX ? u : 0], v[u], A);
+#pragma unroll
+      for (int t = 0; t < NA; ++t) A[t] = MET == kPwLinf ? dpp_max8(A[t]) : dpp_sum8(A[t]);
+      const int e = st / G, jj = st % G;
+#pragma unroll
+      for (int t = 0; t < NA; ++t) mine[t] = j == jj ? A[t] : mine[t];
+      if (jj == G - 1) {
+        const int64_t c = (int64_t)R * (4 * (e * G + j) + w) + g;  // the lane's row in the chunk
+        const uint64_t r = rank_of_dist(finish(mine), c0 + c);
+        key[e] = c < valid ? (uint32_t)(r >> 32) : 0u;
+        low[e] = (uint32_t)r;
+      }
+    }
+  }
+  // one row, with the partial sums of chunk() in its order
+  __device__ __forceinline__ uint64_t rank(int64_t r) const {
+    const uint32_t off = (uint32_t)(r - r0) * (128u * NL);
+    float P[G][3];
+#pragma unroll
+    for (int jl = 0; jl < G; ++jl) {
+      P[jl][0] = P[jl][1] = P[jl][2] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NL; ++u) {
+        const int vec = jl + G * u;
+        const u32x4 xv = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u * vec, 0, 0));
+        float qe[4], qx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qe[i] = query[4 * vec + i];
+          qx[i] = AUX ? aux_of(qe[i]) : 0.0f;
+        }
+        acc(qe, qx, xv, P[jl]);
+      }
+    }
+    float A[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      if (MET == kPwLinf)
+        A[t] = fmaxf(fmaxf(fmaxf(P[0][t], P[1][t]), fmaxf(P[2][t], P[3][t])),
+                     fmaxf(fmaxf(P[4][t], P[5][t]), fmaxf(P[6][t], P[7][t])));
+      else
+        A[t] = ((P[0][t] + P[1][t]) + (P[2][t] + P[3][t])) + ((P[4][t] + P[5][t]) + (P[6][t] + P[7][t]));
+    }
+    return rank_of_dist(finish(A), r);
+  }
+};
+
 // The per-split lists of one query as a rank source (through a buffer
 // resource: reads past the m ranks return 0, no rank).
 struct RankSource {
@@ -1411,6 +1581,65 @@ hipError_t topk_inst(TopkMergeArgs a, bool vec, hipStream_t s) {
   return hipSuccess;
 }
 
+// Workgroup (split, query) of the split-parallel pairwise search: the split's
+// exact best k by MetricChunkScorer into part[q][split][k] (unordered).
+template <int NL, int MET>
+__global__ __launch_bounds__(256) void pairwise_scan_kernel(PairwiseArgs a) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  __shared__ float s_q[2];
+  const int tid = threadIdx.x;
+  // (split, query): XCD id % 8 takes splits xcd, xcd + 8, ..., each with
+  // its nq queries in a row
+  const int64_t id = blockIdx.x, local = id >> 3;
+  const int xcd = (int)(id & 7);
+  const int split = (int)(local / a.nq) * 8 + xcd;
+  const int64_t q = local % a.nq;
+  const int64_t r0 = min(a.n, (int64_t)split * a.rows_per_split);
+  const int64_t r1 = min(a.n, r0 + a.rows_per_split);
+  constexpr int rowb = 128 * NL;
+  MetricChunkScorer<NL, MET> sc;
+  sc.rs = __builtin_amdgcn_make_buffer_rsrc((void*)((const char*)a.base + r0 * rowb), (short)0,
+                                           (int)((r1 - r0) * rowb), 0x00020000);
+  sc.r0 = r0;
+  sc.query = a.queries + q * a.ld;
+  sc.allow = a.allow ? a.allow + q * a.allow_stride : nullptr;
+  sc.fd = (float)a.d;
+  sc.p = a.p;
+  sc.inv_p = a.inv_p;
+  {
+    const int j = (tid & 63) % MetricChunkScorer<NL, MET>::G;
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc.qv[u][i] = sc.query[4 * (j + 8 * u) + i];
+        if constexpr (MetricChunkScorer<NL, MET>::AUX)
+          sc.qa[u][i] = MetricChunkScorer<NL, MET>::aux_of(sc.qv[u][i]);
+      }
+  }
+  if constexpr (MET == kPwCorrelation) {
+    if (tid == 0) {
+      float s = 0.0f, ss = 0.0f;
+      for (int c = 0; c < a.d; ++c) {
+        s += sc.query[c];
+        ss += sc.query[c] * sc.query[c];
+      }
+      s_q[0] = s;
+      s_q[1] = ss;
+    }
+    __syncthreads();
+    sc.qs = s_q[0];
+    sc.qss = s_q[1];
+  } else {
+    sc.qs = sc.qss = 0.0f;
+  }
+  // the merge takes each list as a set: no sort
+  const int keff = select_rows(sc, r0, r1, a.k, sm, false);
+  uint64_t* dst = a.part + (q * a.nsplit + split) * a.k;
+  for (int i = tid; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+}
+
 }  // namespace
 
 hipError_t launch_redo(const RedoArgs& a, hipStream_t s) {
@@ -1470,6 +1699,47 @@ hipError_t launch_pairwise(const PairwiseArgs& a, hipStream_t s) {
     default: return hipErrorInvalidValue;
   }
 #undef MLXVS_PW
+  return hipGetLastError();
+}
+
+hipError_t launch_pairwise_scan(const PairwiseArgs& a, hipStream_t s) {
+  if (a.nq <= 0 || a.nsplit <= 0) return hipSuccess;
+  if (a.k < 1 || a.k > kMaxK || a.d < 1 || a.d > a.ld || !pairwise_supported(a.metric) ||
+      a.nsplit % 8 != 0 || a.rows_per_split <= 0 || (int64_t)a.nsplit * a.rows_per_split < a.n ||
+      (a.allow && a.allow_stride != 0 && a.allow_stride < (a.n + 31) / 32) ||
+      (uintptr_t)a.base % 16 != 0 || (uintptr_t)a.queries % 16 != 0 || !a.part ||
+      (int64_t)a.nsplit * a.nq >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  // a split's rows and the chunk past them in 32-bit byte offsets
+  if ((a.rows_per_split + 4096) * 4 * (int64_t)a.ld >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(a.nsplit * a.nq));
+#define MLXVS_PWS(NL, M)                                                                      \
+  case M:                                                                                     \
+    hipLaunchKernelGGL((pairwise_scan_kernel<NL, M>), grid, dim3(256), 0, s, a);              \
+    break;
+#define MLXVS_PWS_NL(NL)                                                                      \
+  switch (a.metric) {                                                                         \
+    MLXVS_PWS(NL, kPwL1)                                                                      \
+    MLXVS_PWS(NL, kPwLinf)                                                                    \
+    MLXVS_PWS(NL, kPwCanberra)                                                                \
+    MLXVS_PWS(NL, kPwLp)                                                                      \
+    MLXVS_PWS(NL, kPwCorrelation)                                                             \
+    MLXVS_PWS(NL, kPwHellinger)                                                               \
+    MLXVS_PWS(NL, kPwBrayCurtis)                                                              \
+    MLXVS_PWS(NL, kPwJensenShannon)                                                           \
+    MLXVS_PWS(NL, kPwHamming)                                                                 \
+    MLXVS_PWS(NL, kPwKLDivergence)                                                            \
+    MLXVS_PWS(NL, kPwRusselRao)                                                               \
+    default: return hipErrorInvalidValue;                                                     \
+  }
+  switch (a.ld) {
+    case 32: MLXVS_PWS_NL(1) break;
+    case 64: MLXVS_PWS_NL(2) break;
+    case 128: MLXVS_PWS_NL(4) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef MLXVS_PWS_NL
+#undef MLXVS_PWS
   return hipGetLastError();
 }
 

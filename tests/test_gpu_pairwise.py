@@ -108,3 +108,31 @@ def test_pairwise_many_queries(engine, oracle):
     b, q = data_for("minkowski", 2_000, 2_500, 8, 11)
     ids, dist = engine.pairwise_knn(b, q, 5, "minkowski", 1.5)
     recall_check(oracle, ids, dist, b, q, 5, "minkowski", 1.5, 2e-4)
+
+
+@pytest.mark.parametrize("d", [5, 32, 64, 100, 128, 129, 200])
+@pytest.mark.parametrize("metric", ["cityblock", "chebyshev", "hamming"])
+def test_pairwise_widths_integer_bit_exact(engine, oracle, d, metric):
+    # rows of at most 128 columns take the split-parallel scan (zero-padded
+    # to 32, 64 or 128 columns unless already a multiple), wider rows a query
+    # per workgroup: both bit-exact on integer rows
+    rng = np.random.default_rng(d)
+    b = rng.integers(0, 3, (9_000, d)).astype(np.float32)
+    q = rng.integers(0, 3, (30, d)).astype(np.float32)
+    q[0] = b[4_321]
+    ids, dist = engine.pairwise_knn(b, q, 33, metric)
+    oid, odist = oracle.pairwise_knn(q, b, 33, metric)
+    assert np.array_equal(ids, oid)
+    assert np.array_equal(dist, odist.astype(np.float32))
+    # the query's own row (or an identical one with a lower id) at distance 0
+    assert dist[0, 0] == 0.0 and ids[0, 0] <= 4_321 and (b[ids[0, 0]] == q[0]).all()
+
+
+@pytest.mark.parametrize("metric", METRICS)
+def test_pairwise_wide_rows_float(engine, oracle, metric):
+    # 160 columns: the per-query kernel, every metric
+    b, q = data_for(metric, 4_000, 20, 160, 13)
+    p = 3.0 if metric == "minkowski" else 2.0
+    tol = 2e-4 if metric in ("minkowski", "jensenshannon", "kl_divergence") else 1e-4
+    ids, dist = engine.pairwise_knn(b, q, 10, metric, p)
+    recall_check(oracle, ids, dist, b, q, 10, metric, p, tol)
