@@ -661,6 +661,13 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
   const int keff = (int)(n < k ? n : k);
   if (tid == 0) sm.cnt = 0;
   uint32_t L = 1;
+  // Rows arrive in increasing id order (scorers; not rank sources, whose
+  // ids come in any order): once the candidates have been trimmed to the
+  // best k of the rows seen, a later row whose key equals the k-th's has a
+  // larger id, so a lower rank, and cannot enter -- candidates then need a
+  // key above S, a lower bound on the k-th key (equal keys of many rows
+  // otherwise refill the buffer chunk after chunk).
+  uint32_t S = 0;
   int64_t seen = 0;
   bool overflow = false;
   __syncthreads();
@@ -722,7 +729,12 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
       __syncthreads();
       for (int i = tid; i < want0; i += NT) sm.buf[i] = sm.tmp[i];
       if (tid == 0) sm.cnt = want0;
-      if (want0 == k) L = max(L, (uint32_t)((sm.st.prefix & sm.st.mask) >> 32));
+      if (want0 == k) {
+        // (the k-th rank's decided key bits, the rest zero: at most its key)
+        const uint32_t kth = (uint32_t)((sm.st.prefix & sm.st.mask) >> 32);
+        L = max(L, kth);
+        if constexpr (!Scorer::kRanks) S = max(S, kth);
+      }
       __syncthreads();
     }
     uint32_t lc = 0xffffffffu;
@@ -730,10 +742,10 @@ __device__ int select_rows(Scorer& sc, int64_t c0r, int64_t c1r, int k, RowSelec
     for (int i = 0; i < NW; ++i) lc = min(lc, sm.wbound[i]);
     L = max(L, max(lc, 1u));
     seen += valid;
-    if (__builtin_amdgcn_ballot_w64(mx >= L) != 0) {
+    if (__builtin_amdgcn_ballot_w64(mx >= L && mx > S) != 0) {
 #pragma unroll
       for (int e = 0; e < PER; ++e) {
-        const bool p = key[e] >= L;
+        const bool p = key[e] >= L && key[e] > S;
         const uint64_t b = __builtin_amdgcn_ballot_w64(p);
         if (b == 0) continue;
         const int leader = __builtin_ctzll(b);
