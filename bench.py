@@ -187,14 +187,28 @@ def cpu_baseline(w, sample: int):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: model name, family / model /
+    stepping, clock, AVX-512 or not, and the CPUs this process may use (a
+    virtualised host may report only a generic model name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = (t.strip() for t in line.split(":", 1))
+                info.setdefault(key, val)
+            if not line.strip() and info:
+                break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    parts = [info.get("model name", "unknown"),
+             f"family {info.get('cpu family', '?')} model {info.get('model', '?')} "
+             f"stepping {info.get('stepping', '?')}"]
+    if "cpu MHz" in info:
+        parts.append(f"{float(info['cpu MHz']):.0f} MHz")
+    parts.append("avx512f" if "avx512f" in info.get("flags", "").split() else "no avx512f")
+    parts.append(f"{usable} usable CPUs")
+    return ", ".join(parts)
 
 
 def host_api_ms(w, reps: int = 3):
