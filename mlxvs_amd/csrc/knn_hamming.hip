@@ -352,11 +352,29 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
   __syncthreads();
 
   floatx16 acc[4];
+  // BUF: the tile's accumulators start at -tt instead of zero, tt the
+  // lane's threshold rounded down to a multiple of 1/2 (every half score is
+  // one: the pass set can only grow) and kept below every half score
+  // (-4 ldb is their least), so they end at the exact x - tt (multiples of
+  // 1/2 below 2^15) and the pass mask is their sign bits (select_pair_buf
+  // with PRE).  cinit holds -tt in all 16 registers (a lane's accumulators
+  // are its own query's), rewritten only when some lane's tt moved.
+  float tt = 0.0f;
+  floatx16 cinit = {};
 
   int par = 0;  // LDS buffer of the current chunk
   for (int t = 0; t < ntiles; ++t) {
     SharedBound<S> seen;
     seen.clear();
+    if constexpr (BUF) {
+      const float nt = fmaxf(floorf(2.0f * thr) * 0.5f, -4.0f * (float)ldb - 1.0f);
+      if (__builtin_amdgcn_ballot_w64(nt != tt) != 0) {
+        tt = nt;
+        const float c = -nt + 0.0f;  // +0, not -0, for a zero threshold
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cinit[i] = c;
+      }
+    }
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       if (st == 0 && share) seen.load(gk, a.mslots);
@@ -386,7 +404,8 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
             // 32 r + 8 (i / 4) + 4 h + i % 4
             const floatx16 c0 = {};
             acc[r] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                av, bq, (c == 0 && v == 0) ? c0 : acc[r], 4, 4, 0, sa[v], 0, 0x7f7f7f7f);
+                av, bq, (c == 0 && v == 0) ? (BUF ? cinit : c0) : acc[r], 4, 4, 0, sa[v], 0,
+                0x7f7f7f7f);
           }
         }
       }
@@ -421,15 +440,16 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
       if constexpr (BUF) {
 #pragma unroll
         for (int r = 0; r < 4; r += 2) {
-          // half scores (all integers / 2 below 2^23: exact)
+          // half scores less tt (all integers / 2 below 2^15: exact)
           float sc0[16], sc1[16];
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             sc0[i] = acc[r][i];
             sc1[i] = acc[r + 1][i];
           }
-          inserted |= select_pair_buf<T, true, CB, 256>(K, I, thr, sc0, sc1, h, id0 + 32 * r,
-                                                        lim0 - 32 * r, cb);
+          inserted |= select_pair_buf<T, true, CB, 256, true>(K, I, thr, sc0, sc1, h,
+                                                              id0 + 32 * r, lim0 - 32 * r, cb,
+                                                              0xffffffffu, tt);
         }
       } else {
 #pragma unroll

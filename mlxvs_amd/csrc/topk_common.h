@@ -321,22 +321,29 @@ __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], fl
 // took place), which is when the lane's shared-bound key may have risen.
 // allowm: the positions a prefilter allows (block 0 in bits 0-15, block 1
 // in 16-31), all by default.
-template <int T, bool HALF, int B, int S>
+// PRE: the caller's accumulators already subtracted a threshold t <= thr
+// (sc = x - t, exact): the mask is the sign bits of sc themselves, and a
+// passing score is stored as sc + t (off = t) -- one instruction a position
+// for the mask instead of two.
+template <int T, bool HALF, int B, int S, bool PRE = false>
 __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                                 const float (&sc0)[16], const float (&sc1)[16],
                                                 int h, uint32_t id0, int lim, CandBuf<B, S>& cb,
-                                                uint32_t allowm = 0xffffffffu) {
+                                                uint32_t allowm = 0xffffffffu, float off = 0.0f) {
   // (no max tree and vote first: some lane passes in almost every pair of
   // blocks of a list of 16, so the mask is built anyway)
   // the failing positions: the sign of x - thr (x >= thr gives +0 or more),
   // shifted in one per funnel shift, position i ending at bit i.  thr must
   // be a number or -inf here (no NaN): -inf passes everything, and inf - inf
   // is the positive default NaN
+  const float sub = PRE ? 0.0f : thr;
   uint32_t fm = 0;
 #pragma unroll
-  for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc1[i] - thr), 31);
+  for (int i = 15; i >= 0; --i)
+    fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(PRE ? sc1[i] : sc1[i] - sub), 31);
 #pragma unroll
-  for (int i = 15; i >= 0; --i) fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(sc0[i] - thr), 31);
+  for (int i = 15; i >= 0; --i)
+    fm = __builtin_amdgcn_alignbit(fm, __float_as_uint(PRE ? sc0[i] : sc0[i] - sub), 31);
   uint32_t pm = ~fm & allowm;
   if (lim < 64) pm &= real_rows(h, lim) | (real_rows(h, lim - 32) << 16);
   bool flushed = false;
@@ -349,7 +356,7 @@ __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[
     }
     if (pm) {
       const int i = __builtin_ctz(pm);
-      const float x = pick32(sc0, sc1, i);
+      const float x = PRE ? pick32(sc0, sc1, i) + off : pick32(sc0, sc1, i);
       const int j = i & 15;
       const int m = (i & 16 ? 32 : 0) + 8 * (j >> 2) + 4 * h + (j & 3);
       cb.slot[S * cb.cnt] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(id0 + m);
