@@ -810,11 +810,11 @@ bool hamming_scan(Session& ss, const uint8_t* rows, int64_t n, const uint8_t* qu
   uint64_t* part = ar.take<uint64_t>((size_t)(nq * nsplit * k));
   kern::ScanBitsArgs sa{bw, qw, n, (int)nq, nv, rps, (int)nsplit, k, part};
   launch(s, "scan_bits", [&] { return kern::launch_scan_bits(sa, s); });
-  // each list holds its split's exact best k: one exact select per query
-  // over them
+  // each list holds its split's exact best k: the ranks that reach the
+  // slots' bound, then one exact select per query over them
   const int64_t m = nsplit * k;
-  uint64_t* lev = ar.take<uint64_t>((size_t)std::max<int64_t>(1, kern::merge_ranks_scratch(nq, m, k)));
-  launch(s, "merge", [&] { return kern::launch_merge_ranks(part, nq, m, k, lev, ids, dists, s); });
+  uint64_t* surv = ar.take<uint64_t>((size_t)(nq * m));
+  launch(s, "merge", [&] { return kern::launch_merge_scan_bits(part, nq, m, k, surv, ids, dists, s); });
   return true;
 }
 

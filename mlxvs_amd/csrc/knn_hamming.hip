@@ -353,12 +353,14 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
 
   floatx16 acc[4];
   // BUF: the tile's accumulators start at -tt instead of zero, tt the
-  // lane's threshold rounded down to a multiple of 1/2 (every half score is
-  // one: the pass set can only grow) and kept below every half score
-  // (-4 ldb is their least), so they end at the exact x - tt (multiples of
-  // 1/2 below 2^15) and the pass mask is their sign bits (select_pair_buf
-  // with PRE).  cinit holds -tt in all 16 registers (a lane's accumulators
-  // are its own query's), rewritten only when some lane's tt moved.
+  // lane's threshold rounded up to a multiple of 1/2 (every half score x is
+  // one, so x >= tt exactly when x >= thr: the same pass set; rounding
+  // down would pass the ties at the list's last score, which cannot enter)
+  // and kept below every half score (-4 ldb is their least), so they end at
+  // the exact x - tt (multiples of 1/2 below 2^15) and the pass mask is
+  // their sign bits (select_pair_buf with PRE).  cinit holds -tt in all 16
+  // registers (a lane's accumulators are its own query's), rewritten only
+  // when some lane's tt moved.
   float tt = 0.0f;
   floatx16 cinit = {};
 
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void bits_kernel(FusedArgs a) {
     SharedBound<S> seen;
     seen.clear();
     if constexpr (BUF) {
-      const float nt = fmaxf(floorf(2.0f * thr) * 0.5f, -4.0f * (float)ldb - 1.0f);
+      const float nt = fmaxf(ceilf(2.0f * thr) * 0.5f, -4.0f * (float)ldb - 1.0f);
       if (__builtin_amdgcn_ballot_w64(nt != tt) != 0) {
         tt = nt;
         const float c = -nt + 0.0f;  // +0, not -0, for a zero threshold

@@ -490,6 +490,15 @@ struct ScanBitsArgs {
   uint64_t* part;           // [nq][nsplit][k] out
 };
 hipError_t launch_scan_bits(const ScanBitsArgs& a, hipStream_t s);
+// The best k of each query's nsplit * k = m ranks of launch_scan_bits, as
+// Hamming results: the ranks at or above the bound of the scan's k slots
+// (the smallest of k splits' best ranks, each split of its own class s % k)
+// are gathered into surv ([nq][m] scratch) by parallel workgroups, then one
+// workgroup per query selects their best k and resets the slots.  Must
+// follow the launch_scan_bits whose lists part holds, with no other scan of
+// the device between them.
+hipError_t launch_merge_scan_bits(const uint64_t* part, int64_t nq, int64_t m, int k,
+                                  uint64_t* surv, int32_t* ids, float* dists, hipStream_t s);
 // Exact float k-NN of a few queries (at most kScanQueries), HBM-bound:
 // workgroup (split, query) scores its split's rows against the query with
 // VALU dot products -- eight lanes a row, each reading nl 16-byte vectors

@@ -321,10 +321,10 @@ __device__ __forceinline__ void flush_buf(uint32_t (&K)[T], uint32_t (&I)[T], fl
 // took place), which is when the lane's shared-bound key may have risen.
 // allowm: the positions a prefilter allows (block 0 in bits 0-15, block 1
 // in 16-31), all by default.
-// PRE: the caller's accumulators already subtracted a threshold t <= thr
-// (sc = x - t, exact): the mask is the sign bits of sc themselves, and a
-// passing score is stored as sc + t (off = t) -- one instruction a position
-// for the mask instead of two.
+// PRE: the caller's accumulators already subtracted a threshold t (sc =
+// x - t, exact; x >= t for every x >= thr): the mask is the sign bits of sc
+// themselves, and a passing score is stored as sc + t (off = t) -- one
+// instruction a position for the mask instead of two.
 template <int T, bool HALF, int B, int S, bool PRE = false>
 __device__ __forceinline__ bool select_pair_buf(uint32_t (&K)[T], uint32_t (&I)[T], float& thr,
                                                 const float (&sc0)[16], const float (&sc1)[16],

@@ -992,6 +992,16 @@ struct BitsChunkScorer {
   }
 };
 
+// The Hamming scan's bound slots and survivor counts, per query slot: slot
+// c holds the largest best rank of the splits s with s % k == c (k ranks of
+// distinct splits once every class has one, so the query's k-th best rank
+// is at least their smallest; 0 while a class has none).  scan_bits_kernel
+// fills them, filter_ranks_kernel and merge_survivors_kernel read them, and
+// merge_survivors_kernel resets them (zero when the module loads; calls on
+// a device are ordered, so one search uses them at a time).
+__device__ unsigned long long g_bits_slot[kScanQueries][kMaxK];
+__device__ uint32_t g_bits_cnt[kScanQueries];
+
 template <int NV>
 __global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
   constexpr int NT = 256;
@@ -1012,6 +1022,106 @@ __global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
   const int keff = select_rows(sc, r0, r1, a.k, sm, false);
   uint64_t* dst = a.part + ((int64_t)q * a.nsplit + split) * a.k;
   for (int i = threadIdx.x; i < a.k; i += NT) dst[i] = i < keff ? sm.buf[i] : 0ull;
+  // the split's best rank into its class's slot
+  if (threadIdx.x < 64) {
+    uint64_t mx = 0;
+    for (int i = threadIdx.x; i < keff; i += 64) mx = sm.buf[i] > mx ? sm.buf[i] : mx;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t x = __shfl_xor(mx, o);
+      mx = x > mx ? x : mx;
+    }
+    if (threadIdx.x == 0 && mx) atomicMax(&g_bits_slot[q][split % a.k], (unsigned long long)mx);
+  }
+}
+
+// The smallest of query q's k bound slots (0 while one is empty), returned
+// to every thread.  All threads call it.
+__device__ uint64_t bits_slot_bound(int q, int k) {
+  __shared__ unsigned long long s_b;
+  if (threadIdx.x < 64) {
+    uint64_t mn = ~0ull;
+    for (int i = threadIdx.x; i < k; i += 64) {
+      const uint64_t v = __hip_atomic_load(&g_bits_slot[q][i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      mn = v < mn ? v : mn;
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t x = __shfl_xor(mn, o);
+      mn = x < mn ? x : mn;
+    }
+    if (threadIdx.x == 0) s_b = mn;
+  }
+  __syncthreads();
+  return s_b;
+}
+
+// The ranks of the Hamming scan's split lists that reach the slots' bound,
+// appended to the query's survivors surv[q][0, g_bits_cnt[q]) in no
+// particular order (one counter update a wavefront).  Workgroup (q, g)
+// reads ranks [4,096 g, 4,096 g + 4,096) of part[q][0, m).
+__global__ __launch_bounds__(256) void filter_ranks_kernel(const uint64_t* part, int64_t m, int k,
+                                                           uint64_t* surv) {
+  constexpr int NT = 256, PER = 16;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  const uint64_t B = bits_slot_bound(q, k);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(part + (int64_t)q * m), (short)0, (int)(m * 8), 0x00020000);
+  const int64_t c0 = (int64_t)blockIdx.y * NT * PER;
+  // all of the thread's loads in flight at once (reads past m are zero)
+  uint64_t r[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(c0 + e * NT + tid) * 8u, 0, 0));
+    r[e] = ((uint64_t)v[1] << 32) | v[0];
+  }
+  uint64_t b[PER];
+  int tot = 0;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    b[e] = __builtin_amdgcn_ballot_w64(r[e] != 0 && r[e] >= B);
+    tot += __builtin_popcountll(b[e]);
+  }
+  if (tot == 0) return;
+  int base = 0;
+  if ((tid & 63) == 0) base = (int)atomicAdd(&g_bits_cnt[q], (uint32_t)tot);
+  base = __shfl(base, 0);
+  uint64_t* dst = surv + (int64_t)q * m;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const uint32_t lo = (uint32_t)b[e], hi = (uint32_t)(b[e] >> 32);
+    if ((b[e] >> (tid & 63)) & 1ull)
+      dst[base + (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = r[e];
+    base += __builtin_popcountll(b[e]);
+  }
+}
+
+__device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_t B,
+                                 RowSelect& sm);
+
+// The best k of query q's survivors (filter_ranks_kernel) as Hamming
+// results (ids; distances = -score; -1 / +inf past the ranks there are),
+// then the query's slots and count reset for the next search.
+__global__ __launch_bounds__(256) void merge_survivors_kernel(const uint64_t* surv, int64_t m,
+                                                              int k, int32_t* ids, float* dists) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  const uint64_t B = bits_slot_bound(q, k);
+  const int64_t c = __hip_atomic_load(&g_bits_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int kq = merge_split_lists(surv + (int64_t)q * m, c <= m ? c : m, k, B, sm);
+  // every thread read the slots and the count before the barriers above
+  if (tid < k) g_bits_slot[q][tid] = 0ull;
+  if (tid == 0) g_bits_cnt[q] = 0u;
+  for (int i = tid; i < k; i += NT) {
+    const uint64_t r = i < kq ? sm.buf[i] : 0ull;
+    const int64_t o = (int64_t)q * k + i;
+    ids[o] = r ? id_of_rank(r) : -1;
+    if (dists) dists[o] = r ? -score_of_key((uint32_t)(r >> 32)) : INFINITY;
+  }
 }
 
 // ---- exact float scan of a few queries --------------------------------------------
@@ -1832,6 +1942,21 @@ hipError_t launch_merge_ranks(const uint64_t* part, int64_t nq, int64_t m, int k
   }
   hipLaunchKernelGGL(merge_ranks_kernel, dim3((unsigned)nq, 1), dim3(256), 0, s, part, m, m, k,
                      nullptr, ids, dists);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge_scan_bits(const uint64_t* part, int64_t nq, int64_t m, int k,
+                                  uint64_t* surv, int32_t* ids, float* dists, hipStream_t s) {
+  if (nq <= 0) return hipSuccess;
+  if (nq > kScanQueries || k < 1 || k > kMaxK || m < 1 || (m + 4096) * 8 >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  const unsigned groups = (unsigned)((m + 4095) / 4096);
+  hipLaunchKernelGGL(filter_ranks_kernel, dim3((unsigned)nq, groups), dim3(256), 0, s, part, m,
+                     k, surv);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(merge_survivors_kernel, dim3((unsigned)nq), dim3(256), 0, s, surv, m, k, ids,
+                     dists);
   return hipGetLastError();
 }
 

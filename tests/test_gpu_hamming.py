@@ -185,6 +185,29 @@ def test_few_queries_scan(engine, oracle, nq, nbytes, n, k):
     assert not np.signbit(dist).any()
 
 
+@pytest.mark.parametrize("k", [10, 100])
+def test_few_queries_scan_bound_slots_reset(engine, oracle, k):
+    # the scan's bound slots (the best rank of each class of splits) persist
+    # on the device between searches and are reset by the search's merge: a
+    # search whose rows hold exact copies of its queries (every slot at the
+    # best rank there is) followed by searches of rows far from theirs, whose
+    # results a leftover bound would drop
+    rng = np.random.default_rng(k)
+    x = rng.integers(0, 256, (100_000, 64), dtype=np.uint8)
+    q = rng.integers(0, 256, (3, 64), dtype=np.uint8)
+    x[::50] = q[0]
+    ids, dist = engine.hamming_knn(x, q, k)
+    oid, odist = oracle.hamming(x, q, k)
+    assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+    assert (dist[0] == 0).all()
+    for seed in range(2):
+        y = rng.integers(0, 256, (50_000, 64), dtype=np.uint8)
+        p = (~y[:2]).copy()  # queries at distance 512 from rows 0 and 1
+        ids, dist = engine.hamming_knn(y, p, k)
+        oid, odist = oracle.hamming(y, p, k)
+        assert np.array_equal(ids, oid) and np.array_equal(dist, odist)
+
+
 @pytest.mark.parametrize("n", [1, 21, 255])
 @pytest.mark.parametrize("k", [44, 256])
 def test_few_queries_scan_under_k_rows(engine, oracle, n, k):
