@@ -53,8 +53,10 @@ constexpr int kCandCap = 4096;
 
 // State of one radix select (in LDS).  After radix_pick, the wanted ranks
 // are those with (r & mask) > prefix, and of those with (r & mask) ==
-// prefix all of them when `done`, else `need` of them (equal ranks are
-// equal (score, id) pairs, so which copies does not matter).
+// prefix all of them when done is 1, the `need` largest when done is 2
+// (at most 64 of them: radix_gather sorts them), else `need` of them (the
+// prefix is then a whole rank, and equal ranks are equal (score, id) pairs,
+// so which copies does not matter).
 struct PickState {
   uint64_t prefix;
   uint64_t mask;
@@ -62,13 +64,33 @@ struct PickState {
   int done;
   int taken;
   int tie;
+  uint64_t few[64];  // done == 2: the ranks equal to the prefix
 };
+
+// 64-bit bitonic sort across a wavefront, descending: lane i ends with the
+// i-th largest of the 64 values.
+__device__ __forceinline__ uint64_t wave_sort_desc64(uint64_t v, int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = __shfl_xor(v, stride);
+      const bool lo = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;
+      v = (lo == desc) ? (v > o ? v : o) : (v < o ? v : o);
+    }
+  }
+  return v;
+}
+
+
 
 // MSB-first radix select of the `want` largest ranks among those `visit`
 // hands to f (each thread its own), 8 bits per pass.  A pass histograms
 // the digit of the ranks still matching the prefix; wavefront 0 finds the
 // digit of the want-th largest and stops the passes once the ranks matching
-// the new prefix are exactly the ones still needed.  All threads call it.
+// the new prefix are exactly the ones still needed, or at most 64 (which
+// radix_gather sorts).  All threads call it.
 template <int NT, typename Visit>
 __device__ void radix_pick(Visit visit, int want, uint32_t* hist, PickState& st) {
   if (threadIdx.x == 0) {
@@ -121,7 +143,10 @@ __device__ void radix_pick(Visit visit, int want, uint32_t* hist, PickState& st)
         st.need = (int)(need - acc);
         st.prefix = pre | ((uint64_t)dig << sh);
         st.mask = msk | (255ull << sh);
-        st.done = cnt == need - acc ? 1 : 0;
+        // the digit's ranks all wanted, or few enough to sort (which ends
+        // the passes where ties at the k-th key would run them to the
+        // last digit)
+        st.done = cnt == need - acc ? 1 : (cnt <= 64 ? 2 : 0);
       }
     }
     __syncthreads();
@@ -129,13 +154,40 @@ __device__ void radix_pick(Visit visit, int want, uint32_t* hist, PickState& st)
   }
 }
 
-// Writes the ranks radix_pick chose into out (unordered).  Ends without a
-// barrier.
+// Writes the ranks radix_pick chose into out (unordered).  All threads call
+// it; it ends without a barrier.
 template <typename Visit>
 __device__ void radix_gather(Visit visit, PickState& st, uint64_t* out) {
   const uint64_t pre = st.prefix, msk = st.mask;
-  const bool done = st.done != 0;
+  const int mode = st.done;
+  const bool done = mode == 1;
   const int need = st.need;
+  if (mode == 2) {
+    // the ranks equal to the prefix (at most 64) into st.few, the larger
+    // ones into out; wavefront 0 sorts the few and appends their need
+    // largest, and the prefix becomes the k-th rank itself (every bit
+    // decided, as callers read it for a bound)
+    visit([&](uint64_t r) {
+      const uint64_t m = r & msk;
+      const bool take = m > pre, tied = m == pre;
+      const int t = wave_take(&st.tie, tied);
+      if (tied) st.few[t] = r;
+      const int o = wave_take(&st.taken, take);
+      if (take) out[o] = r;
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const uint64_t v = wave_sort_desc64(lane < st.tie ? st.few[lane] : 0ull, lane);
+      if (lane < need) out[st.taken + lane] = v;
+      const uint64_t kth = __shfl(v, need - 1);
+      if (lane == 0) {
+        st.prefix = kth;
+        st.mask = ~0ull;
+      }
+    }
+    return;
+  }
   visit([&](uint64_t r) {
     const uint64_t m = r & msk;
     bool take = m > pre;
@@ -1451,22 +1503,6 @@ constexpr int kScanSlots = 32;  // the largest k of the float scan
 __device__ uint32_t g_scan_done[kScanQueries];
 __device__ unsigned long long g_scan_bound[kScanQueries];
 __device__ unsigned long long g_scan_slot[kScanQueries][kScanSlots];
-
-// 64-bit bitonic sort across a wavefront, descending: lane i ends with the
-// i-th largest of the 64 values.
-__device__ __forceinline__ uint64_t wave_sort_desc64(uint64_t v, int lane) {
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t o = __shfl_xor(v, stride);
-      const bool lo = (lane & stride) == 0;
-      const bool desc = (lane & size) == 0;
-      v = (lo == desc) ? (v > o ? v : o) : (v < o ? v : o);
-    }
-  }
-  return v;
-}
 
 // The best k of one query's split lists part[0, m) (ranks, 0: none), given
 // B, a rank that at least k of the lists' ranks reach (0 if none is known),
