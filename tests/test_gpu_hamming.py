@@ -186,6 +186,18 @@ def test_few_queries_scan(engine, oracle, nq, nbytes, n, k):
 
 
 @pytest.mark.parametrize("k", [10, 100])
+def test_few_queries_scan_all_ties(engine, k):
+    # every distance 0 through the scan path (64-byte codes, three queries):
+    # at k = 10 the slots' bound leaves the first ten splits' lists, 100
+    # ranks of one key, chosen by id in the survivors' select; at k = 100
+    # there are fewer splits than slots, no bound, and all the splits'
+    # ranks (more than the select's buffer holds) go to the fallback
+    x = np.zeros((200_000, 64), np.uint8)
+    ids, dist = engine.hamming_knn(x, x[:3], k)
+    assert (ids == np.arange(k)[None, :]).all() and (dist == 0).all()
+
+
+@pytest.mark.parametrize("k", [10, 100])
 def test_few_queries_scan_bound_slots_reset(engine, oracle, k):
     # the scan's bound slots (the best rank of each class of splits) persist
     # on the device between searches and are reset by the search's merge: a
