@@ -1162,8 +1162,9 @@ __global__ __launch_bounds__(256) void merge_survivors_kernel(const uint64_t* su
   constexpr int NT = 256;
   __shared__ RowSelect sm;
   const int q = blockIdx.x, tid = threadIdx.x;
-  const uint64_t B = bits_slot_bound(q, k);
+  // (the count's load in flight with the slots')
   const int64_t c = __hip_atomic_load(&g_bits_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t B = bits_slot_bound(q, k);
   const int kq = merge_split_lists(surv + (int64_t)q * m, c <= m ? c : m, k, B, sm);
   // every thread read the slots and the count before the barriers above
   if (tid < k) g_bits_slot[q][tid] = 0ull;
@@ -1566,8 +1567,41 @@ __device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_
     radix_pick<NT>(visit, keff, sm.hist, sm.st);
     radix_gather(visit, sm.st, sm.tmp);
     __syncthreads();
-    for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
-    __syncthreads();
+    if (keff <= 128) {
+      // the picks in rank order in registers (the output order unless a -0
+      // score is among them): up to 64 by one wavefront; up to 128 by two,
+      // each sorting 64, then the half-cleaner of their bitonic merge
+      // (wavefront 0 the larger of A[l] and B[63 - l], wavefront 1 the
+      // smaller) and each wavefront's 64 merged by shuffles
+      __shared__ int s_nz;
+      const int w = tid >> 6;
+      uint64_t v = 0ull;
+      if (w < 2) {
+        v = wave_sort_desc64(tid < keff ? sm.tmp[tid] : 0ull, lane);
+        if (keff > 64) sm.buf[tid] = v;
+      }
+      if (tid == 0) s_nz = 0;
+      __syncthreads();
+      if (keff > 64 && w < 2) {
+        const uint64_t a = sm.buf[lane], b = sm.buf[127 - lane];
+        v = w == 0 ? (a > b ? a : b) : (a < b ? a : b);
+#pragma unroll
+        for (int stride = 32; stride > 0; stride >>= 1) {
+          const uint64_t o = __shfl_xor(v, stride);
+          v = (lane & stride) == 0 ? (v > o ? v : o) : (v < o ? v : o);
+        }
+      }
+      __syncthreads();
+      if (w < 2 && tid < keff) {
+        sm.buf[tid] = v;
+        if ((uint32_t)(v >> 32) == 0x7fffffffu) s_nz = 1;
+      }
+      __syncthreads();
+      if (!s_nz) return keff;
+    } else {
+      for (int i = tid; i < keff; i += NT) sm.buf[i] = sm.tmp[i];
+      __syncthreads();
+    }
   }
   const int P = pow2_at_least(keff > 1 ? keff : 1);
   for (int i = keff + tid; i < P; i += NT) sm.buf[i] = 0;
