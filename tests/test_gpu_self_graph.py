@@ -65,7 +65,8 @@ def test_c5_subset(engine, oracle):
     assert (ids[:32] == g["ids"]).mean() > 0.95
     # 1,024 strided rows (and the first 32) against float64 brute force:
     # tie-tolerant recall 1.0 with the row itself excluded, distances within
-    # 2e-3 of the exact ones (float16 storage, BASELINE bar)
+    # 2e-3 of the exact ones (the tolerance the path's north star states for
+    # float16 storage)
     sel = np.unique(np.concatenate([np.arange(32), np.arange(0, 200_000, 195)[:1024]]))
     assert sel.size >= 1024
     for c0 in range(0, sel.size, 256):
