@@ -453,9 +453,25 @@ int max_merge_segments(int k, int T) {
 // merge_kernel, from the sentinels the levels pass on.
 // The part lists are stream lists, sorted best first (the merge's sort
 // starts from the sorted runs).
+// A small batch of many lists takes the bounded merge instead
+// (launch_bound_merge: a bound from the lists' best entries, the candidates
+// at or above it gathered in parallel, then one exact select per query),
+// where the levels would each wait on a few workgroups.
 void merge_lists(Arena& ar, hipStream_t s, const uint64_t* part, int nseg, int T, int k,
                  int64_t nq, int metric, const float* qnorm, int dist_mode, int32_t* ids,
                  float* dists, int* flags) {
+  const int64_t C = (int64_t)nseg * T;
+  // (not in a fixed workspace: its survivor buffer, nq * C ranks, is larger
+  // than the levels' outputs)
+  if (!ar.fixed() && nq <= kern::kBoundMergeQueries && C > 1024 &&
+      (C + 4096) * 8 < (int64_t(1) << 31)) {
+    uint64_t* surv = ar.take<uint64_t>((size_t)(nq * C));
+    uint64_t* tails = flags ? ar.take<uint64_t>((size_t)nq * nseg) : nullptr;
+    kern::BoundMergeArgs bm{part, nseg, T, k, (int)nq, metric, qnorm, dist_mode, surv, tails,
+                            ids, dists, flags};
+    launch(s, "merge", [&] { return kern::launch_bound_merge(bm, s); });
+    return;
+  }
   const uint64_t* mpart = part;
   int mseg = nseg, mT = T;
   uint64_t* sentinel = nullptr;

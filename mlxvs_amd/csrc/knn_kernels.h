@@ -232,6 +232,35 @@ struct MergeArgs {
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
+// The merge of a small batch's many stream lists (each sorted best first):
+// k bound slots take the best entry of each class of segments (s % k), so
+// the query's k-th best rank is at least their smallest; the candidates
+// that reach it are gathered into surv by workgroups of 4,096 candidates,
+// with (flags) the segments' last entries that reach it into tails; then
+// one workgroup per query selects the best k of them exactly, flags the
+// query as merge_kernel does (a full segment whose last entry made the best
+// k) and writes the results: the same output as launch_merge over the same
+// lists, in three short launches where the merge levels of a small batch
+// each wait on a few workgroups.  At most kBoundMergeQueries queries; calls
+// on a device are ordered (the slots and counts live in device memory).
+constexpr int kBoundMergeQueries = 128;
+struct BoundMergeArgs {
+  const uint64_t* part;  // [nq][nseg][T], each list sorted best first
+  int nseg;
+  int T;
+  int k;
+  int nq;
+  int metric;            // as MergeArgs
+  const float* qnorm;
+  int dist_mode;
+  uint64_t* surv;        // [nq][nseg * T] scratch
+  uint64_t* tails;       // [nq][nseg] scratch (flags only)
+  int32_t* ids;
+  float* dists;
+  int* flags;            // [nq] or null (T >= k)
+};
+hipError_t launch_bound_merge(const BoundMergeArgs& a, hipStream_t s);
+
 // First merge level when the segments exceed what one workgroup sorts: the
 // `keep` best ranks of each group of gs consecutive segment lists (keep = T
 // when k <= T, else k <= gs T: a group's best k hold all of its members of

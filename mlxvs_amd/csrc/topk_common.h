@@ -492,19 +492,10 @@ __device__ __forceinline__ int pow2_at_least(int x) {
   return p;
 }
 
-// Writes the k best of `best` (sorted descending by rank, first k entries
-// valid, 0 = empty) to ids / dists row `orow`, in the reference's output
-// order.  `work` is LDS scratch of at least pow2(k) entries.  Distances:
-// dist_mode 0 -> L2: max(qn - s, 0) (+inf when empty); IP / cosine: s
-// (-inf when empty); dist_mode 1 -> Hamming: -s (+inf when empty).
+// emit_topk's writes for k ranks already in the output order (0 = empty).
 template <int NT>
-__device__ void emit_topk(const uint64_t* best, uint64_t* work, int k,
-                          int64_t orow, int metric, float qn, int dist_mode,
-                          int32_t* ids, float* dists) {
-  const int K2 = pow2_at_least(k);
-  for (int i = threadIdx.x; i < K2; i += NT) work[i] = i < k ? best[i] : 0;
-  __syncthreads();
-  bitonic_desc<NT>(work, K2, OutputOrder{});
+__device__ void emit_ordered(const uint64_t* work, int k, int64_t orow, int metric, float qn,
+                             int dist_mode, int32_t* ids, float* dists) {
   const bool l2 = metric == 1;
   for (int i = threadIdx.x; i < k; i += NT) {
     uint64_t r = work[i];
@@ -527,6 +518,22 @@ __device__ void emit_topk(const uint64_t* best, uint64_t* work, int k,
       }
     }
   }
+}
+
+// Writes the k best of `best` (sorted descending by rank, first k entries
+// valid, 0 = empty) to ids / dists row `orow`, in the reference's output
+// order.  `work` is LDS scratch of at least pow2(k) entries.  Distances:
+// dist_mode 0 -> L2: max(qn - s, 0) (+inf when empty); IP / cosine: s
+// (-inf when empty); dist_mode 1 -> Hamming: -s (+inf when empty).
+template <int NT>
+__device__ void emit_topk(const uint64_t* best, uint64_t* work, int k,
+                          int64_t orow, int metric, float qn, int dist_mode,
+                          int32_t* ids, float* dists) {
+  const int K2 = pow2_at_least(k);
+  for (int i = threadIdx.x; i < K2; i += NT) work[i] = i < k ? best[i] : 0;
+  __syncthreads();
+  bitonic_desc<NT>(work, K2, OutputOrder{});
+  emit_ordered<NT>(work, k, orow, metric, qn, dist_mode, ids, dists);
 }
 
 }  // namespace mlxvs::kern

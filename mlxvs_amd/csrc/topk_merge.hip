@@ -1177,6 +1177,151 @@ __global__ __launch_bounds__(256) void merge_survivors_kernel(const uint64_t* su
   }
 }
 
+// ---- bounded merge of a small batch's segment lists --------------------------------
+
+// Bound slots, survivor counts and segment-tail counts per query:
+// bound_slots_kernel fills the slots, bound_filter_kernel reads them and
+// adds to the counts, bound_merge_kernel reads and resets all three (zero
+// when the module loads; calls on a device are ordered, so one merge uses
+// them at a time).
+__device__ unsigned long long g_bm_slot[kBoundMergeQueries][kMaxK];
+__device__ uint32_t g_bm_cnt[kBoundMergeQueries];
+__device__ uint32_t g_bm_tails[kBoundMergeQueries];
+
+// The smallest of query q's k bound slots (0 while one is empty), returned
+// to every thread.  All threads call it.
+__device__ uint64_t bm_bound(int q, int k) {
+  __shared__ unsigned long long s_b;
+  if (threadIdx.x < 64) {
+    uint64_t mn = ~0ull;
+    for (int i = threadIdx.x; i < k; i += 64) {
+      const uint64_t v = __hip_atomic_load(&g_bm_slot[q][i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      mn = v < mn ? v : mn;
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t x = __shfl_xor(mn, o);
+      mn = x < mn ? x : mn;
+    }
+    if (threadIdx.x == 0) s_b = mn;
+  }
+  __syncthreads();
+  return s_b;
+}
+
+// Workgroup (q, g): the first (best) entries of segments [256 g, 256 g +
+// 256) of query q into their classes' slots, reduced in LDS first (one
+// device atomic per class and workgroup).
+__global__ __launch_bounds__(256) void bound_slots_kernel(BoundMergeArgs a) {
+  __shared__ unsigned long long ls[kMaxK];
+  const int q = blockIdx.x, tid = threadIdx.x;
+  if (tid < a.k) ls[tid] = 0ull;
+  __syncthreads();
+  const int sgm = blockIdx.y * 256 + tid;
+  if (sgm < a.nseg) {
+    const uint64_t r = a.part[((int64_t)q * a.nseg + sgm) * a.T];
+    if (r) atomicMax(&ls[sgm % a.k], (unsigned long long)r);
+  }
+  __syncthreads();
+  if (tid < a.k && ls[tid]) atomicMax(&g_bm_slot[q][tid], ls[tid]);
+}
+
+// Appends, one counter update a wavefront, the entries of b (a ballot per
+// element of r) to dst[0, *ctr).
+template <int PER>
+__device__ __forceinline__ void append_ballots(const uint64_t (&r)[PER], const uint64_t (&b)[PER],
+                                               uint32_t* ctr, uint64_t* dst) {
+  int tot = 0;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) tot += __builtin_popcountll(b[e]);
+  if (tot == 0) return;
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  if (lane == 0) base = (int)atomicAdd(ctr, (uint32_t)tot);
+  base = __shfl(base, 0);
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    if ((b[e] >> lane) & 1ull)
+      dst[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b[e] >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)b[e], 0u))] = r[e];
+    base += __builtin_popcountll(b[e]);
+  }
+}
+
+// Workgroup (q, g): candidates [4,096 g, 4,096 g + 4,096) of query q's
+// nseg * T.
+__global__ __launch_bounds__(256) void bound_filter_kernel(BoundMergeArgs a) {
+  constexpr int NT = 256, PER = 16;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  const int64_t C = (int64_t)a.nseg * a.T;
+  const uint64_t B = bm_bound(q, a.k);
+  const uint64_t* src = a.part + (int64_t)q * C;
+  const int64_t c0 = (int64_t)blockIdx.y * NT * PER;
+  uint64_t r[PER], b[PER], t[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int64_t i = c0 + e * NT + tid;
+    r[e] = i < C ? src[i] : 0ull;
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int64_t i = c0 + e * NT + tid;
+    const bool take = r[e] != 0 && r[e] >= B;
+    b[e] = __builtin_amdgcn_ballot_w64(take);
+    t[e] = __builtin_amdgcn_ballot_w64(take && a.flags && i % a.T == a.T - 1);
+  }
+  append_ballots<PER>(r, b, &g_bm_cnt[q], a.surv + (int64_t)q * C);
+  if (a.flags) append_ballots<PER>(r, t, &g_bm_tails[q], a.tails + (int64_t)q * a.nseg);
+}
+
+__global__ __launch_bounds__(256) void bound_merge_kernel(BoundMergeArgs a) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  __shared__ int s_flag;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  const int64_t C = (int64_t)a.nseg * a.T;
+  // (the counts' loads in flight with the bound's)
+  const int64_t c = __hip_atomic_load(&g_bm_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int nt = (int)__hip_atomic_load(&g_bm_tails[q], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t B = bm_bound(q, a.k);
+  const int keff = merge_split_lists(a.surv + (int64_t)q * C, c <= C ? c : C, a.k, B, sm);
+  for (int i = keff + tid; i < a.k; i += NT) sm.buf[i] = 0;
+  if (tid == 0) s_flag = 0;
+  __syncthreads();
+  // every thread read the slots and counts before the barriers above
+  if (tid < a.k) g_bm_slot[q][tid] = 0ull;
+  if (tid == 0) {
+    g_bm_cnt[q] = 0u;
+    g_bm_tails[q] = 0u;
+  }
+  if (a.flags) {
+    // the k-th best rank: the smallest of the k chosen (0 when fewer), at or
+    // above the bound, so every segment tail at or above it was kept
+    __shared__ unsigned long long s_kth;
+    if (tid < 64) {
+      uint64_t mn = ~0ull;
+      for (int i = tid; i < a.k; i += 64) mn = sm.buf[i] < mn ? sm.buf[i] : mn;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t x = __shfl_xor(mn, o);
+        mn = x < mn ? x : mn;
+      }
+      if (tid == 0) s_kth = keff < a.k ? 0ull : mn;
+    }
+    __syncthreads();
+    const uint64_t kth = s_kth;
+    const uint64_t* tl = a.tails + (int64_t)q * a.nseg;
+    for (int i = tid; i < (nt <= a.nseg ? nt : a.nseg); i += NT)
+      if (tl[i] >= kth) s_flag = 1;
+    __syncthreads();
+    if (tid == 0) a.flags[q] = s_flag;
+  }
+  const float qn = (a.metric == kL2 && a.dist_mode == 0) ? a.qnorm[q] : 0.0f;
+  emit_ordered<NT>(sm.buf, a.k, q, a.metric, qn, a.dist_mode, a.ids, a.dists);
+}
+
 // ---- exact float scan of a few queries --------------------------------------------
 
 // The sum of x over each aligned group of eight lanes, in every lane of the
@@ -2027,6 +2172,24 @@ hipError_t launch_merge_scan_bits(const uint64_t* part, int64_t nq, int64_t m, i
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(merge_survivors_kernel, dim3((unsigned)nq), dim3(256), 0, s, surv, m, k, ids,
                      dists);
+  return hipGetLastError();
+}
+
+hipError_t launch_bound_merge(const BoundMergeArgs& a, hipStream_t s) {
+  if (a.nq <= 0) return hipSuccess;
+  const int64_t C = (int64_t)a.nseg * a.T;
+  if (a.nq > kBoundMergeQueries || a.k < 1 || a.k > kMaxK || a.nseg < 1 || a.T < 1 ||
+      (C + 4096) * 8 >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(bound_slots_kernel, dim3((unsigned)a.nq, (unsigned)((a.nseg + 255) / 256)),
+                     dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const unsigned groups = (unsigned)((C + 4095) / 4096);
+  hipLaunchKernelGGL(bound_filter_kernel, dim3((unsigned)a.nq, groups), dim3(256), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(bound_merge_kernel, dim3((unsigned)a.nq), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
