@@ -453,7 +453,8 @@ int max_merge_segments(int k, int T) {
 // merge_kernel, from the sentinels the levels pass on.
 // The part lists are stream lists, sorted best first (the merge's sort
 // starts from the sorted runs).
-// A small batch of many lists takes the bounded merge instead
+// A batch of many lists (at most kBoundMergeQueries queries) takes the
+// bounded merge instead
 // (launch_bound_merge: a bound from the lists' best entries, the candidates
 // at or above it gathered in parallel, then one exact select per query),
 // where the levels would each wait on a few workgroups.

@@ -243,7 +243,7 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 // lists, in three short launches where the merge levels of a small batch
 // each wait on a few workgroups.  At most kBoundMergeQueries queries; calls
 // on a device are ordered (the slots and counts live in device memory).
-constexpr int kBoundMergeQueries = 128;
+constexpr int kBoundMergeQueries = 1024;
 struct BoundMergeArgs {
   const uint64_t* part;  // [nq][nseg][T], each list sorted best first
   int nseg;
