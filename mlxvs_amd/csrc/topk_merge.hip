@@ -1087,15 +1087,14 @@ __global__ __launch_bounds__(256) void scan_bits_kernel(ScanBitsArgs a) {
   }
 }
 
-// The smallest of query q's k bound slots (0 while one is empty), returned
-// to every thread.  All threads call it.
-__device__ uint64_t bits_slot_bound(int q, int k) {
+// The smallest of k bound slots in device memory (0 while one is empty),
+// returned to every thread.  All threads call it.
+__device__ uint64_t slot_min(const unsigned long long* sl, int k) {
   __shared__ unsigned long long s_b;
   if (threadIdx.x < 64) {
     uint64_t mn = ~0ull;
     for (int i = threadIdx.x; i < k; i += 64) {
-      const uint64_t v = __hip_atomic_load(&g_bits_slot[q][i], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t v = __hip_atomic_load(sl + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       mn = v < mn ? v : mn;
     }
 #pragma unroll
@@ -1107,124 +1106,6 @@ __device__ uint64_t bits_slot_bound(int q, int k) {
   }
   __syncthreads();
   return s_b;
-}
-
-// The ranks of the Hamming scan's split lists that reach the slots' bound,
-// appended to the query's survivors surv[q][0, g_bits_cnt[q]) in no
-// particular order (one counter update a wavefront).  Workgroup (q, g)
-// reads ranks [4,096 g, 4,096 g + 4,096) of part[q][0, m).
-__global__ __launch_bounds__(256) void filter_ranks_kernel(const uint64_t* part, int64_t m, int k,
-                                                           uint64_t* surv) {
-  constexpr int NT = 256, PER = 16;
-  const int q = blockIdx.x, tid = threadIdx.x;
-  const uint64_t B = bits_slot_bound(q, k);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(part + (int64_t)q * m), (short)0, (int)(m * 8), 0x00020000);
-  const int64_t c0 = (int64_t)blockIdx.y * NT * PER;
-  // all of the thread's loads in flight at once (reads past m are zero)
-  uint64_t r[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = __builtin_bit_cast(
-        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(c0 + e * NT + tid) * 8u, 0, 0));
-    r[e] = ((uint64_t)v[1] << 32) | v[0];
-  }
-  uint64_t b[PER];
-  int tot = 0;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    b[e] = __builtin_amdgcn_ballot_w64(r[e] != 0 && r[e] >= B);
-    tot += __builtin_popcountll(b[e]);
-  }
-  if (tot == 0) return;
-  int base = 0;
-  if ((tid & 63) == 0) base = (int)atomicAdd(&g_bits_cnt[q], (uint32_t)tot);
-  base = __shfl(base, 0);
-  uint64_t* dst = surv + (int64_t)q * m;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const uint32_t lo = (uint32_t)b[e], hi = (uint32_t)(b[e] >> 32);
-    if ((b[e] >> (tid & 63)) & 1ull)
-      dst[base + (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = r[e];
-    base += __builtin_popcountll(b[e]);
-  }
-}
-
-__device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_t B,
-                                 RowSelect& sm);
-
-// The best k of query q's survivors (filter_ranks_kernel) as Hamming
-// results (ids; distances = -score; -1 / +inf past the ranks there are),
-// then the query's slots and count reset for the next search.
-__global__ __launch_bounds__(256) void merge_survivors_kernel(const uint64_t* surv, int64_t m,
-                                                              int k, int32_t* ids, float* dists) {
-  constexpr int NT = 256;
-  __shared__ RowSelect sm;
-  const int q = blockIdx.x, tid = threadIdx.x;
-  // (the count's load in flight with the slots')
-  const int64_t c = __hip_atomic_load(&g_bits_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t B = bits_slot_bound(q, k);
-  const int kq = merge_split_lists(surv + (int64_t)q * m, c <= m ? c : m, k, B, sm);
-  // every thread read the slots and the count before the barriers above
-  if (tid < k) g_bits_slot[q][tid] = 0ull;
-  if (tid == 0) g_bits_cnt[q] = 0u;
-  for (int i = tid; i < k; i += NT) {
-    const uint64_t r = i < kq ? sm.buf[i] : 0ull;
-    const int64_t o = (int64_t)q * k + i;
-    ids[o] = r ? id_of_rank(r) : -1;
-    if (dists) dists[o] = r ? -score_of_key((uint32_t)(r >> 32)) : INFINITY;
-  }
-}
-
-// ---- bounded merge of a small batch's segment lists --------------------------------
-
-// Bound slots, survivor counts and segment-tail counts per query:
-// bound_slots_kernel fills the slots, bound_filter_kernel reads them and
-// adds to the counts, bound_merge_kernel reads and resets all three (zero
-// when the module loads; calls on a device are ordered, so one merge uses
-// them at a time).
-__device__ unsigned long long g_bm_slot[kBoundMergeQueries][kMaxK];
-__device__ uint32_t g_bm_cnt[kBoundMergeQueries];
-__device__ uint32_t g_bm_tails[kBoundMergeQueries];
-
-// The smallest of query q's k bound slots (0 while one is empty), returned
-// to every thread.  All threads call it.
-__device__ uint64_t bm_bound(int q, int k) {
-  __shared__ unsigned long long s_b;
-  if (threadIdx.x < 64) {
-    uint64_t mn = ~0ull;
-    for (int i = threadIdx.x; i < k; i += 64) {
-      const uint64_t v = __hip_atomic_load(&g_bm_slot[q][i], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      mn = v < mn ? v : mn;
-    }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t x = __shfl_xor(mn, o);
-      mn = x < mn ? x : mn;
-    }
-    if (threadIdx.x == 0) s_b = mn;
-  }
-  __syncthreads();
-  return s_b;
-}
-
-// Workgroup (q, g): the first (best) entries of segments [256 g, 256 g +
-// 256) of query q into their classes' slots, reduced in LDS first (one
-// device atomic per class and workgroup).
-__global__ __launch_bounds__(256) void bound_slots_kernel(BoundMergeArgs a) {
-  __shared__ unsigned long long ls[kMaxK];
-  const int q = blockIdx.x, tid = threadIdx.x;
-  if (tid < a.k) ls[tid] = 0ull;
-  __syncthreads();
-  const int sgm = blockIdx.y * 256 + tid;
-  if (sgm < a.nseg) {
-    const uint64_t r = a.part[((int64_t)q * a.nseg + sgm) * a.T];
-    if (r) atomicMax(&ls[sgm % a.k], (unsigned long long)r);
-  }
-  __syncthreads();
-  if (tid < a.k && ls[tid]) atomicMax(&g_bm_slot[q][tid], ls[tid]);
 }
 
 // Appends, one counter update a wavefront, the entries of b (a ballot per
@@ -1249,13 +1130,94 @@ __device__ __forceinline__ void append_ballots(const uint64_t (&r)[PER], const u
   }
 }
 
+// The ranks of the Hamming scan's split lists that reach the slots' bound,
+// appended to the query's survivors surv[q][0, g_bits_cnt[q]) in no
+// particular order (one counter update a wavefront).  Workgroup (q, g)
+// reads ranks [4,096 g, 4,096 g + 4,096) of part[q][0, m).
+__global__ __launch_bounds__(256) void filter_ranks_kernel(const uint64_t* part, int64_t m, int k,
+                                                           uint64_t* surv) {
+  constexpr int NT = 256, PER = 16;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  const uint64_t B = slot_min(g_bits_slot[q], k);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(part + (int64_t)q * m), (short)0, (int)(m * 8), 0x00020000);
+  const int64_t c0 = (int64_t)blockIdx.y * NT * PER;
+  // all of the thread's loads in flight at once (reads past m are zero)
+  uint64_t r[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(c0 + e * NT + tid) * 8u, 0, 0));
+    r[e] = ((uint64_t)v[1] << 32) | v[0];
+  }
+  uint64_t b[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) b[e] = __builtin_amdgcn_ballot_w64(r[e] != 0 && r[e] >= B);
+  append_ballots<PER>(r, b, &g_bits_cnt[q], surv + (int64_t)q * m);
+}
+
+__device__ int merge_split_lists(const uint64_t* part, int64_t m, int k, uint64_t B,
+                                 RowSelect& sm);
+
+// The best k of query q's survivors (filter_ranks_kernel) as Hamming
+// results (ids; distances = -score; -1 / +inf past the ranks there are),
+// then the query's slots and count reset for the next search.
+__global__ __launch_bounds__(256) void merge_survivors_kernel(const uint64_t* surv, int64_t m,
+                                                              int k, int32_t* ids, float* dists) {
+  constexpr int NT = 256;
+  __shared__ RowSelect sm;
+  const int q = blockIdx.x, tid = threadIdx.x;
+  // (the count's load in flight with the slots')
+  const int64_t c = __hip_atomic_load(&g_bits_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t B = slot_min(g_bits_slot[q], k);
+  const int kq = merge_split_lists(surv + (int64_t)q * m, c <= m ? c : m, k, B, sm);
+  // every thread read the slots and the count before the barriers above
+  if (tid < k) g_bits_slot[q][tid] = 0ull;
+  if (tid == 0) g_bits_cnt[q] = 0u;
+  for (int i = tid; i < k; i += NT) {
+    const uint64_t r = i < kq ? sm.buf[i] : 0ull;
+    const int64_t o = (int64_t)q * k + i;
+    ids[o] = r ? id_of_rank(r) : -1;
+    if (dists) dists[o] = r ? -score_of_key((uint32_t)(r >> 32)) : INFINITY;
+  }
+}
+
+// ---- bounded merge of a batch's segment lists ----------------------------------------
+
+// Bound slots, survivor counts and segment-tail counts per query:
+// bound_slots_kernel fills the slots, bound_filter_kernel reads them and
+// adds to the counts, bound_merge_kernel reads and resets all three (zero
+// when the module loads; calls on a device are ordered, so one merge uses
+// them at a time).
+__device__ unsigned long long g_bm_slot[kBoundMergeQueries][kMaxK];
+__device__ uint32_t g_bm_cnt[kBoundMergeQueries];
+__device__ uint32_t g_bm_tails[kBoundMergeQueries];
+
+// Workgroup (q, g): the first (best) entries of segments [256 g, 256 g +
+// 256) of query q into their classes' slots, reduced in LDS first (one
+// device atomic per class and workgroup).
+__global__ __launch_bounds__(256) void bound_slots_kernel(BoundMergeArgs a) {
+  __shared__ unsigned long long ls[kMaxK];
+  const int q = blockIdx.x, tid = threadIdx.x;
+  if (tid < a.k) ls[tid] = 0ull;
+  __syncthreads();
+  const int sgm = blockIdx.y * 256 + tid;
+  if (sgm < a.nseg) {
+    const uint64_t r = a.part[((int64_t)q * a.nseg + sgm) * a.T];
+    if (r) atomicMax(&ls[sgm % a.k], (unsigned long long)r);
+  }
+  __syncthreads();
+  if (tid < a.k && ls[tid]) atomicMax(&g_bm_slot[q][tid], ls[tid]);
+}
+
 // Workgroup (q, g): candidates [4,096 g, 4,096 g + 4,096) of query q's
 // nseg * T.
 __global__ __launch_bounds__(256) void bound_filter_kernel(BoundMergeArgs a) {
   constexpr int NT = 256, PER = 16;
   const int q = blockIdx.x, tid = threadIdx.x;
   const int64_t C = (int64_t)a.nseg * a.T;
-  const uint64_t B = bm_bound(q, a.k);
+  const uint64_t B = slot_min(g_bm_slot[q], a.k);
   const uint64_t* src = a.part + (int64_t)q * C;
   const int64_t c0 = (int64_t)blockIdx.y * NT * PER;
   uint64_t r[PER], b[PER], t[PER];
@@ -1285,7 +1247,7 @@ __global__ __launch_bounds__(256) void bound_merge_kernel(BoundMergeArgs a) {
   const int64_t c = __hip_atomic_load(&g_bm_cnt[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nt = (int)__hip_atomic_load(&g_bm_tails[q], __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t B = bm_bound(q, a.k);
+  const uint64_t B = slot_min(g_bm_slot[q], a.k);
   const int keff = merge_split_lists(a.surv + (int64_t)q * C, c <= C ? c : C, a.k, B, sm);
   for (int i = keff + tid; i < a.k; i += NT) sm.buf[i] = 0;
   if (tid == 0) s_flag = 0;
