@@ -31,6 +31,10 @@ def test_no_alloc_matches_the_allocating_entry(engine, f16):
     from mlxvs_amd import _hip, synth
 
     lib = engine._L()
+    # (at 300 and 500 queries, over 1,024 candidates a query, the allocating
+    # entry merges by the bounded batch merge and the no-allocation entry by
+    # the merge levels, so the comparison covers both; at k = 64 the redo
+    # flags as well)
     cases = [(200_000, 2_000, 128, 10, engine.Metric.l2),
              (30_000, 300, 64, 8, engine.Metric.inner_product),
              (50_000, 500, 128, 64, engine.Metric.l2)]
